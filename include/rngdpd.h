@@ -1,0 +1,228 @@
+/*
+ * rngdpd.h -- C ABI of the MI355X (gfx950) prefill->decode KV handoff and
+ * decode-attention library (librngdpd.so).
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, and
+ * returns an int status: PDK_OK (0) on success, a negative errno-style code
+ * otherwise, with a message readable through pdk_last_error() on the calling
+ * thread. Streams and events travel as uintptr_t (a hipStream_t / hipEvent_t
+ * value; 0 is the null stream). Compute entry points enqueue work on the given
+ * stream and return without synchronising the host; they allocate nothing.
+ * Allocation, stream, event and IPC entry points are explicit set-up calls.
+ *
+ * Tensor conventions (all element types are bf16 carried as uint16 bits):
+ *   prefill KV, per request   K/V [L][T][Hkv][D] with free layer and token
+ *                             strides (elements); [Hkv][D] contiguous per token
+ *   transport frame           [L][2][F], F = Hkv*D*S: the K frame [Hkv][D][S]
+ *                             then the V frame [Hkv][S][D], columns >= P zero.
+ *                             This is byte for byte the bf16 payload of the
+ *                             reference's shm wire for one layer's (k, v).
+ *   paged decode cache        K [L][num_blocks][Hkv][16][D]   (token rows)
+ *                             V [L][num_blocks][Hkv][D][16]   (dim rows)
+ *                             block table int32 [n_table], block j holds
+ *                             tokens 16j .. 16j+15 of the request
+ *
+ * Reference citations are file:line in ai-computing/rngd-pd.
+ */
+#ifndef RNGDPD_H
+#define RNGDPD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PDK_OK 0
+#define PDK_EHIP (-5)      /* EIO: the HIP runtime reported an error         */
+#define PDK_EAGAIN (-11)   /* event or stream not complete yet               */
+#define PDK_ENOMEM (-12)   /* allocation failed                              */
+#define PDK_EINVAL (-22)   /* bad argument: shape, alignment, null pointer   */
+#define PDK_ENOTSUP (-95)  /* shape the kernels do not implement             */
+
+#define PDK_BLOCK_SIZE 16     /* tokens per paged cache block                  */
+#define PDK_MAX_BATCH 16      /* requests per batched pack/scatter launch      */
+#define PDK_IPC_HANDLE_BYTES 64
+
+/* ---- library state ------------------------------------------------------ */
+
+/* ABI version (major*100 + minor). */
+int pdk_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* pdk_last_error(void);
+
+/* Number of visible devices / select the calling thread's device. */
+int pdk_device_count(int* out);
+int pdk_set_device(int device);
+
+/* ---- pack: prefill KV -> transport frame --------------------------------
+ * Replaces the per-layer-group frame step of FullPrefillEngine.prefill_stream
+ * (engines/prefill_full.py:366-384: zero-pad columns >= P to S at :378-379,
+ * download at :381-382) and the bf16 encode of ser()
+ * (connector/transport.py:29-37: f32 bits >> 16). The frame written here is
+ * the u16 payload ser() would pickle for the same bf16 K and V.
+ */
+typedef struct pdk_pack_req {
+  const uint16_t* src_k;   /* K of layer 0, token 0                         */
+  const uint16_t* src_v;   /* V of layer 0, token 0                         */
+  uint16_t* frame;         /* [L][2][Hkv*D*S]                               */
+  int64_t layer_stride;    /* elements between layers (both K and V)        */
+  int64_t tok_stride;      /* elements between tokens; a multiple of 8      */
+  int32_t P;               /* valid tokens, 0 <= P <= S                     */
+  int32_t reserved;
+} pdk_pack_req;
+
+/* One request: all L layers in one launch. Requires D % 64 == 0, S % 8 == 0,
+ * 16-byte aligned pointers. */
+int pdk_pack_kv(const uint16_t* src_k, const uint16_t* src_v,
+                int64_t layer_stride, int64_t tok_stride, int n_layers, int P,
+                int S, int n_kv_heads, int head_dim, uint16_t* frame,
+                uintptr_t stream);
+
+/* Up to PDK_MAX_BATCH requests of the same (L, S, Hkv, D) in one launch. */
+int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_layers,
+                      int S, int n_kv_heads, int head_dim, uintptr_t stream);
+
+/* ---- scatter: transport frame -> paged decode cache ----------------------
+ * Replaces the decode-side placement of a delivered layer
+ * (connector/rngd_kv.py:160-165), the f32->bf16 stage, lane stack and upload
+ * (engines/decode_batch.py:305-351) and the in-place lane write
+ * (engines/decode_batch.py:357-377). Writes blocks 0 .. ceil(P/16)-1 of the
+ * request; token slots >= P inside the last block are written as zero, as
+ * the reference's one-hot injection needs a zero slot
+ * (connector/rngd_kv.py:155-159). Block ids outside [0, num_blocks) are
+ * skipped by the kernel; callers validate tables before the call.
+ */
+typedef struct pdk_scatter_req {
+  const uint16_t* frame;   /* [L][2][Hkv*D*S]                               */
+  const int32_t* table;    /* device int32 [n_table]                        */
+  int32_t P;               /* tokens to place                               */
+  int32_t n_table;         /* >= ceil(P/16)                                 */
+} pdk_scatter_req;
+
+int pdk_scatter_paged(const uint16_t* frame, const int32_t* block_table,
+                      int n_table, int n_layers, int P, int S, int n_kv_heads,
+                      int head_dim, uint16_t* cache_k, uint16_t* cache_v,
+                      int64_t cache_layer_stride, int num_blocks,
+                      uintptr_t stream);
+
+int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs,
+                            int n_layers, int S, int n_kv_heads, int head_dim,
+                            uint16_t* cache_k, uint16_t* cache_v,
+                            int64_t cache_layer_stride, int num_blocks,
+                            uintptr_t stream);
+
+/* ---- gather: paged decode cache -> transport frame -----------------------
+ * Inverse of the scatter (the frame is written S-wide, zero for t >= P).
+ * Replaces the resident-cache export BatchDecodeEngine.download_kv
+ * (engines/decode_batch.py:379-390) and ResidentSession.export_kv
+ * (engines/decode_resident.py:222-225).
+ */
+int pdk_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v,
+                     int64_t cache_layer_stride, int num_blocks,
+                     const int32_t* block_table, int n_table, int n_layers,
+                     int P, int S, int n_kv_heads, int head_dim,
+                     uint16_t* frame, uintptr_t stream);
+
+/* ---- decode attention -----------------------------------------------------
+ * GQA decode attention for one layer over the paged cache. Replaces the
+ * attention slice of DecodeLayer.forward (kernels/decode_batch.py:83-85)
+ * and softmax_dsl (kernels/dsl_batch.py:73-86); the fp32 reference it must
+ * match is cpu_layer (kernels/decode_batch.py:151-156).
+ *   q      [B][Hq][D] bf16; query head qh reads KV head qh / (Hq/Hkv)
+ *   ctx    device int32 [B]: stream b attends to tokens 0 .. ctx[b]-1
+ *          (the reference's slots 0..pos inclusive, pos = ctx-1)
+ *   tables device int32 [B][max_blocks]
+ *   scale  multiplies q.k (1.0 when the scale is folded into q, as the
+ *          reference folds 1/sqrt(D) into wq, kernels/decode_batch.py:204)
+ *   max_ctx  host upper bound of ctx[] used for the launch grid
+ *   workspace  fp32 scratch of pdk_decode_attn_workspace_bytes() bytes
+ *   out    [B][Hq][D] bf16
+ * Requires D == 128 and Hq/Hkv in {1, 2, 4, 8, 16}.
+ */
+size_t pdk_decode_attn_workspace_bytes(int B, int n_q_heads, int max_ctx,
+                                       int head_dim);
+
+int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k,
+                    const uint16_t* cache_v, int num_blocks,
+                    const int32_t* block_tables, int max_blocks,
+                    const int32_t* ctx_lens, int max_ctx, int B,
+                    int n_q_heads, int n_kv_heads, int head_dim, float scale,
+                    void* workspace, size_t workspace_bytes, uint16_t* out,
+                    uintptr_t stream);
+
+/* Write one new token's k and v per stream at slot ctx[b]-1 of the paged
+ * cache: the one-hot cache injection Kf = Kp + k*oh, Vf = Vp + v*oh
+ * (kernels/decode_batch.py:81-82), done as a store.
+ *   k_new, v_new [B][Hkv][D] bf16. */
+int pdk_cache_append(const uint16_t* k_new, const uint16_t* v_new,
+                     uint16_t* cache_k, uint16_t* cache_v, int num_blocks,
+                     const int32_t* block_tables, int max_blocks,
+                     const int32_t* ctx_lens, int B, int n_kv_heads,
+                     int head_dim, uintptr_t stream);
+
+/* ---- greedy sampling -------------------------------------------------------
+ * First-maximum argmax per row of bf16 logits [B][ld] over V columns
+ * (greedy_tokens, engines/decode_batch.py:162-171: torch.argmax semantics,
+ * NaN counts as the maximum). out: device int32 [B]. */
+int pdk_greedy_argmax(const uint16_t* logits, int B, int V, int64_t ld,
+                      int32_t* out, uintptr_t stream);
+
+/* ---- staging and device memory ----------------------------------------------
+ * Pinned host staging replaces the synchronous .cpu() download
+ * (engines/prefill_full.py:381-382) and .to(dev) upload
+ * (engines/decode_batch.py:343-351). Pinned memory is allocated here
+ * (hipHostMalloc); existing memory is never registered. */
+int pdk_host_alloc(size_t bytes, void** out);
+int pdk_host_free(void* p);
+int pdk_dev_alloc(size_t bytes, void** out);
+int pdk_dev_free(void* p);
+int pdk_memcpy_d2h(void* host_dst, const void* dev_src, size_t bytes,
+                   uintptr_t stream);
+int pdk_memcpy_h2d(void* dev_dst, const void* host_src, size_t bytes,
+                   uintptr_t stream);
+int pdk_memcpy_d2d(void* dev_dst, const void* dev_src, size_t bytes,
+                   uintptr_t stream);
+/* A plain streaming copy kernel (16-byte vectors; bytes % 16 == 0), used to
+ * calibrate HBM traffic counters against a known byte count. */
+int pdk_copy_kernel(void* dev_dst, const void* dev_src, size_t bytes,
+                    uintptr_t stream);
+
+/* ---- streams and events ------------------------------------------------------
+ * Fences for the side-stream staging and for wait_for_save()
+ * (connector/rngd_kv.py:129-131), which becomes a real barrier once saves
+ * are asynchronous. Streams are created at the default priority. */
+int pdk_stream_create(uintptr_t* out);
+int pdk_stream_destroy(uintptr_t stream);
+int pdk_stream_sync(uintptr_t stream);
+#define PDK_EVENT_TIMING 0
+#define PDK_EVENT_INTERPROCESS 1   /* hipEventInterprocess | DisableTiming */
+int pdk_event_create(uintptr_t* out, int flags);
+int pdk_event_destroy(uintptr_t event);
+int pdk_event_record(uintptr_t event, uintptr_t stream);
+int pdk_event_query(uintptr_t event);   /* PDK_OK done, PDK_EAGAIN pending */
+int pdk_event_sync(uintptr_t event);
+int pdk_stream_wait_event(uintptr_t stream, uintptr_t event);
+int pdk_event_elapsed_ms(uintptr_t start, uintptr_t stop, float* ms);
+
+/* ---- same-GPU inter-process handoff --------------------------------------------
+ * The /dev/shm file handoff between the prefill and decode processes
+ * (connector/transport.py:80-101) becomes, on one GPU, an IPC handle to the
+ * producer's device frame pool plus an IPC event as the publish fence (the
+ * reference's tmp+fsync+rename, :90-94). Handles are PDK_IPC_HANDLE_BYTES
+ * opaque bytes. The producer owns the memory until the consumer acknowledges;
+ * the consumer closes what it opened. Exported allocations must come from
+ * pdk_dev_alloc and stay below 2 GiB each. */
+int pdk_ipc_export_mem(const void* dev_ptr, void* handle_out);
+int pdk_ipc_open_mem(const void* handle, void** dev_ptr_out);
+int pdk_ipc_close_mem(void* dev_ptr);
+int pdk_ipc_export_event(uintptr_t event, void* handle_out);
+int pdk_ipc_open_event(const void* handle, uintptr_t* event_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RNGDPD_H */

@@ -1,0 +1,338 @@
+// Prefill->decode KV handoff kernels for gfx950: pack (prefill KV -> transport
+// frame), scatter (frame -> paged decode cache) and gather (its inverse).
+//
+// All three are pure permutations of bf16 bits, bound by HBM bandwidth. Each
+// wavefront owns a 64-token x 64-dim tile of one (request, layer, head); a lane
+// owns an 8x8 sub-tile, moves it with 16-byte loads and stores, and transposes
+// it in registers where the two layouts disagree (K in pack; K and V in
+// scatter/gather), so no LDS round trip is needed. Lane (ti, di) = (lane>>3,
+// lane&7) holds tokens 8ti..8ti+7 and dims 8di..8di+7 of the tile: for every
+// load and store instruction the 64 lanes touch eight full 128-byte lines.
+//
+// Requests are batched through the kernel argument block (grid.y = request),
+// so a launch moves up to PDK_MAX_BATCH requests without any device-side
+// descriptor buffer or allocation.
+
+#include "pdk_common.h"
+
+namespace {
+
+using pdk::v8;
+
+constexpr int kWaves = 4;        // wavefronts per workgroup
+constexpr int kTileT = 64;       // tokens per wavefront tile
+constexpr int kTileD = 64;       // dims per wavefront tile
+
+struct PackArgs {
+  pdk_pack_req req[PDK_MAX_BATCH];
+  int S, Hkv, D, nT, nD;
+  int64_t units;                 // wavefront tiles per request
+};
+
+// Frame layout per request: [L][2][F], F = Hkv*D*S; K frame [Hkv][D][S],
+// V frame [Hkv][S][D]; columns t >= P are zero (engines/prefill_full.py:378-379).
+__global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
+  const int64_t unit = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (unit >= a.units) return;
+  const pdk_pack_req& R = a.req[blockIdx.y];
+  const int lane = threadIdx.x & 63;
+  int64_t u = unit;
+  const int dt = (int)(u % a.nD); u /= a.nD;
+  const int tt = (int)(u % a.nT); u /= a.nT;
+  const int h = (int)(u % a.Hkv); u /= a.Hkv;
+  const int l = (int)u;
+  const int ti = lane >> 3, di = lane & 7;
+  const int S = a.S, D = a.D, P = R.P;
+  const int t0 = tt * kTileT + ti * 8;
+  const int d0 = dt * kTileD + di * 8;
+  const int64_t F = (int64_t)a.Hkv * D * S;
+
+  const uint16_t* sk = R.src_k + (int64_t)l * R.layer_stride + (int64_t)h * D + d0;
+  const uint16_t* sv = R.src_v + (int64_t)l * R.layer_stride + (int64_t)h * D + d0;
+  v8 kin[8], vin[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int t = t0 + r;
+    if (t < P) {
+      kin[r] = pdk::ld16(sk + (int64_t)t * R.tok_stride);
+      vin[r] = pdk::ld16(sv + (int64_t)t * R.tok_stride);
+    } else {
+      kin[r] = pdk::zero8();
+      vin[r] = pdk::zero8();
+    }
+  }
+  if (t0 >= S) return;           // S % 8 == 0: the lane's 8 tokens are all in or all out
+  uint16_t* fk = R.frame + (int64_t)(2 * l) * F;
+  uint16_t* fv = fk + F;
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    pdk::st16(fv + ((int64_t)h * S + t0 + r) * D + d0, vin[r]);
+  v8 kout[8];
+  pdk::transpose8x8(kin, kout);  // kout[c]: dim d0+c, tokens t0..t0+7
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    pdk::st16(fk + ((int64_t)h * D + d0 + c) * S + t0, kout[c]);
+}
+
+struct ScatterArgs {
+  pdk_scatter_req req[PDK_MAX_BATCH];
+  uint16_t* cache_k;
+  uint16_t* cache_v;
+  int64_t cache_ls;              // elements between layers of the cache
+  int num_blocks, S, Hkv, D, nC, nD;
+  int64_t units;
+};
+
+// Frame -> paged cache. K cache block [Hkv][16][D] (token rows), V cache block
+// [Hkv][D][16] (dim rows): both need an 8x8 transpose from the frame.
+__global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
+  const int64_t unit = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (unit >= a.units) return;
+  const pdk_scatter_req& R = a.req[blockIdx.y];
+  const int lane = threadIdx.x & 63;
+  int64_t u = unit;
+  const int dt = (int)(u % a.nD); u /= a.nD;
+  const int ct = (int)(u % a.nC); u /= a.nC;
+  const int h = (int)(u % a.Hkv); u /= a.Hkv;
+  const int l = (int)u;
+  const int ti = lane >> 3, di = lane & 7;
+  const int S = a.S, D = a.D, P = R.P;
+  const int t0 = ct * kTileT + ti * 8;
+  if (t0 >= ((P + 15) & ~15)) return;          // beyond the request's last block
+  const int j = t0 >> 4;
+  if (j >= R.n_table) return;
+  const int blk = R.table[j];
+  if (blk < 0 || blk >= a.num_blocks) return;
+  const int slot0 = t0 & 15;
+  const int d0 = dt * kTileD + di * 8;
+  const int64_t F = (int64_t)a.Hkv * D * S;
+  const uint16_t* fk = R.frame + (int64_t)(2 * l) * F;
+  const uint16_t* fv = fk + F;
+
+  v8 kin[8], vin[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    // K frame row d0+r holds tokens contiguously; V frame row t0+r holds dims.
+    kin[r] = (t0 < P) ? pdk::ld16(fk + ((int64_t)h * D + d0 + r) * S + t0) : pdk::zero8();
+    if (t0 + 8 > P) pdk::mask_tail(kin[r], t0, P);
+    vin[r] = (t0 + r < P) ? pdk::ld16(fv + ((int64_t)h * S + t0 + r) * D + d0) : pdk::zero8();
+  }
+  v8 kout[8], vout[8];
+  pdk::transpose8x8(kin, kout);  // kout[c]: token t0+c, dims d0..d0+7
+  pdk::transpose8x8(vin, vout);  // vout[c]: dim d0+c, tokens t0..t0+7
+  uint16_t* ck = a.cache_k + (int64_t)l * a.cache_ls + ((int64_t)blk * a.Hkv + h) * 16 * D;
+  uint16_t* cv = a.cache_v + (int64_t)l * a.cache_ls + ((int64_t)blk * a.Hkv + h) * D * 16;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    pdk::st16(ck + (int64_t)(slot0 + c) * D + d0, kout[c]);
+    pdk::st16(cv + (int64_t)(d0 + c) * 16 + slot0, vout[c]);
+  }
+}
+
+struct GatherArgs {
+  const uint16_t* cache_k;
+  const uint16_t* cache_v;
+  const int32_t* table;
+  uint16_t* frame;
+  int64_t cache_ls;
+  int num_blocks, n_table, P, S, Hkv, D, nC, nD;
+  int64_t units;
+};
+
+// Paged cache -> S-wide frame (zero for t >= P).
+__global__ __launch_bounds__(256) void gather_kernel(const GatherArgs a) {
+  const int64_t unit = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (unit >= a.units) return;
+  const int lane = threadIdx.x & 63;
+  int64_t u = unit;
+  const int dt = (int)(u % a.nD); u /= a.nD;
+  const int ct = (int)(u % a.nC); u /= a.nC;
+  const int h = (int)(u % a.Hkv); u /= a.Hkv;
+  const int l = (int)u;
+  const int ti = lane >> 3, di = lane & 7;
+  const int S = a.S, D = a.D, P = a.P;
+  const int t0 = ct * kTileT + ti * 8;
+  if (t0 >= S) return;
+  const int d0 = dt * kTileD + di * 8;
+  const int64_t F = (int64_t)a.Hkv * D * S;
+  uint16_t* fk = a.frame + (int64_t)(2 * l) * F;
+  uint16_t* fv = fk + F;
+
+  int blk = -1;
+  if (t0 < P && (t0 >> 4) < a.n_table) blk = a.table[t0 >> 4];
+  const bool ok = blk >= 0 && blk < a.num_blocks;
+  const int slot0 = t0 & 15;
+  const uint16_t* ck = a.cache_k + (int64_t)l * a.cache_ls + ((int64_t)(ok ? blk : 0) * a.Hkv + h) * 16 * D;
+  const uint16_t* cv = a.cache_v + (int64_t)l * a.cache_ls + ((int64_t)(ok ? blk : 0) * a.Hkv + h) * D * 16;
+  v8 kin[8], vin[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    kin[r] = (ok && t0 + r < P) ? pdk::ld16(ck + (int64_t)(slot0 + r) * D + d0) : pdk::zero8();
+    vin[r] = ok ? pdk::ld16(cv + (int64_t)(d0 + r) * 16 + slot0) : pdk::zero8();
+    if (t0 + 8 > P) pdk::mask_tail(vin[r], t0, P);
+  }
+  v8 kout[8], vout[8];
+  pdk::transpose8x8(kin, kout);  // kout[c]: dim d0+c, tokens t0..t0+7
+  pdk::transpose8x8(vin, vout);  // vout[c]: token t0+c, dims d0..d0+7
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    pdk::st16(fk + ((int64_t)h * D + d0 + c) * S + t0, kout[c]);
+    pdk::st16(fv + ((int64_t)h * S + t0 + c) * D + d0, vout[c]);
+  }
+}
+
+int check_common(int n_layers, int S, int Hkv, int D) {
+  PDK_REQUIRE(n_layers >= 1, "n_layers must be >= 1 (got %d)", n_layers);
+  PDK_REQUIRE(Hkv >= 1, "n_kv_heads must be >= 1 (got %d)", Hkv);
+  if (D < 64 || D % 64 != 0 || D > 1024) {
+    pdk::set_error("head_dim must be a multiple of 64 in [64, 1024] (got %d)", D);
+    return PDK_ENOTSUP;
+  }
+  PDK_REQUIRE(S >= 16 && S % 16 == 0, "S must be a positive multiple of 16 (got %d)", S);
+  return PDK_OK;
+}
+
+int64_t grid_x(int64_t units) { return (units + kWaves - 1) / kWaves; }
+
+}  // namespace
+
+extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_layers,
+                                 int S, int n_kv_heads, int head_dim, uintptr_t stream) {
+  pdk::clear_error();
+  int rc = check_common(n_layers, S, n_kv_heads, head_dim);
+  if (rc) return rc;
+  PDK_REQUIRE(reqs != nullptr, "reqs is null");
+  PDK_REQUIRE(n_reqs >= 1 && n_reqs <= PDK_MAX_BATCH, "n_reqs must be in [1, %d] (got %d)",
+              PDK_MAX_BATCH, n_reqs);
+  PackArgs a{};
+  for (int i = 0; i < n_reqs; ++i) {
+    const pdk_pack_req& r = reqs[i];
+    PDK_REQUIRE(r.frame && pdk::aligned16(r.frame), "request %d: frame null or not 16-byte aligned", i);
+    PDK_REQUIRE(r.P >= 0 && r.P <= S, "request %d: P=%d outside [0, S=%d]", i, r.P, S);
+    if (r.P > 0) {
+      PDK_REQUIRE(r.src_k && r.src_v && pdk::aligned16(r.src_k) && pdk::aligned16(r.src_v),
+                  "request %d: src_k/src_v null or not 16-byte aligned", i);
+      PDK_REQUIRE(r.tok_stride >= (int64_t)n_kv_heads * head_dim && r.tok_stride % 8 == 0,
+                  "request %d: tok_stride=%lld must be a multiple of 8 and >= Hkv*D", i,
+                  (long long)r.tok_stride);
+      PDK_REQUIRE(r.layer_stride % 8 == 0 && (n_layers == 1 || r.layer_stride != 0),
+                  "request %d: layer_stride=%lld must be a multiple of 8", i,
+                  (long long)r.layer_stride);
+    }
+    a.req[i] = r;
+  }
+  a.S = S;
+  a.Hkv = n_kv_heads;
+  a.D = head_dim;
+  a.nT = (S + kTileT - 1) / kTileT;
+  a.nD = head_dim / kTileD;
+  a.units = (int64_t)n_layers * n_kv_heads * a.nT * a.nD;
+  const int64_t gx = grid_x(a.units);
+  PDK_REQUIRE(gx < (1ll << 31), "launch too large");
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)gx, (unsigned)n_reqs), dim3(256), 0,
+                     pdk::as_stream(stream), a);
+  return pdk::check_launch("pack_kernel");
+}
+
+extern "C" int pdk_pack_kv(const uint16_t* src_k, const uint16_t* src_v, int64_t layer_stride,
+                           int64_t tok_stride, int n_layers, int P, int S, int n_kv_heads,
+                           int head_dim, uint16_t* frame, uintptr_t stream) {
+  pdk_pack_req r{src_k, src_v, frame, layer_stride, tok_stride, P, 0};
+  return pdk_pack_kv_batch(&r, 1, n_layers, S, n_kv_heads, head_dim, stream);
+}
+
+extern "C" int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs, int n_layers,
+                                       int S, int n_kv_heads, int head_dim, uint16_t* cache_k,
+                                       uint16_t* cache_v, int64_t cache_layer_stride,
+                                       int num_blocks, uintptr_t stream) {
+  pdk::clear_error();
+  int rc = check_common(n_layers, S, n_kv_heads, head_dim);
+  if (rc) return rc;
+  PDK_REQUIRE(reqs != nullptr, "reqs is null");
+  PDK_REQUIRE(n_reqs >= 1 && n_reqs <= PDK_MAX_BATCH, "n_reqs must be in [1, %d] (got %d)",
+              PDK_MAX_BATCH, n_reqs);
+  PDK_REQUIRE(cache_k && cache_v && pdk::aligned16(cache_k) && pdk::aligned16(cache_v),
+              "cache_k/cache_v null or not 16-byte aligned");
+  PDK_REQUIRE(num_blocks >= 1, "num_blocks must be >= 1");
+  const int64_t per_layer = (int64_t)num_blocks * n_kv_heads * 16 * head_dim;
+  PDK_REQUIRE(n_layers == 1 || cache_layer_stride >= per_layer,
+              "cache_layer_stride=%lld smaller than one layer (%lld)",
+              (long long)cache_layer_stride, (long long)per_layer);
+  PDK_REQUIRE(cache_layer_stride % 8 == 0, "cache_layer_stride must be a multiple of 8");
+  ScatterArgs a{};
+  int max_p = 0;
+  for (int i = 0; i < n_reqs; ++i) {
+    const pdk_scatter_req& r = reqs[i];
+    PDK_REQUIRE(r.P >= 0 && r.P <= S, "request %d: P=%d outside [0, S=%d]", i, r.P, S);
+    if (r.P > 0) {
+      PDK_REQUIRE(r.frame && pdk::aligned16(r.frame), "request %d: frame null or not 16-byte aligned", i);
+      PDK_REQUIRE(r.table != nullptr, "request %d: block table is null", i);
+      PDK_REQUIRE(r.n_table >= (r.P + 15) / 16, "request %d: table has %d blocks, P=%d needs %d",
+                  i, r.n_table, r.P, (r.P + 15) / 16);
+    }
+    a.req[i] = r;
+    if (r.P > max_p) max_p = r.P;
+  }
+  if (max_p == 0) return PDK_OK;
+  a.cache_k = cache_k;
+  a.cache_v = cache_v;
+  a.cache_ls = cache_layer_stride;
+  a.num_blocks = num_blocks;
+  a.S = S;
+  a.Hkv = n_kv_heads;
+  a.D = head_dim;
+  a.nC = (max_p + kTileT - 1) / kTileT;
+  a.nD = head_dim / kTileD;
+  a.units = (int64_t)n_layers * n_kv_heads * a.nC * a.nD;
+  const int64_t gx = grid_x(a.units);
+  PDK_REQUIRE(gx < (1ll << 31), "launch too large");
+  hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)gx, (unsigned)n_reqs), dim3(256), 0,
+                     pdk::as_stream(stream), a);
+  return pdk::check_launch("scatter_kernel");
+}
+
+extern "C" int pdk_scatter_paged(const uint16_t* frame, const int32_t* block_table, int n_table,
+                                 int n_layers, int P, int S, int n_kv_heads, int head_dim,
+                                 uint16_t* cache_k, uint16_t* cache_v,
+                                 int64_t cache_layer_stride, int num_blocks, uintptr_t stream) {
+  pdk_scatter_req r{frame, block_table, P, n_table};
+  return pdk_scatter_paged_batch(&r, 1, n_layers, S, n_kv_heads, head_dim, cache_k, cache_v,
+                                 cache_layer_stride, num_blocks, stream);
+}
+
+extern "C" int pdk_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v,
+                                int64_t cache_layer_stride, int num_blocks,
+                                const int32_t* block_table, int n_table, int n_layers, int P,
+                                int S, int n_kv_heads, int head_dim, uint16_t* frame,
+                                uintptr_t stream) {
+  pdk::clear_error();
+  int rc = check_common(n_layers, S, n_kv_heads, head_dim);
+  if (rc) return rc;
+  PDK_REQUIRE(frame && pdk::aligned16(frame), "frame null or not 16-byte aligned");
+  PDK_REQUIRE(P >= 0 && P <= S, "P=%d outside [0, S=%d]", P, S);
+  PDK_REQUIRE(cache_k && cache_v && pdk::aligned16(cache_k) && pdk::aligned16(cache_v),
+              "cache_k/cache_v null or not 16-byte aligned");
+  PDK_REQUIRE(num_blocks >= 1, "num_blocks must be >= 1");
+  PDK_REQUIRE(cache_layer_stride % 8 == 0, "cache_layer_stride must be a multiple of 8");
+  PDK_REQUIRE(P == 0 || (block_table && n_table >= (P + 15) / 16),
+              "block table null or shorter than ceil(P/16)");
+  GatherArgs a{};
+  a.cache_k = cache_k;
+  a.cache_v = cache_v;
+  a.table = block_table;
+  a.frame = frame;
+  a.cache_ls = cache_layer_stride;
+  a.num_blocks = num_blocks;
+  a.n_table = n_table;
+  a.P = P;
+  a.S = S;
+  a.Hkv = n_kv_heads;
+  a.D = head_dim;
+  a.nC = (S + kTileT - 1) / kTileT;
+  a.nD = head_dim / kTileD;
+  a.units = (int64_t)n_layers * n_kv_heads * a.nC * a.nD;
+  const int64_t gx = grid_x(a.units);
+  PDK_REQUIRE(gx < (1ll << 31), "launch too large");
+  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
+  return pdk::check_launch("gather_kernel");
+}

@@ -1,0 +1,92 @@
+// Internal helpers shared by the librngdpd HIP sources (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rngdpd.h"
+
+namespace pdk {
+
+// Thread-local error text behind pdk_last_error().
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+// Records a HIP failure and returns PDK_EHIP.
+int hip_fail(hipError_t e, const char* what);
+// Reports a launch error (hipGetLastError) after a kernel launch.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(uintptr_t s) { return reinterpret_cast<hipStream_t>(s); }
+inline hipEvent_t as_event(uintptr_t e) { return reinterpret_cast<hipEvent_t>(e); }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// 8 bf16 values in one 16-byte register group: word w holds elements 2w (low
+// half) and 2w+1 (high half).
+struct v8 {
+  uint32_t w[4];
+};
+
+__device__ __forceinline__ v8 ld16(const uint16_t* p) {
+  const uint4 x = *reinterpret_cast<const uint4*>(p);
+  return v8{{x.x, x.y, x.z, x.w}};
+}
+
+__device__ __forceinline__ void st16(uint16_t* p, const v8& v) {
+  *reinterpret_cast<uint4*>(p) = make_uint4(v.w[0], v.w[1], v.w[2], v.w[3]);
+}
+
+__device__ __forceinline__ v8 zero8() { return v8{{0u, 0u, 0u, 0u}}; }
+
+// Zero the elements e with first + e >= limit (first..first+7 are the token
+// indices of the 8 elements).
+__device__ __forceinline__ void mask_tail(v8& v, int first, int limit) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t lo = (first + 2 * w < limit) ? 0x0000ffffu : 0u;
+    const uint32_t hi = (first + 2 * w + 1 < limit) ? 0xffff0000u : 0u;
+    v.w[w] &= (lo | hi);
+  }
+}
+
+// 8x8 transpose of 16-bit elements held by one lane: in[r] is row r
+// (elements c = 0..7); out[c] becomes column c (elements r = 0..7).
+__device__ __forceinline__ void transpose8x8(const v8 in[8], v8 out[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int w = c >> 1;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t a = in[2 * p].w[w];
+      const uint32_t b = in[2 * p + 1].w[w];
+      out[c].w[p] = (c & 1) ? ((a >> 16) | (b & 0xffff0000u))
+                            : ((a & 0x0000ffffu) | (b << 16));
+    }
+  }
+}
+
+// fp32 -> bf16 bits, round to nearest even (inputs here are finite).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+}  // namespace pdk
+
+#define PDK_TRY_HIP(call)                              \
+  do {                                                 \
+    hipError_t _pdk_e = (call);                        \
+    if (_pdk_e != hipSuccess) return pdk::hip_fail(_pdk_e, #call); \
+  } while (0)
+
+#define PDK_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      pdk::set_error(__VA_ARGS__);    \
+      return PDK_EINVAL;              \
+    }                                 \
+  } while (0)

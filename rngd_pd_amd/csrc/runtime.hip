@@ -1,0 +1,313 @@
+// Library state, staging memory, streams, events, same-GPU IPC, the greedy
+// argmax kernel and a plain copy kernel (traffic-counter calibration).
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "pdk_common.h"
+
+namespace pdk {
+
+static thread_local char g_err[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+int hip_fail(hipError_t e, const char* what) {
+  set_error("%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+  return PDK_EHIP;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, what);
+  return PDK_OK;
+}
+
+}  // namespace pdk
+
+namespace {
+
+// First-maximum argmax of one bf16 row; NaN ranks above every number (the
+// torch.argmax convention greedy_tokens relies on).
+struct Best {
+  float v;
+  int i;
+  int nan;
+};
+
+__device__ __forceinline__ bool better(const Best& x, const Best& y) {
+  if (x.nan != y.nan) return x.nan > y.nan;
+  if (!x.nan && x.v != y.v) return x.v > y.v;
+  return x.i < y.i;
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* logits, int V, int64_t ld,
+                                                     int32_t* out) {
+  __shared__ Best red[256];
+  const uint16_t* row = logits + (int64_t)blockIdx.x * ld;
+  Best best{-INFINITY, 0x7fffffff, 0};
+  for (int i = threadIdx.x; i < V; i += blockDim.x) {
+    const float x = pdk::bf16_to_f32(row[i]);
+    const Best c{x, i, x != x ? 1 : 0};
+    if (better(c, best)) best = c;
+  }
+  red[threadIdx.x] = best;
+  __syncthreads();
+  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s && better(red[threadIdx.x + s], red[threadIdx.x]))
+      red[threadIdx.x] = red[threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[blockIdx.x] = red[0].i;
+}
+
+__global__ __launch_bounds__(256) void copy_kernel(uint4* dst, const uint4* src, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    dst[i] = src[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+int pdk_version(void) { return 100; }
+
+const char* pdk_last_error(void) { return pdk::g_err; }
+
+int pdk_device_count(int* out) {
+  pdk::clear_error();
+  PDK_REQUIRE(out != nullptr, "out is null");
+  PDK_TRY_HIP(hipGetDeviceCount(out));
+  return PDK_OK;
+}
+
+int pdk_set_device(int device) {
+  pdk::clear_error();
+  PDK_TRY_HIP(hipSetDevice(device));
+  return PDK_OK;
+}
+
+int pdk_greedy_argmax(const uint16_t* logits, int B, int V, int64_t ld, int32_t* out,
+                      uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(logits && out, "null pointer argument");
+  PDK_REQUIRE(B >= 1 && V >= 1 && ld >= V, "bad shape B=%d V=%d ld=%lld", B, V, (long long)ld);
+  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, pdk::as_stream(stream), logits, V, ld,
+                     out);
+  return pdk::check_launch("argmax_kernel");
+}
+
+int pdk_host_alloc(size_t bytes, void** out) {
+  pdk::clear_error();
+  PDK_REQUIRE(out != nullptr && bytes > 0, "bad arguments");
+  *out = nullptr;
+  const hipError_t e = hipHostMalloc(out, bytes, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    pdk::hip_fail(e, "hipHostMalloc");
+    return PDK_ENOMEM;
+  }
+  return PDK_OK;
+}
+
+int pdk_host_free(void* p) {
+  pdk::clear_error();
+  if (!p) return PDK_OK;
+  PDK_TRY_HIP(hipHostFree(p));
+  return PDK_OK;
+}
+
+int pdk_dev_alloc(size_t bytes, void** out) {
+  pdk::clear_error();
+  PDK_REQUIRE(out != nullptr && bytes > 0, "bad arguments");
+  *out = nullptr;
+  const hipError_t e = hipMalloc(out, bytes);
+  if (e != hipSuccess) {
+    pdk::hip_fail(e, "hipMalloc");
+    return PDK_ENOMEM;
+  }
+  return PDK_OK;
+}
+
+int pdk_dev_free(void* p) {
+  pdk::clear_error();
+  if (!p) return PDK_OK;
+  PDK_TRY_HIP(hipFree(p));
+  return PDK_OK;
+}
+
+int pdk_memcpy_d2h(void* host_dst, const void* dev_src, size_t bytes, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(host_dst && dev_src, "null pointer argument");
+  PDK_TRY_HIP(hipMemcpyAsync(host_dst, dev_src, bytes, hipMemcpyDeviceToHost,
+                             pdk::as_stream(stream)));
+  return PDK_OK;
+}
+
+int pdk_memcpy_h2d(void* dev_dst, const void* host_src, size_t bytes, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(dev_dst && host_src, "null pointer argument");
+  PDK_TRY_HIP(hipMemcpyAsync(dev_dst, host_src, bytes, hipMemcpyHostToDevice,
+                             pdk::as_stream(stream)));
+  return PDK_OK;
+}
+
+int pdk_memcpy_d2d(void* dev_dst, const void* dev_src, size_t bytes, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(dev_dst && dev_src, "null pointer argument");
+  PDK_TRY_HIP(hipMemcpyAsync(dev_dst, dev_src, bytes, hipMemcpyDeviceToDevice,
+                             pdk::as_stream(stream)));
+  return PDK_OK;
+}
+
+int pdk_copy_kernel(void* dev_dst, const void* dev_src, size_t bytes, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(dev_dst && dev_src, "null pointer argument");
+  PDK_REQUIRE(bytes % 16 == 0 && pdk::aligned16(dev_dst) && pdk::aligned16(dev_src),
+              "copy needs 16-byte aligned pointers and a multiple of 16 bytes");
+  const int64_t n = (int64_t)(bytes / 16);
+  if (n == 0) return PDK_OK;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, pdk::as_stream(stream),
+                     static_cast<uint4*>(dev_dst), static_cast<const uint4*>(dev_src), n);
+  return pdk::check_launch("copy_kernel");
+}
+
+int pdk_stream_create(uintptr_t* out) {
+  pdk::clear_error();
+  PDK_REQUIRE(out != nullptr, "out is null");
+  hipStream_t s = nullptr;
+  PDK_TRY_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *out = reinterpret_cast<uintptr_t>(s);
+  return PDK_OK;
+}
+
+int pdk_stream_destroy(uintptr_t stream) {
+  pdk::clear_error();
+  if (!stream) return PDK_OK;
+  PDK_TRY_HIP(hipStreamDestroy(pdk::as_stream(stream)));
+  return PDK_OK;
+}
+
+int pdk_stream_sync(uintptr_t stream) {
+  pdk::clear_error();
+  PDK_TRY_HIP(hipStreamSynchronize(pdk::as_stream(stream)));
+  return PDK_OK;
+}
+
+int pdk_event_create(uintptr_t* out, int flags) {
+  pdk::clear_error();
+  PDK_REQUIRE(out != nullptr, "out is null");
+  PDK_REQUIRE(flags == PDK_EVENT_TIMING || flags == PDK_EVENT_INTERPROCESS, "bad flags %d", flags);
+  hipEvent_t e = nullptr;
+  if (flags == PDK_EVENT_INTERPROCESS) {
+    PDK_TRY_HIP(hipEventCreateWithFlags(&e, hipEventInterprocess | hipEventDisableTiming));
+  } else {
+    PDK_TRY_HIP(hipEventCreate(&e));
+  }
+  *out = reinterpret_cast<uintptr_t>(e);
+  return PDK_OK;
+}
+
+int pdk_event_destroy(uintptr_t event) {
+  pdk::clear_error();
+  if (!event) return PDK_OK;
+  PDK_TRY_HIP(hipEventDestroy(pdk::as_event(event)));
+  return PDK_OK;
+}
+
+int pdk_event_record(uintptr_t event, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(event != 0, "event is null");
+  PDK_TRY_HIP(hipEventRecord(pdk::as_event(event), pdk::as_stream(stream)));
+  return PDK_OK;
+}
+
+int pdk_event_query(uintptr_t event) {
+  pdk::clear_error();
+  PDK_REQUIRE(event != 0, "event is null");
+  const hipError_t e = hipEventQuery(pdk::as_event(event));
+  if (e == hipSuccess) return PDK_OK;
+  if (e == hipErrorNotReady) return PDK_EAGAIN;
+  return pdk::hip_fail(e, "hipEventQuery");
+}
+
+int pdk_event_sync(uintptr_t event) {
+  pdk::clear_error();
+  PDK_REQUIRE(event != 0, "event is null");
+  PDK_TRY_HIP(hipEventSynchronize(pdk::as_event(event)));
+  return PDK_OK;
+}
+
+int pdk_stream_wait_event(uintptr_t stream, uintptr_t event) {
+  pdk::clear_error();
+  PDK_REQUIRE(event != 0, "event is null");
+  PDK_TRY_HIP(hipStreamWaitEvent(pdk::as_stream(stream), pdk::as_event(event), 0));
+  return PDK_OK;
+}
+
+int pdk_event_elapsed_ms(uintptr_t start, uintptr_t stop, float* ms) {
+  pdk::clear_error();
+  PDK_REQUIRE(start && stop && ms, "null argument");
+  PDK_TRY_HIP(hipEventElapsedTime(ms, pdk::as_event(start), pdk::as_event(stop)));
+  return PDK_OK;
+}
+
+int pdk_ipc_export_mem(const void* dev_ptr, void* handle_out) {
+  pdk::clear_error();
+  PDK_REQUIRE(dev_ptr && handle_out, "null argument");
+  static_assert(sizeof(hipIpcMemHandle_t) == PDK_IPC_HANDLE_BYTES, "IPC handle size");
+  hipIpcMemHandle_t h;
+  PDK_TRY_HIP(hipIpcGetMemHandle(&h, const_cast<void*>(dev_ptr)));
+  memcpy(handle_out, &h, sizeof(h));
+  return PDK_OK;
+}
+
+int pdk_ipc_open_mem(const void* handle, void** dev_ptr_out) {
+  pdk::clear_error();
+  PDK_REQUIRE(handle && dev_ptr_out, "null argument");
+  hipIpcMemHandle_t h;
+  memcpy(&h, handle, sizeof(h));
+  *dev_ptr_out = nullptr;
+  PDK_TRY_HIP(hipIpcOpenMemHandle(dev_ptr_out, h, hipIpcMemLazyEnablePeerAccess));
+  return PDK_OK;
+}
+
+int pdk_ipc_close_mem(void* dev_ptr) {
+  pdk::clear_error();
+  PDK_REQUIRE(dev_ptr != nullptr, "null argument");
+  PDK_TRY_HIP(hipIpcCloseMemHandle(dev_ptr));
+  return PDK_OK;
+}
+
+int pdk_ipc_export_event(uintptr_t event, void* handle_out) {
+  pdk::clear_error();
+  PDK_REQUIRE(event && handle_out, "null argument");
+  static_assert(sizeof(hipIpcEventHandle_t) == PDK_IPC_HANDLE_BYTES, "IPC event handle size");
+  hipIpcEventHandle_t h;
+  PDK_TRY_HIP(hipIpcGetEventHandle(&h, pdk::as_event(event)));
+  memcpy(handle_out, &h, sizeof(h));
+  return PDK_OK;
+}
+
+int pdk_ipc_open_event(const void* handle, uintptr_t* event_out) {
+  pdk::clear_error();
+  PDK_REQUIRE(handle && event_out, "null argument");
+  hipIpcEventHandle_t h;
+  memcpy(&h, handle, sizeof(h));
+  hipEvent_t e = nullptr;
+  PDK_TRY_HIP(hipIpcOpenEventHandle(&e, h));
+  *event_out = reinterpret_cast<uintptr_t>(e);
+  return PDK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,87 @@
+"""torch-facing wrappers of decode attention, cache append and greedy argmax.
+
+Replaces the attention slice of DecodeLayer.forward (kernels/decode_batch.py:81-85),
+softmax_dsl (kernels/dsl_batch.py:73-86) and greedy_tokens
+(engines/decode_batch.py:162-171) with HIP kernels over the paged cache.
+"""
+import torch
+
+from .. import _lib
+from .handoff import _need, stream_handle
+
+BF16 = torch.bfloat16
+
+
+def workspace_bytes(B, n_q_heads, max_ctx, head_dim=128):
+    return int(_lib.lib().pdk_decode_attn_workspace_bytes(B, n_q_heads, max_ctx, head_dim))
+
+
+def _check_layer_cache(cache_k, cache_v):
+    _need(cache_k, "cache_k")
+    _need(cache_v, "cache_v")
+    if cache_k.dim() != 4 or cache_k.shape[2] != 16:
+        raise ValueError(f"cache_k must be one layer [nb, Hkv, 16, D], got {tuple(cache_k.shape)}")
+    nb, H, _, D = cache_k.shape
+    if tuple(cache_v.shape) != (nb, H, D, 16):
+        raise ValueError(f"cache_v must be [nb, Hkv, D, 16], got {tuple(cache_v.shape)}")
+    if not (cache_k.is_contiguous() and cache_v.is_contiguous()):
+        raise ValueError("paged caches must be contiguous")
+    return nb, H, D
+
+
+def decode_attention(q, cache_k, cache_v, block_tables, ctx_lens, max_ctx, scale=1.0,
+                     out=None, workspace=None, stream=None):
+    """GQA decode attention for one layer.
+
+    q [B, Hq, D] bf16 (query head h reads KV head h // (Hq/Hkv)); cache_k
+    [nb, Hkv, 16, D], cache_v [nb, Hkv, D, 16]; block_tables int32 [B, max_blocks]
+    and ctx_lens int32 [B] on the device; ``max_ctx`` >= every ctx_lens[b]."""
+    _need(q, "q")
+    nb, H, D = _check_layer_cache(cache_k, cache_v)
+    if q.dim() != 3 or q.shape[2] != D or not q.is_contiguous():
+        raise ValueError(f"q must be contiguous [B, Hq, {D}], got {tuple(q.shape)}")
+    B, Hq, _ = q.shape
+    _need(block_tables, "block_tables", torch.int32)
+    _need(ctx_lens, "ctx_lens", torch.int32)
+    if block_tables.dim() != 2 or block_tables.shape[0] != B or not block_tables.is_contiguous():
+        raise ValueError("block_tables must be contiguous int32 [B, max_blocks]")
+    if ctx_lens.numel() != B:
+        raise ValueError("ctx_lens must hold B entries")
+    if out is None:
+        out = torch.empty_like(q)
+    need = workspace_bytes(B, Hq, max_ctx, D)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
+    ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
+    ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr else 0
+    _lib.call("pdk_decode_attn", q.data_ptr(), cache_k.data_ptr(), cache_v.data_ptr(), nb,
+              block_tables.data_ptr(), block_tables.shape[1], ctx_lens.data_ptr(), int(max_ctx),
+              B, Hq, H, D, float(scale), ws_ptr, ws_bytes, out.data_ptr(), stream_handle(stream))
+    return out
+
+
+def cache_append(k_new, v_new, cache_k, cache_v, block_tables, ctx_lens, stream=None):
+    """Write each stream's new k/v [B, Hkv, D] at slot ctx_lens[b]-1
+    (the one-hot injection of kernels/decode_batch.py:81-82)."""
+    _need(k_new, "k_new")
+    _need(v_new, "v_new")
+    nb, H, D = _check_layer_cache(cache_k, cache_v)
+    B = k_new.shape[0]
+    if tuple(k_new.shape) != (B, H, D) or tuple(v_new.shape) != (B, H, D):
+        raise ValueError("k_new/v_new must be [B, Hkv, D]")
+    _lib.call("pdk_cache_append", k_new.contiguous().data_ptr(), v_new.contiguous().data_ptr(),
+              cache_k.data_ptr(), cache_v.data_ptr(), nb, block_tables.data_ptr(),
+              block_tables.shape[1], ctx_lens.data_ptr(), B, H, D, stream_handle(stream))
+
+
+def greedy_argmax(logits, out=None, stream=None):
+    """First-maximum argmax per row of bf16 logits [B, V] -> int32 [B]."""
+    _need(logits, "logits")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [B, V] with unit column stride")
+    B, V = logits.shape
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    _lib.call("pdk_greedy_argmax", logits.data_ptr(), B, V, logits.stride(0), out.data_ptr(),
+              stream_handle(stream))
+    return out

@@ -1,0 +1,225 @@
+"""Parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Handoff kernels are permutations of bf16 bits: bit-exact. Decode attention is
+floating point: bf16 outputs within 2e-2 abs / 1e-2 rel of the fp32 check
+(the tolerance the decode path is specified to).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import native as orc
+from tests._util import rand_bf16, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _prefill(rng, L, T, H, D):
+    return rand_bf16(rng, (L, T, H, D)), rand_bf16(rng, (L, T, H, D))
+
+
+@pytest.mark.parametrize("L,T,S,P,H,D", [
+    (2, 16, 16, 16, 8, 128),
+    (2, 64, 64, 37, 8, 128),
+    (3, 100, 128, 100, 8, 128),
+    (1, 512, 512, 512, 8, 128),
+    (2, 512, 512, 0, 8, 128),
+    (4, 300, 512, 300, 8, 128),
+    (2, 80, 80, 65, 2, 64),
+    (32, 512, 512, 257, 8, 128),
+])
+def test_pack_bit_exact(cuda, L, T, S, P, H, D):
+    from rngd_pd_amd.kernels import pack_kv
+    rng = np.random.default_rng(L * 1000 + P)
+    k, v = _prefill(rng, L, T, H, D)
+    want = orc.pack_kv(k, v, P, S)
+    frame = pack_kv(to_dev(k), to_dev(v), P, S)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(frame), want)
+
+
+def test_pack_strided_stack(cuda):
+    """A stacked [L, 2, T, Hkv, D] prefill tensor packs through kv[:, 0] / kv[:, 1]."""
+    from rngd_pd_amd.kernels import pack_kv
+    rng = np.random.default_rng(7)
+    L, T, H, D, S, P = 4, 96, 8, 128, 128, 90
+    kv = rand_bf16(rng, (L, 2, T, H, D))
+    want = orc.pack_kv(kv[:, 0], kv[:, 1], P, S)
+    d = to_dev(kv)
+    frame = pack_kv(d[:, 0], d[:, 1], P, S)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(frame), want)
+
+
+def test_pack_batch(cuda):
+    from rngd_pd_amd.kernels import pack_kv_batch, frame_shape
+    rng = np.random.default_rng(11)
+    L, H, D, S = 3, 8, 128, 512
+    Ps = [64, 511, 1, 512, 200]
+    reqs, wants = [], []
+    for P in Ps:
+        k, v = _prefill(rng, L, S, H, D)
+        wants.append(orc.pack_kv(k, v, P, S))
+        frame = torch.full(frame_shape(L, H, D, S), 7.0, dtype=torch.bfloat16, device=cuda)
+        reqs.append((to_dev(k), to_dev(v), P, frame))
+    pack_kv_batch(reqs, S)
+    torch.cuda.synchronize()
+    for (_, _, _, frame), want in zip(reqs, wants):
+        np.testing.assert_array_equal(to_host(frame), want)
+
+
+def _cache(L, nb, H, D, fill=0x3F80):
+    ck = np.full((L, nb, H, 16, D), fill, np.uint16)
+    cv = np.full((L, nb, H, D, 16), fill, np.uint16)
+    return ck, cv
+
+
+@pytest.mark.parametrize("L,S,P,H,D", [
+    (2, 16, 16, 8, 128),
+    (2, 64, 37, 8, 128),
+    (3, 512, 512, 8, 128),
+    (2, 512, 1, 8, 128),
+    (2, 512, 0, 8, 128),
+    (32, 512, 333, 8, 128),
+    (2, 96, 81, 2, 64),
+])
+def test_scatter_bit_exact(cuda, L, S, P, H, D):
+    from rngd_pd_amd.kernels import scatter_paged
+    rng = np.random.default_rng(P + 5)
+    k, v = _prefill(rng, L, S, H, D)
+    frame = orc.pack_kv(k, v, P, S)
+    nb = max(1, (S // 16) * 2)
+    table = rng.permutation(nb)[: max(1, (P + 15) // 16)].astype(np.int32)
+    ck, cv = _cache(L, nb, H, D)
+    want_k, want_v = ck.copy(), cv.copy()
+    orc.scatter_paged(frame, table, P, S, H, D, want_k, want_v)
+    dk, dv = to_dev(ck), to_dev(cv)
+    scatter_paged(to_dev(frame), table, P, S, dk, dv)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(dk), want_k)
+    np.testing.assert_array_equal(to_host(dv), want_v)
+
+
+def test_scatter_batch_and_gather_round_trip(cuda):
+    from rngd_pd_amd.kernels import scatter_paged_batch, gather_paged
+    rng = np.random.default_rng(3)
+    L, S, H, D = 4, 512, 8, 128
+    Ps = [int(p) for p in rng.integers(64, 513, 8)]
+    need = [(p + 15) // 16 for p in Ps]
+    nb = sum(need) + 5
+    perm = rng.permutation(nb).astype(np.int32)
+    tables, off = [], 0
+    for n in need:
+        tables.append(perm[off:off + n])
+        off += n
+    ck, cv = _cache(L, nb, H, D, fill=0)
+    want_k, want_v = ck.copy(), cv.copy()
+    frames = []
+    for P, t in zip(Ps, tables):
+        k, v = _prefill(rng, L, S, H, D)
+        f = orc.pack_kv(k, v, P, S)
+        frames.append(f)
+        orc.scatter_paged(f, t, P, S, H, D, want_k, want_v)
+    dk, dv = to_dev(ck), to_dev(cv)
+    reqs = [(to_dev(f), torch.from_numpy(t).to(cuda), P) for f, t, P in zip(frames, tables, Ps)]
+    scatter_paged_batch(reqs, S, dk, dv)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(dk), want_k)
+    np.testing.assert_array_equal(to_host(dv), want_v)
+    for f, t, P in zip(frames, tables, Ps):
+        back = gather_paged(dk, dv, t, P, S)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_host(back), f)
+        np.testing.assert_array_equal(to_host(back), orc.gather_paged(want_k, want_v, t, P, S))
+
+
+def _attn_case(rng, B, Hq, H, ctx, D=128):
+    max_blocks = max((c + 15) // 16 for c in ctx)
+    nb = B * max_blocks + 3
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.full((B, max_blocks), -1, np.int32)
+    off = 0
+    for b, c in enumerate(ctx):
+        n = (c + 15) // 16
+        tables[b, :n] = perm[off:off + n]
+        off += n
+    ck = rand_bf16(rng, (nb, H, 16, D))
+    cv = rand_bf16(rng, (nb, H, D, 16))
+    q = rand_bf16(rng, (B, Hq, D))
+    return q, ck, cv, tables, np.asarray(ctx, np.int32)
+
+
+@pytest.mark.parametrize("B,Hq,H,ctx", [
+    (1, 32, 8, [1]),
+    (2, 32, 8, [17, 16]),
+    (4, 32, 8, [512, 512, 512, 512]),
+    (4, 32, 8, [129, 128, 127, 1]),
+    (8, 32, 8, [512, 64, 300, 511, 2, 33, 256, 480]),
+    (16, 32, 8, [512] * 16),
+    (3, 32, 8, [2048, 1500, 700]),
+    (2, 8, 8, [200, 37]),
+    (2, 16, 8, [200, 37]),
+    (2, 64, 8, [200, 37]),
+    (2, 128, 8, [300, 5]),
+])
+def test_decode_attention_vs_fp32(cuda, B, Hq, H, ctx):
+    from rngd_pd_amd.kernels import decode_attention
+    rng = np.random.default_rng(B * 100 + Hq + len(ctx))
+    q, ck, cv, tables, ctx_a = _attn_case(rng, B, Hq, H, ctx)
+    scale = 1.0 / math.sqrt(128)
+    want = orc.decode_attn(q, ck, cv, tables, ctx_a, scale)
+    out = decode_attention(to_dev(q), to_dev(ck), to_dev(cv), torch.from_numpy(tables).to(cuda),
+                           torch.from_numpy(ctx_a).to(cuda), int(ctx_a.max()), scale=scale)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+
+
+def test_decode_attention_max_ctx_bound_above_actual(cuda):
+    """A launch sized for a larger max_ctx gives the same result (empty splits)."""
+    from rngd_pd_amd.kernels import decode_attention
+    rng = np.random.default_rng(5)
+    q, ck, cv, tables, ctx_a = _attn_case(rng, 4, 32, 8, [100, 40, 1, 77])
+    tables = np.concatenate([tables, np.full((4, 30), -1, np.int32)], 1)
+    want = orc.decode_attn(q, ck, cv, tables, ctx_a, 0.1)
+    out = decode_attention(to_dev(q), to_dev(ck), to_dev(cv), torch.from_numpy(tables).to(cuda),
+                           torch.from_numpy(ctx_a).to(cuda), 16 * tables.shape[1], scale=0.1)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+
+
+def test_cache_append_then_attend(cuda):
+    from rngd_pd_amd.kernels import cache_append, decode_attention
+    rng = np.random.default_rng(9)
+    B, Hq, H, D = 4, 32, 8, 128
+    q, ck, cv, tables, ctx_a = _attn_case(rng, B, Hq, H, [64, 65, 1, 300])
+    k_new = rand_bf16(rng, (B, H, D))
+    v_new = rand_bf16(rng, (B, H, D))
+    want_k, want_v = ck.copy(), cv.copy()
+    orc.cache_append(k_new, v_new, want_k, want_v, tables, ctx_a)
+    dk, dv = to_dev(ck), to_dev(cv)
+    dt, dc = torch.from_numpy(tables).to(cuda), torch.from_numpy(ctx_a).to(cuda)
+    cache_append(to_dev(k_new), to_dev(v_new), dk, dv, dt, dc)
+    out = decode_attention(to_dev(q), dk, dv, dt, dc, int(ctx_a.max()), scale=1 / math.sqrt(D))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(dk), want_k)
+    np.testing.assert_array_equal(to_host(dv), want_v)
+    want = orc.decode_attn(q, want_k, want_v, tables, ctx_a, 1 / math.sqrt(D))
+    np.testing.assert_allclose(out.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+
+
+def test_greedy_argmax(cuda):
+    from rngd_pd_amd.kernels import greedy_argmax
+    rng = np.random.default_rng(2)
+    B, V = 16, 128256
+    x = rand_bf16(rng, (B, V), scale=3.0)
+    x[3, 1000] = x[3, 5] = 0x4300        # a tie (128.0): the first index wins
+    x[5, 77] = 0x7FC0                     # NaN ranks first
+    want = orc.greedy_argmax(x)
+    got = greedy_argmax(to_dev(x)).cpu().numpy()
+    np.testing.assert_array_equal(got, want)
+    assert want[3] == 5 and want[5] == 77
