@@ -1,0 +1,482 @@
+#!/usr/bin/env python3
+"""Benchmark of the prefill->decode KV handoff and decode_batch attention on one MI355X.
+
+Metric (one JSON line on stdout): KV handoff GB/s over a batch of 8 Llama-3.1-8B
+requests (32 layers x K/V x 8 KV heads x head_dim 128, bf16, S=512 frames,
+lengths uniform in [64, 512] from seed 0), with the ms per 512-token request and
+decode_batch tokens/s alongside.
+
+  step      pack all 8 requests into their transport frames (one launch) and
+            scatter every frame into the paged decode cache (block 16, seeded
+            permuted block table; one launch). Prefill KV is resident in HBM
+            before the clock starts; handoff bytes = sum(P) * 131072 B.
+  staged    the same request through pinned host memory: per layer pack ->
+            D2H (side stream) -> H2D (second stream) -> scatter, chained by
+            events (the reference's device->host->device staging).
+  decode    GQA decode attention, 32 layers x B streams at context 512, per-layer
+            launches, eager and replayed from a HIP graph.
+  cpu       the oracle's restatement of the reference CPU shm path (ser -> /dev/shm
+            -> deser -> f32 place) on a bounded sample of the same requests.
+
+  python bench.py [--steps K] [--warmup W] [--cpu-seconds X]
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+L, H, D, S, BS = 32, 8, 128, 512, 16
+HQ = 32
+TOKEN_BYTES = L * 2 * H * D * 2          # 131072 B of K+V per token, all layers
+HBM_PEAK_GBS = 8000.0
+METRIC = "KV handoff GB/s + ms per 512-tok Llama-8B request; decode_batch tokens/s"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bound on the CPU baseline sample (0 skips it)")
+    ap.add_argument("--only", choices=["all", "handoff", "decode", "copy"], default="all",
+                    help="restrict the run (for profiler passes)")
+    ap.add_argument("--copy-mib", type=int, default=1024,
+                    help="bytes moved by --only copy (traffic-counter calibration)")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def roofline(bytes_per_launch, seconds_per_launch, traffic=None):
+    achieved = bytes_per_launch / seconds_per_launch / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "bytes_per_launch": int(bytes_per_launch),
+            "us_per_launch": round(seconds_per_launch * 1e6, 2)}
+
+
+class Timer:
+    """HIP-event pairs on torch's current stream (the stream the kernels run on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = {}
+
+    def begin(self, name):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.setdefault(name, []).append([e, None])
+
+    def end(self, name):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs[name][-1][1] = e
+
+    def mean_s(self, name):
+        ms = [a.elapsed_time(b) for a, b in self.pairs[name]]
+        return statistics.fmean(ms) / 1e3
+
+    def median_s(self, name):
+        return statistics.median(a.elapsed_time(b) for a, b in self.pairs[name]) / 1e3
+
+
+def workload(seed=0, n=8):
+    rng = np.random.default_rng(seed)
+    return [int(p) for p in rng.integers(64, S + 1, n)]
+
+
+def make_tables(torch, dev, lengths, seed=0, slack=16):
+    rng = np.random.default_rng(seed + 1)
+    need = [(p + BS - 1) // BS for p in lengths]
+    nb = sum(need) + slack
+    perm = rng.permutation(nb).astype(np.int32)
+    tables, off = [], 0
+    for n in need:
+        tables.append(torch.from_numpy(perm[off:off + n].copy()).to(dev))
+        off += n
+    return nb, tables
+
+
+def bench_handoff(args, torch, K, lib, dev, out):
+    from rngd_pd_amd._lib import PackReq, ScatterReq
+    lengths = workload()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    prefill = [torch.randn((L, 2, S, H, D), generator=gen, device=dev).to(torch.bfloat16)
+               for _ in lengths]
+    frames = [torch.empty(K.frame_shape(L, H, D, S), dtype=torch.bfloat16, device=dev)
+              for _ in lengths]
+    nb, tables = make_tables(torch, dev, lengths)
+    cache_k = torch.zeros((L, nb, H, BS, D), dtype=torch.bfloat16, device=dev)
+    cache_v = torch.zeros((L, nb, H, D, BS), dtype=torch.bfloat16, device=dev)
+    pack = (PackReq * len(lengths))(*[
+        PackReq(p.data_ptr(), p[:, 1].data_ptr(), f.data_ptr(), p.stride(0), p.stride(2), P, 0)
+        for p, f, P in zip(prefill, frames, lengths)])
+    scat = (ScatterReq * len(lengths))(*[
+        ScatterReq(f.data_ptr(), t.data_ptr(), P, t.numel())
+        for f, t, P in zip(frames, tables, lengths)])
+    st = torch.cuda.current_stream().cuda_stream
+    n = len(lengths)
+
+    def step(timer=None):
+        if timer:
+            timer.begin("pack")
+        rc = lib.pdk_pack_kv_batch(pack, n, L, S, H, D, st)
+        if timer:
+            timer.end("pack")
+            timer.begin("scatter")
+        rc |= lib.pdk_scatter_paged_batch(scat, n, L, S, H, D, cache_k.data_ptr(),
+                                          cache_v.data_ptr(), cache_k.stride(0), nb, st)
+        if timer:
+            timer.end("scatter")
+        if rc:
+            raise RuntimeError("handoff launch failed: " + lib.pdk_last_error().decode())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # Parity spot check of the timed path: gather request 0 back and compare with its source.
+    back = K.gather_paged(cache_k, cache_v, tables[0], lengths[0], S)
+    ref = K.pack_kv(prefill[0][:, 0], prefill[0][:, 1], lengths[0], S)
+    torch.cuda.synchronize()
+    if not torch.equal(back.view(torch.int16), ref.view(torch.int16)):
+        raise RuntimeError("handoff round trip is not bit-exact")
+
+    timer = Timer(torch)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(timer)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    tokens = sum(lengths)
+    handoff_bytes = tokens * TOKEN_BYTES
+    out["value"] = round(handoff_bytes * args.steps / wall / 1e9, 2)
+    out["ms_per_step"] = round(wall / args.steps * 1e3, 4)
+    pack_bytes = (tokens + n * S) * TOKEN_BYTES       # read valid tokens + write S-wide frames
+    scat_bytes = 2 * tokens * TOKEN_BYTES             # read valid frame columns + write blocks
+    out["roofline"] = roofline(pack_bytes, timer.mean_s("pack"))
+    out["kernels"] = {"pack_kv_batch": roofline(pack_bytes, timer.mean_s("pack")),
+                      "scatter_paged_batch": roofline(scat_bytes, timer.mean_s("scatter"))}
+    out["config"]["lengths"] = lengths
+    out["config"]["handoff_bytes_per_step"] = handoff_bytes
+    log(f"handoff batch: {out['value']} GB/s, {out['ms_per_step']} ms/step, "
+        f"pack {timer.mean_s('pack')*1e6:.1f} us, scatter {timer.mean_s('scatter')*1e6:.1f} us")
+
+    # One 512-token request through the device path (pack + scatter), median of repeats.
+    single = Timer(torch)
+    p512 = prefill[0]
+    f512 = frames[0]
+    nb1 = (S + BS - 1) // BS
+    t512 = torch.from_numpy(np.random.default_rng(5).permutation(nb).astype(np.int32)[:nb1]).to(dev)
+    for i in range(args.warmup + args.steps):
+        if i >= args.warmup:
+            single.begin("req")
+        K.pack_kv(p512[:, 0], p512[:, 1], S, S, frame=f512)
+        K.scatter_paged(f512, t512, S, S, cache_k, cache_v)
+        if i >= args.warmup:
+            single.end("req")
+    torch.cuda.synchronize()
+    out["extra"]["ms_per_512_request_device"] = round(single.median_s("req") * 1e3, 4)
+    out["extra"]["gbps_512_request_device"] = round(S * TOKEN_BYTES / single.median_s("req") / 1e9, 1)
+
+    bench_staged(args, torch, K, lib, dev, out, prefill, frames, tables, lengths, cache_k,
+                 cache_v, nb)
+
+
+def bench_staged(args, torch, K, lib, dev, out, prefill, frames, tables, lengths, cache_k,
+                 cache_v, nb):
+    """Pinned-host staging: per layer pack -> D2H -> H2D -> scatter across three streams."""
+    from rngd_pd_amd import hip
+    from rngd_pd_amd._lib import PackReq, ScatterReq, PDK_COPY_D2H, PDK_COPY_H2D
+    layer_bytes = 2 * H * D * S * 2
+    req_bytes = L * layer_bytes
+    pinned = hip.PinnedBuffer(req_bytes)
+    dframe = torch.empty(K.frame_shape(L, H, D, S), dtype=torch.bfloat16, device=dev)
+    s_d2h = torch.cuda.Stream(device=dev)
+    s_h2d = torch.cuda.Stream(device=dev)
+    e_pack, e_d2h, e_h2d = hip.EventArray(L), hip.EventArray(L), hip.EventArray(L)
+    comp = torch.cuda.current_stream()
+    st = comp.cuda_stream
+
+    def one(i, timer=None):
+        p, P, t = prefill[i], lengths[i], tables[i]
+        src = frames[i]
+        if timer:
+            timer.begin("staged")
+        r = PackReq(p.data_ptr(), p[:, 1].data_ptr(), src.data_ptr(), p.stride(0), p.stride(2), P, 0)
+        rc = lib.pdk_pack_kv_layerwise(ctypes.byref(r), L, S, H, D, e_pack.ptr, st)
+        rc |= lib.pdk_copy_layers(ctypes.c_void_p(pinned.ptr), ctypes.c_void_p(src.data_ptr()),
+                                  layer_bytes, L, PDK_COPY_D2H, e_pack.ptr, e_d2h.ptr,
+                                  s_d2h.cuda_stream)
+        rc |= lib.pdk_copy_layers(ctypes.c_void_p(dframe.data_ptr()), ctypes.c_void_p(pinned.ptr),
+                                  layer_bytes, L, PDK_COPY_H2D, e_d2h.ptr, e_h2d.ptr,
+                                  s_h2d.cuda_stream)
+        sr = ScatterReq(dframe.data_ptr(), t.data_ptr(), P, t.numel())
+        rc |= lib.pdk_scatter_paged_layerwise(ctypes.byref(sr), L, S, H, D, cache_k.data_ptr(),
+                                              cache_v.data_ptr(), cache_k.stride(0), nb,
+                                              e_h2d.ptr, st)
+        if timer:
+            timer.end("staged")
+        if rc:
+            raise RuntimeError("staged launch failed: " + lib.pdk_last_error().decode())
+
+    n = len(lengths)
+    for i in range(min(args.warmup, 3)):
+        one(i % n)
+        torch.cuda.synchronize()     # the pinned buffer and device frame are reused
+    # Bit-exact check of the staged path: the device frame after H2D equals the packed frame.
+    one(0)
+    torch.cuda.synchronize()
+    if not torch.equal(dframe.view(torch.int16), frames[0].view(torch.int16)):
+        raise RuntimeError("staged frame differs from the packed frame")
+    timer = Timer(torch)
+    reps = max(3, min(args.steps, 20))
+    full = [i for i in range(n) if lengths[i] >= 0]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for rep in range(reps):
+        for i in full:
+            one(i, timer)
+            torch.cuda.synchronize()   # one request at a time: ms per request
+    wall = time.perf_counter() - t0
+    moved = reps * sum(lengths[i] for i in full) * TOKEN_BYTES
+    out["extra"]["staged_gbps"] = round(moved / wall / 1e9, 2)
+    # A 512-token request: the frame moves 64 MiB each way whatever P is.
+    ms = []
+    p512 = prefill[0]
+    saved = lengths[0]
+    lengths[0] = S
+    t512 = torch.arange((S + BS - 1) // BS, dtype=torch.int32, device=dev)
+    tables_0 = tables[0]
+    tables[0] = t512
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        one(0)
+        torch.cuda.synchronize()
+        ms.append((time.perf_counter() - a) * 1e3)
+    lengths[0] = saved
+    tables[0] = tables_0
+    out["extra"]["ms_per_512_request_staged"] = round(statistics.median(ms), 3)
+    out["extra"]["gbps_512_request_staged"] = round(S * TOKEN_BYTES / statistics.median(ms) / 1e6, 2)
+
+    # Host-link rates of the two copy directions alone (64 MiB each).
+    ta, tb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    res = {}
+    for name, direction, dst, src in (("d2h", PDK_COPY_D2H, pinned.ptr, frames[0].data_ptr()),
+                                      ("h2d", PDK_COPY_H2D, dframe.data_ptr(), pinned.ptr)):
+        vals = []
+        for _ in range(5):
+            ta.record()
+            rc = lib.pdk_copy_layers(ctypes.c_void_p(dst), ctypes.c_void_p(src), req_bytes, 1,
+                                     direction, None, None, st)
+            tb.record()
+            torch.cuda.synchronize()
+            if rc:
+                raise RuntimeError(lib.pdk_last_error().decode())
+            vals.append(ta.elapsed_time(tb))
+        res[name + "_gbps"] = round(req_bytes / (statistics.median(vals) / 1e3) / 1e9, 1)
+    out["extra"]["host_link"] = res
+    log(f"staged: {out['extra']['ms_per_512_request_staged']} ms per 512 request, "
+        f"{out['extra']['staged_gbps']} GB/s batch, link {res}")
+    for e in (e_pack, e_d2h, e_h2d):
+        e.close()
+    pinned.close()
+
+
+def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
+    res = {}
+    for B in batches:
+        nb_per = (ctx + BS - 1) // BS
+        nb = B * nb_per
+        gen = torch.Generator(device=dev).manual_seed(B)
+        cache_k = torch.randn((L, nb, H, BS, D), generator=gen, device=dev).to(torch.bfloat16)
+        cache_v = torch.randn((L, nb, H, D, BS), generator=gen, device=dev).to(torch.bfloat16)
+        q = torch.randn((L, B, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
+        perm = np.random.default_rng(B).permutation(nb).astype(np.int32).reshape(B, nb_per)
+        tables = torch.from_numpy(perm).to(dev)
+        ctx_lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        outp = torch.empty((L, B, HQ, D), dtype=torch.bfloat16, device=dev)
+        wsb = K.workspace_bytes(B, HQ, ctx, D)
+        ws = torch.zeros(max(1, wsb // 4), dtype=torch.float32, device=dev)   # split counters start at zero
+        scale = 1.0 / math.sqrt(D)
+        ptrs = [(q[l].data_ptr(), cache_k[l].data_ptr(), cache_v[l].data_ptr(), outp[l].data_ptr())
+                for l in range(L)]
+
+        def step(timer=None):
+            st = torch.cuda.current_stream().cuda_stream
+            rc = 0
+            for l in range(L):
+                qp, kp, vp, op = ptrs[l]
+                if timer:
+                    timer.begin("attn")
+                rc |= lib.pdk_decode_attn(qp, kp, vp, nb, tables.data_ptr(), nb_per,
+                                          ctx_lens.data_ptr(), ctx, B, HQ, H, D, scale,
+                                          ws.data_ptr(), wsb, op, st)
+                if timer:
+                    timer.end("attn")
+            if rc:
+                raise RuntimeError("decode attention launch failed: " + lib.pdk_last_error().decode())
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        timer = Timer(torch)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step(timer)
+        torch.cuda.synchronize()
+        eager = (time.perf_counter() - t0) / args.steps
+        # The same 32-layer step replayed from a HIP graph (no host launch cost).
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                step()
+        torch.cuda.synchronize()
+        graph_ref = outp.clone()
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(outp.view(torch.int16), graph_ref.view(torch.int16)):
+            raise RuntimeError("graph replay differs from eager attention")
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            g.replay()
+        torch.cuda.synchronize()
+        graphed = (time.perf_counter() - t0) / args.steps
+        kv_bytes = B * ctx * H * D * 2 * 2 + 2 * B * HQ * D * 2   # K+V read, q read, out write
+        kern = timer.mean_s("attn")
+        res[f"B{B}"] = {
+            "tokens_per_s_graph": round(B / graphed, 1),
+            "tokens_per_s_eager": round(B / eager, 1),
+            "step_us_graph": round(graphed * 1e6, 1),
+            "step_us_eager": round(eager * 1e6, 1),
+            "layer_call_us": round(kern * 1e6, 2),
+            "roofline": roofline(kv_bytes, kern),
+            "step_hbm_frac_graph": round(L * kv_bytes / graphed / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"decode B={B}: graph {graphed*1e6:.1f} us/step ({B/graphed:.0f} tok/s), "
+            f"eager {eager*1e6:.1f} us, layer call {kern*1e6:.2f} us")
+        del cache_k, cache_v, q, outp, ws, g
+        torch.cuda.empty_cache()
+    out["extra"]["decode_batch"] = res
+    out["kernels"] = dict(out.get("kernels", {}), decode_attn_B16=res[f"B{batches[-1]}"]["roofline"])
+
+
+def bench_cpu(args, out):
+    """The reference CPU shm path (oracle restatement), bounded to ~cpu_seconds."""
+    from oracle import wire
+    lengths = out["config"].get("lengths") or workload()
+    root_parent = "/dev/shm" if os.access("/dev/shm", os.W_OK) else None
+    root = tempfile.mkdtemp(prefix="pdk_cpu_baseline.", dir=root_parent)
+    times, moved, reqs = [], 0, 0
+    try:
+        data = []
+        budget_t0 = time.perf_counter()
+        for i, P in enumerate(lengths):
+            Kf = wire.make_kv(100 + i, (L, H, D, S))
+            Vf = wire.make_kv(200 + i, (L, H, S, D))
+            Kf[:, :, :, P:] = 0.0
+            Vf[:, :, P:, :] = 0.0
+            data.append((P, Kf, Vf))
+            if time.perf_counter() - budget_t0 > args.cpu_seconds / 2:
+                break
+        wire.cpu_shm_handoff(root, "warm", data[0][1], data[0][2])
+        t_start = time.perf_counter()
+        while True:
+            for i, (P, Kf, Vf) in enumerate(data):
+                Kg, Vg, sec = wire.cpu_shm_handoff(root, f"r{reqs}", Kf, Vf)
+                if not (np.array_equal(Kg.view(np.uint32), Kf.view(np.uint32))
+                        and np.array_equal(Vg.view(np.uint32), Vf.view(np.uint32))):
+                    raise RuntimeError("CPU shm round trip is not byte-exact")
+                times.append(sec)
+                moved += P * TOKEN_BYTES
+                reqs += 1
+            if time.perf_counter() - t_start > args.cpu_seconds:
+                break
+        wall = sum(times)
+    finally:
+        for f in os.listdir(root):
+            os.unlink(os.path.join(root, f))
+        os.rmdir(root)
+    cores_avail = len(os.sched_getaffinity(0))
+    out["cpu_baseline"] = {
+        "value": round(moved / wall / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": (f"{reqs} requests ({len(data)} distinct of the batch's lengths, S=512 frames, "
+                   f"64 MiB bf16 each on the wire) through ser -> /dev/shm tmp+fsync+rename -> "
+                   f"read -> deser -> f32 place, single thread, {wall:.1f} s; "
+                   f"{cores_avail} cores visible"),
+        "ms_per_request_median": round(statistics.median(times) * 1e3, 2),
+    }
+    log(f"cpu baseline: {out['cpu_baseline']['value']} GB/s, "
+        f"{out['cpu_baseline']['ms_per_request_median']} ms/request")
+
+
+def bench_copy(args, torch, K, dev):
+    """A plain copy kernel of known size, for scaling the FETCH/WRITE counters."""
+    n = args.copy_mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(args.warmup + args.steps):
+        K.copy_kernel(b, a)
+    torch.cuda.synchronize()
+    log(f"copy kernel: {n} bytes x {args.warmup + args.steps} launches")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+    from rngd_pd_amd import kernels as K
+    from rngd_pd_amd import _lib
+    lib = _lib.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    out = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic: seeded N(0,1) bf16 KV; request lengths U[64,512] from seed 0",
+           "config": {"workload": "KV handoff batch: 8 Llama-3.1-8B requests, lengths U[64,512], "
+                                  "pack (layer-major S=512 frames) + scatter into a paged cache "
+                                  "(block 16, permuted block table)",
+                      "layers": L, "kv_heads": H, "head_dim": D, "frame_tokens": S,
+                      "block_size": BS},
+           "extra": {}}
+    if args.only == "copy":
+        bench_copy(args, torch, K, dev)
+        return 0
+    if args.only in ("all", "handoff"):
+        bench_handoff(args, torch, K, lib, dev, out)
+    if args.only in ("all", "decode"):
+        bench_decode(args, torch, K, lib, dev, out)
+    if args.only == "all" and args.cpu_seconds > 0:
+        bench_cpu(args, out)
+    if args.only == "decode":
+        b = out["extra"]["decode_batch"]["B16"]
+        out.update(value=b["tokens_per_s_graph"], unit="tokens/s",
+                   ms_per_step=b["step_us_graph"] / 1e3, roofline=b["roofline"])
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -71,10 +71,16 @@ typedef struct pdk_pack_req {
   int64_t layer_stride;    /* elements between layers (both K and V)        */
   int64_t tok_stride;      /* elements between tokens; a multiple of 8      */
   int32_t P;               /* valid tokens, 0 <= P <= S                     */
-  int32_t reserved;
+  int32_t flags;           /* 0 or PDK_PACK_NARROW                          */
 } pdk_pack_req;
 
-/* One request: all L layers in one launch. Requires D % 64 == 0, S % 8 == 0,
+/* Leave frame columns >= P unwritten (except inside the 8-token group that
+ * holds column P-1, which is zero-filled). For device-to-device handoffs whose
+ * consumer reads only the first P columns; a frame bound for the shm wire
+ * needs the zero tail and must not set it. */
+#define PDK_PACK_NARROW 1
+
+/* One request: all L layers in one launch. Requires D % 64 == 0, S % 16 == 0,
  * 16-byte aligned pointers. */
 int pdk_pack_kv(const uint16_t* src_k, const uint16_t* src_v,
                 int64_t layer_stride, int64_t tok_stride, int n_layers, int P,
@@ -137,10 +143,16 @@ int pdk_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v,
  *   tables device int32 [B][max_blocks]
  *   scale  multiplies q.k (1.0 when the scale is folded into q, as the
  *          reference folds 1/sqrt(D) into wq, kernels/decode_batch.py:204)
- *   max_ctx  host upper bound of ctx[] used for the launch grid
- *   workspace  fp32 scratch of pdk_decode_attn_workspace_bytes() bytes
+ *   max_ctx  host upper bound of ctx[] used for the launch grid (tokens
+ *          past max_ctx, rounded up to the split size, are not read)
+ *   workspace  scratch of pdk_decode_attn_workspace_bytes() bytes (0 means
+ *          none is needed) holding split partials and per-(b, h) arrival
+ *          counters. It must be zero-filled before its first use; every
+ *          completed call leaves the counters zero again, so the buffer is
+ *          reused without clearing. One workspace serves one stream at a
+ *          time: calls that overlap on one workspace race.
  *   out    [B][Hq][D] bf16
- * Requires D == 128 and Hq/Hkv in {1, 2, 4, 8, 16}.
+ * Requires D == 128, Hq/Hkv in {1, 2, 4, 8, 16}, max_ctx <= 16384.
  */
 size_t pdk_decode_attn_workspace_bytes(int B, int n_q_heads, int max_ctx,
                                        int head_dim);
@@ -190,6 +202,37 @@ int pdk_memcpy_d2d(void* dev_dst, const void* dev_src, size_t bytes,
 int pdk_copy_kernel(void* dev_dst, const void* dev_src, size_t bytes,
                     uintptr_t stream);
 
+/* ---- layer-wise staging pipeline ---------------------------------------------
+ * The reference hands each layer group to the writer while the next computes
+ * (engines/prefill_full.py:337-388, serving/cluster.py:187-218) and loads
+ * layer by layer on the decode side (serving/cluster.py:458-459). These calls
+ * enqueue all layers of one request in a native loop, chaining stages on
+ * different streams through per-layer events (arrays of n_layers events made
+ * by pdk_event_create; a null array means no dependency). */
+#define PDK_COPY_D2H 0
+#define PDK_COPY_H2D 1
+#define PDK_COPY_D2D 2
+
+/* One pack launch per layer l (frame slice l), then done_events[l]. */
+int pdk_pack_kv_layerwise(const pdk_pack_req* req, int n_layers, int S,
+                          int n_kv_heads, int head_dim,
+                          const uintptr_t* done_events, uintptr_t stream);
+
+/* n_layers copies of layer_bytes at offsets l*layer_bytes: wait
+ * wait_events[l], copy, record done_events[l]. Host memory must be pinned
+ * (pdk_host_alloc) for the copies to run asynchronously. */
+int pdk_copy_layers(void* dst, const void* src, size_t layer_bytes,
+                    int n_layers, int direction, const uintptr_t* wait_events,
+                    const uintptr_t* done_events, uintptr_t stream);
+
+/* Wait wait_events[l], then scatter frame layer l into cache layer l. */
+int pdk_scatter_paged_layerwise(const pdk_scatter_req* req, int n_layers,
+                                int S, int n_kv_heads, int head_dim,
+                                uint16_t* cache_k, uint16_t* cache_v,
+                                int64_t cache_layer_stride, int num_blocks,
+                                const uintptr_t* wait_events,
+                                uintptr_t stream);
+
 /* ---- streams and events ------------------------------------------------------
  * Fences for the side-stream staging and for wait_for_save()
  * (connector/rngd_kv.py:129-131), which becomes a real barrier once saves
@@ -199,6 +242,7 @@ int pdk_stream_destroy(uintptr_t stream);
 int pdk_stream_sync(uintptr_t stream);
 #define PDK_EVENT_TIMING 0
 #define PDK_EVENT_INTERPROCESS 1   /* hipEventInterprocess | DisableTiming */
+#define PDK_EVENT_SYNC 2           /* hipEventDisableTiming: dependencies only */
 int pdk_event_create(uintptr_t* out, int flags);
 int pdk_event_destroy(uintptr_t event);
 int pdk_event_record(uintptr_t event, uintptr_t stream);

@@ -22,6 +22,10 @@ PDK_BLOCK_SIZE = 16
 PDK_IPC_HANDLE_BYTES = 64
 PDK_EVENT_TIMING = 0
 PDK_EVENT_INTERPROCESS = 1
+PDK_EVENT_SYNC = 2
+PDK_COPY_D2H = 0
+PDK_COPY_H2D = 1
+PDK_COPY_D2D = 2
 
 
 class PdkError(RuntimeError):
@@ -36,7 +40,10 @@ class PackReq(ctypes.Structure):
     _fields_ = [("src_k", ctypes.c_void_p), ("src_v", ctypes.c_void_p),
                 ("frame", ctypes.c_void_p), ("layer_stride", ctypes.c_int64),
                 ("tok_stride", ctypes.c_int64), ("P", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)]
+                ("flags", ctypes.c_int32)]
+
+
+PDK_PACK_NARROW = 1
 
 
 class ScatterReq(ctypes.Structure):
@@ -90,6 +97,10 @@ SIGNATURES = {
     "pdk_ipc_close_mem": (_I, [_P]),
     "pdk_ipc_export_event": (_I, [_U, _P]),
     "pdk_ipc_open_event": (_I, [_P, ctypes.POINTER(_U)]),
+    "pdk_pack_kv_layerwise": (_I, [ctypes.POINTER(PackReq), _I, _I, _I, _I, _P, _U]),
+    "pdk_copy_layers": (_I, [_P, _P, _SZ, _I, _I, _P, _P, _U]),
+    "pdk_scatter_paged_layerwise": (_I, [ctypes.POINTER(ScatterReq), _I, _I, _I, _I, _P, _P,
+                                         _I64, _I, _P, _U]),
 }
 
 _lib = None

@@ -62,11 +62,13 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
     }
   }
   if (t0 >= S) return;           // S % 8 == 0: the lane's 8 tokens are all in or all out
+  const bool narrow = (R.flags & PDK_PACK_NARROW) != 0;
+  if (narrow && t0 >= P) return;
   uint16_t* fk = R.frame + (int64_t)(2 * l) * F;
   uint16_t* fv = fk + F;
 #pragma unroll
   for (int r = 0; r < 8; ++r)
-    pdk::st16(fv + ((int64_t)h * S + t0 + r) * D + d0, vin[r]);
+    if (!narrow || t0 + r < P) pdk::st16(fv + ((int64_t)h * S + t0 + r) * D + d0, vin[r]);
   v8 kout[8];
   pdk::transpose8x8(kin, kout);  // kout[c]: dim d0+c, tokens t0..t0+7
 #pragma unroll
@@ -101,14 +103,14 @@ __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
   if (t0 >= ((P + 15) & ~15)) return;          // beyond the request's last block
   const int j = t0 >> 4;
   if (j >= R.n_table) return;
-  const int blk = R.table[j];
-  if (blk < 0 || blk >= a.num_blocks) return;
   const int slot0 = t0 & 15;
   const int d0 = dt * kTileD + di * 8;
   const int64_t F = (int64_t)a.Hkv * D * S;
   const uint16_t* fk = R.frame + (int64_t)(2 * l) * F;
   const uint16_t* fv = fk + F;
 
+  // The frame loads do not depend on the block id: issue them with it.
+  const int blk = R.table[j];
   v8 kin[8], vin[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
@@ -117,6 +119,7 @@ __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
     if (t0 + 8 > P) pdk::mask_tail(kin[r], t0, P);
     vin[r] = (t0 + r < P) ? pdk::ld16(fv + ((int64_t)h * S + t0 + r) * D + d0) : pdk::zero8();
   }
+  if (blk < 0 || blk >= a.num_blocks) return;
   v8 kout[8], vout[8];
   pdk::transpose8x8(kin, kout);  // kout[c]: token t0+c, dims d0..d0+7
   pdk::transpose8x8(vin, vout);  // vout[c]: dim d0+c, tokens t0..t0+7
@@ -209,6 +212,7 @@ extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_lay
     const pdk_pack_req& r = reqs[i];
     PDK_REQUIRE(r.frame && pdk::aligned16(r.frame), "request %d: frame null or not 16-byte aligned", i);
     PDK_REQUIRE(r.P >= 0 && r.P <= S, "request %d: P=%d outside [0, S=%d]", i, r.P, S);
+    PDK_REQUIRE((r.flags & ~PDK_PACK_NARROW) == 0, "request %d: unknown flags 0x%x", i, r.flags);
     if (r.P > 0) {
       PDK_REQUIRE(r.src_k && r.src_v && pdk::aligned16(r.src_k) && pdk::aligned16(r.src_v),
                   "request %d: src_k/src_v null or not 16-byte aligned", i);

@@ -207,10 +207,14 @@ int pdk_stream_sync(uintptr_t stream) {
 int pdk_event_create(uintptr_t* out, int flags) {
   pdk::clear_error();
   PDK_REQUIRE(out != nullptr, "out is null");
-  PDK_REQUIRE(flags == PDK_EVENT_TIMING || flags == PDK_EVENT_INTERPROCESS, "bad flags %d", flags);
+  PDK_REQUIRE(flags == PDK_EVENT_TIMING || flags == PDK_EVENT_INTERPROCESS ||
+                  flags == PDK_EVENT_SYNC,
+              "bad flags %d", flags);
   hipEvent_t e = nullptr;
   if (flags == PDK_EVENT_INTERPROCESS) {
     PDK_TRY_HIP(hipEventCreateWithFlags(&e, hipEventInterprocess | hipEventDisableTiming));
+  } else if (flags == PDK_EVENT_SYNC) {
+    PDK_TRY_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   } else {
     PDK_TRY_HIP(hipEventCreate(&e));
   }

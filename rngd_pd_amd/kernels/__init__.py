@@ -1,8 +1,8 @@
 """HIP kernels of the handoff and decode attention, called through the C ABI."""
 from .handoff import (pack_kv, pack_kv_batch, scatter_paged, scatter_paged_batch, gather_paged,
                       frame_shape, frame_views, stream_handle, validate_table, copy_kernel)
-from .attention import decode_attention, cache_append, greedy_argmax, workspace_bytes
+from .attention import decode_attention, cache_append, greedy_argmax, workspace_bytes, get_workspace
 
 __all__ = ["pack_kv", "pack_kv_batch", "scatter_paged", "scatter_paged_batch", "gather_paged",
            "frame_shape", "frame_views", "stream_handle", "validate_table", "copy_kernel",
-           "decode_attention", "cache_append", "greedy_argmax", "workspace_bytes"]
+           "decode_attention", "cache_append", "greedy_argmax", "workspace_bytes", "get_workspace"]

@@ -16,6 +16,23 @@ def workspace_bytes(B, n_q_heads, max_ctx, head_dim=128):
     return int(_lib.lib().pdk_decode_attn_workspace_bytes(B, n_q_heads, max_ctx, head_dim))
 
 
+_WORKSPACES = {}
+
+
+def get_workspace(nbytes, device):
+    """A zero-initialised fp32 workspace of at least ``nbytes`` on ``device``.
+
+    The kernel's split counters must read zero before a call and every call
+    leaves them zero, so one buffer is reused across calls. It serves one
+    stream at a time: concurrent calls on different streams need their own."""
+    key = torch.device(device).index or 0
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20) // 4 + 64, dtype=torch.float32, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def _check_layer_cache(cache_k, cache_v):
     _need(cache_k, "cache_k")
     _need(cache_v, "cache_v")
@@ -50,10 +67,16 @@ def decode_attention(q, cache_k, cache_v, block_tables, ctx_lens, max_ctx, scale
     if out is None:
         out = torch.empty_like(q)
     need = workspace_bytes(B, Hq, max_ctx, D)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
-    ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
-    ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr else 0
+    ws = None
+    if need:
+        if workspace is not None:
+            if workspace.numel() * workspace.element_size() < need:
+                raise ValueError(f"workspace holds fewer than the {need} bytes needed")
+            ws = workspace
+        else:
+            ws = get_workspace(need, q.device)
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
     _lib.call("pdk_decode_attn", q.data_ptr(), cache_k.data_ptr(), cache_v.data_ptr(), nb,
               block_tables.data_ptr(), block_tables.shape[1], ctx_lens.data_ptr(), int(max_ctx),
               B, Hq, H, D, float(scale), ws_ptr, ws_bytes, out.data_ptr(), stream_handle(stream))

@@ -80,9 +80,10 @@ def pack_kv(k, v, num_tokens, S, frame=None, stream=None):
     return frame
 
 
-def pack_kv_batch(reqs, S, stream=None):
+def pack_kv_batch(reqs, S, narrow=False, stream=None):
     """reqs: list of (k, v, num_tokens, frame) with equal (L, Hkv, D); frames
-    preallocated [L, 2, Hkv*D*S]. Launches ceil(n/16) kernels."""
+    preallocated [L, 2, Hkv*D*S]. Launches ceil(n/16) kernels. ``narrow``
+    leaves columns >= num_tokens unwritten (device-only consumers)."""
     if not reqs:
         return
     L = H = D = None
@@ -100,7 +101,7 @@ def pack_kv_batch(reqs, S, stream=None):
         if tuple(frame.shape) != frame_shape(L, H, D, S) or not frame.is_contiguous():
             raise ValueError(f"frame must be contiguous {frame_shape(L, H, D, S)}")
         arr.append(PackReq(k.data_ptr(), v.data_ptr(), frame.data_ptr(), k.stride(0),
-                           k.stride(1), int(P), 0))
+                           k.stride(1), int(P), _lib.PDK_PACK_NARROW if narrow else 0))
     st = stream_handle(stream)
     for i in range(0, len(arr), PDK_MAX_BATCH):
         chunk = arr[i:i + PDK_MAX_BATCH]

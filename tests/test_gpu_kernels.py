@@ -223,3 +223,71 @@ def test_greedy_argmax(cuda):
     got = greedy_argmax(to_dev(x)).cpu().numpy()
     np.testing.assert_array_equal(got, want)
     assert want[3] == 5 and want[5] == 77
+
+
+def test_pack_narrow_leaves_tail(cuda):
+    """PDK_PACK_NARROW writes columns < P (rounded to the 8-token group) and nothing past it."""
+    from rngd_pd_amd.kernels import pack_kv_batch, frame_shape
+    rng = np.random.default_rng(21)
+    L, H, D, S, P = 2, 8, 128, 128, 37
+    k, v = _prefill(rng, L, S, H, D)
+    full = orc.pack_kv(k, v, P, S)
+    frame = torch.full(frame_shape(L, H, D, S), 3.0, dtype=torch.bfloat16, device=cuda)
+    pack_kv_batch([(to_dev(k), to_dev(v), P, frame)], S, narrow=True)
+    torch.cuda.synchronize()
+    got = to_host(frame).reshape(L, 2, -1)
+    kf = got[:, 0].reshape(L, H, D, S)
+    vf = got[:, 1].reshape(L, H, S, D)
+    wk = full.reshape(L, 2, -1)[:, 0].reshape(L, H, D, S)
+    wv = full.reshape(L, 2, -1)[:, 1].reshape(L, H, S, D)
+    group_end = (P + 7) // 8 * 8
+    np.testing.assert_array_equal(kf[..., :group_end], wk[..., :group_end])
+    np.testing.assert_array_equal(vf[:, :, :P], wv[:, :, :P])
+    three = np.uint16(0x4040)
+    assert (kf[..., group_end:] == three).all() and (vf[:, :, P:] == three).all()
+
+
+def test_decode_attention_workspace_reuse(cuda):
+    """Split counters reset themselves: back-to-back calls of different shapes on one
+    workspace all match the oracle."""
+    from rngd_pd_amd.kernels import decode_attention, get_workspace, workspace_bytes
+    rng = np.random.default_rng(31)
+    ws = get_workspace(workspace_bytes(16, 32, 2048), cuda)
+    for B, ctx in [(16, [512] * 16), (4, [2048, 33, 1000, 512]), (16, [300] * 16), (1, [5])]:
+        q, ck, cv, tables, ctx_a = _attn_case(rng, B, 32, 8, ctx)
+        want = orc.decode_attn(q, ck, cv, tables, ctx_a, 0.088)
+        for _ in range(2):
+            out = decode_attention(to_dev(q), to_dev(ck), to_dev(cv),
+                                   torch.from_numpy(tables).to(cuda),
+                                   torch.from_numpy(ctx_a).to(cuda), int(ctx_a.max()),
+                                   scale=0.088, workspace=ws)
+            torch.cuda.synchronize()
+            np.testing.assert_allclose(out.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+
+
+def test_decode_attention_graph_replays(cuda):
+    """Captured in a HIP graph, every replay (with eager work between replays) equals
+    the eager result."""
+    from rngd_pd_amd.kernels import decode_attention
+    rng = np.random.default_rng(41)
+    B = 8
+    q, ck, cv, tables, ctx_a = _attn_case(rng, B, 32, 8, [512, 100, 7, 300, 512, 64, 65, 200])
+    dq, dk, dv = to_dev(q), to_dev(ck), to_dev(cv)
+    dt, dc = torch.from_numpy(tables).to(cuda), torch.from_numpy(ctx_a).to(cuda)
+    out = torch.empty_like(dq)
+    decode_attention(dq, dk, dv, dt, dc, 512, scale=0.1, out=out)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            decode_attention(dq, dk, dv, dt, dc, 512, scale=0.1, out=out)
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        decode_attention(dq, dk, dv, dt, dc, 512, scale=0.1, out=torch.empty_like(dq))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {i} differs"
