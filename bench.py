@@ -57,6 +57,21 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k, c = t.get("kernels", {}).get(kernel), t.get("calibration", {})
+    if not k:
+        return None
+    return int((k["fetch_kib"] * c["fetch_scale"] + k["write_kib"] * c["write_scale"]) * 1024)
+
+
 def roofline(bytes_per_launch, seconds_per_launch, traffic=None):
     achieved = bytes_per_launch / seconds_per_launch / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -164,9 +179,10 @@ def bench_handoff(args, torch, K, lib, dev, out):
     out["ms_per_step"] = round(wall / args.steps * 1e3, 4)
     pack_bytes = (tokens + n * S) * TOKEN_BYTES       # read valid tokens + write S-wide frames
     scat_bytes = 2 * tokens * TOKEN_BYTES             # read valid frame columns + write blocks
-    out["roofline"] = roofline(pack_bytes, timer.mean_s("pack"))
-    out["kernels"] = {"pack_kv_batch": roofline(pack_bytes, timer.mean_s("pack")),
-                      "scatter_paged_batch": roofline(scat_bytes, timer.mean_s("scatter"))}
+    out["roofline"] = roofline(pack_bytes, timer.mean_s("pack"), measured_traffic("pack_kv_batch"))
+    out["kernels"] = {"pack_kv_batch": out["roofline"],
+                      "scatter_paged_batch": roofline(scat_bytes, timer.mean_s("scatter"),
+                                                      measured_traffic("scatter_paged_batch"))}
     out["config"]["lengths"] = lengths
     out["config"]["handoff_bytes_per_step"] = handoff_bytes
     log(f"handoff batch: {out['value']} GB/s, {out['ms_per_step']} ms/step, "
@@ -314,17 +330,19 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
                 for l in range(L)]
 
         def step(timer=None):
+            # Event pairs bracket a whole 32-layer step: per-call pairs around a
+            # ~10 us kernel would also time the host's enqueue of the next call.
             st = torch.cuda.current_stream().cuda_stream
             rc = 0
+            if timer:
+                timer.begin("step")
             for l in range(L):
                 qp, kp, vp, op = ptrs[l]
-                if timer:
-                    timer.begin("attn")
                 rc |= lib.pdk_decode_attn(qp, kp, vp, nb, tables.data_ptr(), nb_per,
                                           ctx_lens.data_ptr(), ctx, B, HQ, H, D, scale,
                                           ws.data_ptr(), wsb, op, st)
-                if timer:
-                    timer.end("attn")
+            if timer:
+                timer.end("step")
             if rc:
                 raise RuntimeError("decode attention launch failed: " + lib.pdk_last_error().decode())
 
@@ -359,7 +377,7 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
         torch.cuda.synchronize()
         graphed = (time.perf_counter() - t0) / args.steps
         kv_bytes = B * ctx * H * D * 2 * 2 + 2 * B * HQ * D * 2   # K+V read, q read, out write
-        kern = timer.mean_s("attn")
+        kern = timer.mean_s("step") / L                           # one layer's launch(es)
         res[f"B{B}"] = {
             "tokens_per_s_graph": round(B / graphed, 1),
             "tokens_per_s_eager": round(B / eager, 1),
