@@ -146,11 +146,14 @@ int pdk_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v,
  *   max_ctx  host upper bound of ctx[] used for the launch grid (tokens
  *          past max_ctx, rounded up to the split size, are not read)
  *   workspace  scratch of pdk_decode_attn_workspace_bytes() bytes (0 means
- *          none is needed) holding split partials and per-(b, h) arrival
- *          counters. It must be zero-filled before its first use; every
- *          completed call leaves the counters zero again, so the buffer is
- *          reused without clearing. One workspace serves one stream at a
- *          time: calls that overlap on one workspace race.
+ *          none is needed) holding the per-split partial maxima, sums and
+ *          outputs when the context is split across workgroups. Every
+ *          entry read is written earlier in the same call, so it needs no
+ *          clearing. One workspace serves one stream at a time: calls that
+ *          overlap on one workspace race.
+ *   Splitting: the context is split across workgroups while B * Hkv is
+ *          below PDK_ATTN_SPLIT_BELOW (environment, default 128); results
+ *          agree with the unsplit path to fp32 rounding.
  *   out    [B][Hq][D] bf16
  * Requires D == 128, Hq/Hkv in {1, 2, 4, 8, 16}, max_ctx <= 16384.
  */

@@ -30,6 +30,7 @@
 // captured in a HIP graph.
 
 #include <math.h>
+#include <stdlib.h>
 
 #include "pdk_common.h"
 
@@ -68,26 +69,26 @@ struct AttnArgs {
 // Registers of one span between its loads and its use.
 struct Span {
   v8 ka[4], kb[4], vf[8];
+  bool v_ok;                     // this lane's V block id was valid
 };
 
-// Issue every load of the span starting at `span` (< lim). Loads are
-// unconditional from in-bounds addresses (indices clamped, invalid block ids
-// read block 0) so they are all in flight together; V of tokens >= lim is
-// zeroed afterwards, K of such tokens needs nothing (their scores become -inf).
-__device__ __forceinline__ void load_span(const AttnArgs& a, const int32_t* table, int h, int span,
-                                          int lim, int g, int j, Span& r) {
+// Issue every load of the 32-token span starting at `span`, whose tokens lie
+// in the blocks blk_lo (tokens span..span+15) and blk_hi (span+16..span+31).
+// Loads are unconditional from in-bounds addresses (an invalid block id reads
+// block 0) so they are all in flight together; V of tokens >= lim is zeroed
+// afterwards, K of such tokens needs nothing (their scores become -inf).
+__device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, int g, int j,
+                                          int blk_lo, int blk_hi, Span& r) {
   const int tau0 = 8 * (j >> 2) + (j & 3);      // QK tile-0 row j -> token offset
-  const int ta = span + tau0, tb = ta + 4;
-  const int tv = span + 8 * g;                   // this lane's 8 V tokens
-  const int last = lim - 1;
-  const int ba = table[min(ta, last) >> 4];
-  const int bb = table[min(tb, last) >> 4];
-  const int bv = table[min(tv, last) >> 4];
-  const int cba = (ba >= 0 && ba < a.num_blocks) ? ba : 0;
-  const int cbb = (bb >= 0 && bb < a.num_blocks) ? bb : 0;
-  const int cbv = (bv >= 0 && bv < a.num_blocks) ? bv : 0;
-  const uint16_t* pa = a.ck + (((int64_t)cba * a.Hkv + h) * 16 + (ta & 15)) * kD + g * 8;
-  const uint16_t* pb = a.ck + (((int64_t)cbb * a.Hkv + h) * 16 + (tb & 15)) * kD + g * 8;
+  const int ta = span + tau0, tb = ta + 4;      // both in blk_lo iff j < 8
+  const int tv = span + 8 * g;                   // this lane's 8 V tokens; blk_lo iff g < 2
+  const int bk = (j < 8) ? blk_lo : blk_hi;
+  const int bv = (g < 2) ? blk_lo : blk_hi;
+  const int cbk = (bk >= 0 && bk < a.num_blocks) ? bk : 0;
+  r.v_ok = bv >= 0 && bv < a.num_blocks;
+  const int cbv = r.v_ok ? bv : 0;
+  const uint16_t* pa = a.ck + (((int64_t)cbk * a.Hkv + h) * 16 + (ta & 15)) * kD + g * 8;
+  const uint16_t* pb = a.ck + (((int64_t)cbk * a.Hkv + h) * 16 + (tb & 15)) * kD + g * 8;
   const uint16_t* pv = a.cv + ((int64_t)cbv * a.Hkv + h) * kD * 16 + (tv & 15) + j * 16;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
@@ -98,66 +99,106 @@ __device__ __forceinline__ void load_span(const AttnArgs& a, const int32_t* tabl
   for (int n = 0; n < 8; ++n) r.vf[n] = pdk::ld16(pv + 16 * 16 * n);
 }
 
-// Fold one loaded span into the running (m, lsum, o) of query j = lane & 15.
-__device__ __forceinline__ void attend_span(const AttnArgs& a, const int32_t* table, Span& r,
-                                            const v8 qv[4], int span, int lim, int g, int j,
-                                            float& m, float& lsum, f32x4 o[8]) {
-  const int tv = span + 8 * g;
-  const int bv = table[min(tv, lim - 1) >> 4];
-  if (tv >= lim || bv < 0 || bv >= a.num_blocks) {
-#pragma unroll
-    for (int n = 0; n < 8; ++n) r.vf[n] = pdk::zero8();
-  } else if (tv + 8 > lim) {
-#pragma unroll
-    for (int n = 0; n < 8; ++n) pdk::mask_tail(r.vf[n], tv, lim);
-  }
+// Reductions over the four lanes of one query column {i, i^16, i^32, i^48}
+// with the gfx950 lane-swap instructions (VALU, no LDS round trip): after
+// v_permlane32_swap each lane holds {x[i], x[i^32]}, after v_permlane16_swap
+// {y[i], y[i^16]}. Both operands of each step are exchanged symmetrically, so
+// every lane of the column ends with the same bits.
+__device__ __forceinline__ float column_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+
+__device__ __forceinline__ float column_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+
+// QK of one span: lane (g, j) gets query j's scaled scores of tokens tv..tv+7
+// (tv = span + 8g); tokens >= lim get -inf.
+__device__ __forceinline__ void span_scores(const Span& r, const v8 qv[4], float scale_log2,
+                                            int tv, int lim, float* sc) {
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     s0 = mfma(r.ka[s], qv[s], s0);
     s1 = mfma(r.kb[s], qv[s], s1);
   }
-  // Lane (g, j): query j, tokens tv + e, e = 0..7.
-  float sc[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    sc[i] = s0[i] * a.scale_log2;
-    sc[4 + i] = s1[i] * a.scale_log2;
+    sc[i] = s0[i] * scale_log2;
+    sc[4 + i] = s1[i] * scale_log2;
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e)
     if (tv + e >= lim) sc[e] = -INFINITY;
-  float mx = sc[0];
+}
+
+// PV of one span with probabilities p[0..7] of tokens tv..tv+7.
+__device__ __forceinline__ void span_pv(Span& r, const float* p, uint32_t pmask, int tv, int lim,
+                                        f32x4 o[8]) {
+  if (tv >= lim || !r.v_ok) {
 #pragma unroll
-  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float m_new = fmaxf(m, mx);             // finite: token `span` is valid
-  const float alpha = exp2f(m - m_new);
-  float p[8], ps = 0.f;
+    for (int n = 0; n < 8; ++n) r.vf[n] = pdk::zero8();
+  } else if (tv + 8 > lim) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    p[e] = exp2f(sc[e] - m_new);
-    ps += p[e];
+    for (int n = 0; n < 8; ++n) pdk::mask_tail(r.vf[n], tv, lim);
   }
-  ps += __shfl_xor(ps, 16);
-  ps += __shfl_xor(ps, 32);
-  lsum = lsum * alpha + ps;
-  m = m_new;
   v8 pv;
-  const uint32_t pmask = j < a.G ? 0xffffffffu : 0u;
 #pragma unroll
   for (int w = 0; w < 4; ++w)
     pv.w[w] = (pdk::f32_to_bf16_rne(p[2 * w]) | (pdk::f32_to_bf16_rne(p[2 * w + 1]) << 16)) & pmask;
-  float ar[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+  for (int n = 0; n < 8; ++n) o[n] = mfma(pv, r.vf[n], o[n]);
+}
+
+// Fold spans A (and B, when has_b) into the running (m, lsum, o) of query
+// j = lane & 15 with one softmax over their 64 tokens. On the first pair the
+// running state is empty, so nothing is rescaled.
+__device__ __forceinline__ void attend_pair(const AttnArgs& a, Span& ra, Span& rb, bool has_b,
+                                            const v8 qv[4], int sa, int sb, int lim, int g, int j,
+                                            bool first, float& m, float& lsum, f32x4 o[8]) {
+  float sc[16];
+  span_scores(ra, qv, a.scale_log2, sa + 8 * g, lim, sc);
+  if (has_b) {
+    span_scores(rb, qv, a.scale_log2, sb + 8 * g, lim, sc + 8);
+  } else {
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[n][i] *= ar[i];
-    o[n] = mfma(pv, r.vf[n], o[n]);
+    for (int e = 8; e < 16; ++e) sc[e] = -INFINITY;
   }
+  float mx = sc[0];
+#pragma unroll
+  for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
+  mx = column_max(mx);                          // finite: token sa is valid
+  const float m_new = first ? mx : fmaxf(m, mx);
+  float p[16], ps = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    p[e] = exp2f(sc[e] - m_new);
+    ps += p[e];
+  }
+  ps = column_sum(ps);
+  if (first) {
+    lsum = ps;
+  } else {
+    const float alpha = exp2f(m - m_new);
+    lsum = lsum * alpha + ps;
+    float ar[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[n][i] *= ar[i];
+  }
+  m = m_new;
+  const uint32_t pmask = j < a.G ? 0xffffffffu : 0u;
+  span_pv(ra, p, pmask, sa + 8 * g, lim, o);
+  if (has_b) span_pv(rb, p + 8, pmask, sb + 8 * g, lim, o);
 }
 
 __global__ __launch_bounds__(512) void decode_attn_kernel(const AttnArgs a) {
@@ -179,25 +220,40 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(const AttnArgs a) {
   v8 qv[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) qv[s] = pdk::ld16(qp + 32 * s);
-  const uint32_t qmask = j < G ? 0xffffffffu : 0u;
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) qv[s].w[w] &= qmask;
+  // Columns j >= G repeat query G-1 (index clamped above); their P is zeroed
+  // before PV and their (m, lsum) are never read, so Q needs no mask.
 
   float m = -INFINITY, lsum = 0.f;
   f32x4 o[8];
 #pragma unroll
   for (int n = 0; n < 8; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // The wavefront index is uniform: spans and their block ids live in SGPRs,
+  // so the block ids of both spans come in as scalar loads before any data
+  // load is issued (a vector load here would make the second span's data
+  // wait, in-order, behind the first span's).
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int stride = W * kSpan;
-  for (int sa = s_begin + wave * kSpan; sa < s_end; sa += 2 * stride) {
+  const int last_blk = (s_end - 1) >> 4;
+  auto two_spans = [&](int sa, bool first) {
     const int sb = sa + stride;
+    const bool has_b = sb < s_end;
+    const int a_lo = table[sa >> 4];
+    const int a_hi = table[min((sa >> 4) + 1, last_blk)];
+    const int b_lo = has_b ? table[sb >> 4] : 0;
+    const int b_hi = has_b ? table[min((sb >> 4) + 1, last_blk)] : 0;
     Span ra, rb;
-    load_span(a, table, h, sa, s_end, g, j, ra);
-    if (sb < s_end) load_span(a, table, h, sb, s_end, g, j, rb);
-    attend_span(a, table, ra, qv, sa, s_end, g, j, m, lsum, o);
-    if (sb < s_end) attend_span(a, table, rb, qv, sb, s_end, g, j, m, lsum, o);
+    load_span(a, h, sa, g, j, a_lo, a_hi, ra);
+    if (has_b) load_span(a, h, sb, g, j, b_lo, b_hi, rb);
+    attend_pair(a, ra, rb, has_b, qv, sa, sb, s_end, g, j, first, m, lsum, o);
+  };
+  // The first pair is peeled out of the loop: a split of up to 2*stride tokens
+  // (512 with 8 wavefronts) then runs straight-line, with its loads issued
+  // right behind the query loads instead of after a loop-header wait.
+  const int sa0 = s_begin + wv * kSpan;
+  if (sa0 < s_end) {
+    two_spans(sa0, true);
+    for (int sa = sa0 + 2 * stride; sa < s_end; sa += 2 * stride) two_spans(sa, false);
   }
 
   // Merge the W wavefronts. Lane (g, j) holds O rows 4g..4g+3, dim 16n+j;
@@ -305,10 +361,21 @@ struct Plan {
   int nsplit, split_tokens, waves;
 };
 
+// Tuning knob: PDK_ATTN_SPLIT_BELOW (default 128) = the number of (stream, KV
+// head) workgroups below which the context is split across workgroups.
+int split_below() {
+  static const int v = [] {
+    const char* e = getenv("PDK_ATTN_SPLIT_BELOW");
+    const int x = e ? atoi(e) : 0;
+    return x > 0 ? x : 128;
+  }();
+  return v;
+}
+
 Plan plan_for(int B, int Hkv, int max_ctx) {
   const int64_t pairs = (int64_t)B * Hkv;
   int nsplit = 1;
-  if (pairs < 128) nsplit = (int)((256 + pairs - 1) / pairs);
+  if (pairs < split_below()) nsplit = (int)((2 * split_below() + pairs - 1) / pairs);
   const int max_splits = max(1, (max_ctx + 63) / 64);
   nsplit = min(min(nsplit, max_splits), kMaxSplits);
   const int split_tokens = (int)round_up((max_ctx + nsplit - 1) / nsplit, kSpan);

@@ -9,9 +9,9 @@
 // lane&7) holds tokens 8ti..8ti+7 and dims 8di..8di+7 of the tile: for every
 // load and store instruction the 64 lanes touch eight full 128-byte lines.
 //
-// Requests are batched through the kernel argument block (grid.y = request),
-// so a launch moves up to PDK_MAX_BATCH requests without any device-side
-// descriptor buffer or allocation.
+// Requests are batched through the kernel argument block: their tiles are laid
+// end to end over grid.x, so a launch moves up to PDK_MAX_BATCH requests of any
+// mix of lengths without a device-side descriptor buffer or an allocation.
 
 #include "pdk_common.h"
 
@@ -23,23 +23,39 @@ constexpr int kWaves = 4;        // wavefronts per workgroup
 constexpr int kTileT = 64;       // tokens per wavefront tile
 constexpr int kTileD = 64;       // dims per wavefront tile
 
+// Requests of a batched launch are laid end to end over grid.x: request r owns
+// wavefront tiles off[r] .. off[r+1]-1, so a launch holds only tiles with
+// work, however different the requests' lengths are.
 struct PackArgs {
   pdk_pack_req req[PDK_MAX_BATCH];
-  int S, Hkv, D, nT, nD;
-  int64_t units;                 // wavefront tiles per request
+  int64_t off[PDK_MAX_BATCH + 1];
+  int32_t nT[PDK_MAX_BATCH];     // 64-token tiles of request r
+  int n_req, S, Hkv, D, nD;
 };
+
+// Request of wavefront tile `unit` (uniform across the wavefront).
+__device__ __forceinline__ int request_of(const int64_t* off, int n_req, int64_t unit) {
+  int r = 0;
+  while (r + 1 < n_req && unit >= off[r + 1]) ++r;
+  return r;
+}
+
+__device__ __forceinline__ int64_t wave_unit() {
+  return (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
 
 // Frame layout per request: [L][2][F], F = Hkv*D*S; K frame [Hkv][D][S],
 // V frame [Hkv][S][D]; columns t >= P are zero (engines/prefill_full.py:378-379).
 __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
-  const int64_t unit = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (unit >= a.units) return;
-  const pdk_pack_req& R = a.req[blockIdx.y];
+  const int64_t unit = wave_unit();
+  if (unit >= a.off[a.n_req]) return;
+  const int r = request_of(a.off, a.n_req, unit);
+  const pdk_pack_req& R = a.req[r];
   const int lane = threadIdx.x & 63;
-  int64_t u = unit;
-  const int dt = (int)(u % a.nD); u /= a.nD;
-  const int tt = (int)(u % a.nT); u /= a.nT;
-  const int h = (int)(u % a.Hkv); u /= a.Hkv;
+  uint32_t u = (uint32_t)(unit - a.off[r]);   // tiles of one request fit 32 bits
+  const int dt = (int)(u % (uint32_t)a.nD); u /= (uint32_t)a.nD;
+  const int tt = (int)(u % (uint32_t)a.nT[r]); u /= (uint32_t)a.nT[r];
+  const int h = (int)(u % (uint32_t)a.Hkv); u /= (uint32_t)a.Hkv;
   const int l = (int)u;
   const int ti = lane >> 3, di = lane & 7;
   const int S = a.S, D = a.D, P = R.P;
@@ -78,24 +94,26 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
 
 struct ScatterArgs {
   pdk_scatter_req req[PDK_MAX_BATCH];
+  int64_t off[PDK_MAX_BATCH + 1];
+  int32_t nC[PDK_MAX_BATCH];     // 64-token chunks of request r
   uint16_t* cache_k;
   uint16_t* cache_v;
   int64_t cache_ls;              // elements between layers of the cache
-  int num_blocks, S, Hkv, D, nC, nD;
-  int64_t units;
+  int n_req, num_blocks, S, Hkv, D, nD;
 };
 
 // Frame -> paged cache. K cache block [Hkv][16][D] (token rows), V cache block
 // [Hkv][D][16] (dim rows): both need an 8x8 transpose from the frame.
 __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
-  const int64_t unit = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (unit >= a.units) return;
-  const pdk_scatter_req& R = a.req[blockIdx.y];
+  const int64_t unit = wave_unit();
+  if (unit >= a.off[a.n_req]) return;
+  const int r = request_of(a.off, a.n_req, unit);
+  const pdk_scatter_req& R = a.req[r];
   const int lane = threadIdx.x & 63;
-  int64_t u = unit;
-  const int dt = (int)(u % a.nD); u /= a.nD;
-  const int ct = (int)(u % a.nC); u /= a.nC;
-  const int h = (int)(u % a.Hkv); u /= a.Hkv;
+  uint32_t u = (uint32_t)(unit - a.off[r]);
+  const int dt = (int)(u % (uint32_t)a.nD); u /= (uint32_t)a.nD;
+  const int ct = (int)(u % (uint32_t)a.nC[r]); u /= (uint32_t)a.nC[r];
+  const int h = (int)(u % (uint32_t)a.Hkv); u /= (uint32_t)a.Hkv;
   const int l = (int)u;
   const int ti = lane >> 3, di = lane & 7;
   const int S = a.S, D = a.D, P = R.P;
@@ -147,10 +165,10 @@ __global__ __launch_bounds__(256) void gather_kernel(const GatherArgs a) {
   const int64_t unit = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (unit >= a.units) return;
   const int lane = threadIdx.x & 63;
-  int64_t u = unit;
-  const int dt = (int)(u % a.nD); u /= a.nD;
-  const int ct = (int)(u % a.nC); u /= a.nC;
-  const int h = (int)(u % a.Hkv); u /= a.Hkv;
+  uint32_t u = (uint32_t)unit;
+  const int dt = (int)(u % (uint32_t)a.nD); u /= (uint32_t)a.nD;
+  const int ct = (int)(u % (uint32_t)a.nC); u /= (uint32_t)a.nC;
+  const int h = (int)(u % (uint32_t)a.Hkv); u /= (uint32_t)a.Hkv;
   const int l = (int)u;
   const int ti = lane >> 3, di = lane & 7;
   const int S = a.S, D = a.D, P = a.P;
@@ -225,16 +243,22 @@ extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_lay
     }
     a.req[i] = r;
   }
+  a.n_req = n_reqs;
   a.S = S;
   a.Hkv = n_kv_heads;
   a.D = head_dim;
-  a.nT = (S + kTileT - 1) / kTileT;
   a.nD = head_dim / kTileD;
-  a.units = (int64_t)n_layers * n_kv_heads * a.nT * a.nD;
-  const int64_t gx = grid_x(a.units);
+  a.off[0] = 0;
+  for (int i = 0; i < n_reqs; ++i) {
+    // A narrow frame needs only the tiles that hold valid columns.
+    const int cols = (a.req[i].flags & PDK_PACK_NARROW) ? a.req[i].P : S;
+    a.nT[i] = (cols + kTileT - 1) / kTileT;
+    a.off[i + 1] = a.off[i] + (int64_t)n_layers * n_kv_heads * a.nT[i] * a.nD;
+  }
+  if (a.off[n_reqs] == 0) return PDK_OK;
+  const int64_t gx = grid_x(a.off[n_reqs]);
   PDK_REQUIRE(gx < (1ll << 31), "launch too large");
-  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)gx, (unsigned)n_reqs), dim3(256), 0,
-                     pdk::as_stream(stream), a);
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
   return pdk::check_launch("pack_kernel");
 }
 
@@ -282,16 +306,19 @@ extern "C" int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs, 
   a.cache_v = cache_v;
   a.cache_ls = cache_layer_stride;
   a.num_blocks = num_blocks;
+  a.n_req = n_reqs;
   a.S = S;
   a.Hkv = n_kv_heads;
   a.D = head_dim;
-  a.nC = (max_p + kTileT - 1) / kTileT;
   a.nD = head_dim / kTileD;
-  a.units = (int64_t)n_layers * n_kv_heads * a.nC * a.nD;
-  const int64_t gx = grid_x(a.units);
+  a.off[0] = 0;
+  for (int i = 0; i < n_reqs; ++i) {
+    a.nC[i] = (a.req[i].P + kTileT - 1) / kTileT;
+    a.off[i + 1] = a.off[i] + (int64_t)n_layers * n_kv_heads * a.nC[i] * a.nD;
+  }
+  const int64_t gx = grid_x(a.off[n_reqs]);
   PDK_REQUIRE(gx < (1ll << 31), "launch too large");
-  hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)gx, (unsigned)n_reqs), dim3(256), 0,
-                     pdk::as_stream(stream), a);
+  hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
   return pdk::check_launch("scatter_kernel");
 }
 
