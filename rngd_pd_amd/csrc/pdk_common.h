@@ -35,6 +35,21 @@ __device__ __forceinline__ void st16(uint16_t* p, const v8& v) {
   *reinterpret_cast<uint4*>(p) = make_uint4(v.w[0], v.w[1], v.w[2], v.w[3]);
 }
 
+// Streaming (non-temporal) variants: the same data movement with a hint that
+// the lines are not reused soon. Use the store for full 128-byte lines only:
+// a partial-line streaming store loses the L2's write combining.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v8 ld16_stream(const uint16_t* p) {
+  const u32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return v8{{x[0], x[1], x[2], x[3]}};
+}
+
+__device__ __forceinline__ void st16_stream(uint16_t* p, const v8& v) {
+  const u32x4_t x = {v.w[0], v.w[1], v.w[2], v.w[3]};
+  __builtin_nontemporal_store(x, reinterpret_cast<u32x4_t*>(p));
+}
+
 __device__ __forceinline__ v8 zero8() { return v8{{0u, 0u, 0u, 0u}}; }
 
 // Zero the elements e with first + e >= limit (first..first+7 are the token
