@@ -151,8 +151,9 @@ int pdk_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v,
  *          entry read is written earlier in the same call, so it needs no
  *          clearing. One workspace serves one stream at a time: calls that
  *          overlap on one workspace race.
- *   Splitting: the context is split across workgroups while B * Hkv is
- *          below PDK_ATTN_SPLIT_BELOW (environment, default 128); results
+ *   Splitting: the context is split across workgroups (splits of at least
+ *          128 tokens, about 256 workgroups in all) while B * Hkv is below
+ *          128, and for contexts of 1024 tokens or more above that; results
  *          agree with the unsplit path to fp32 rounding.
  *   out    [B][Hq][D] bf16
  * Requires D == 128, Hq/Hkv in {1, 2, 4, 8, 16}, max_ctx <= 16384.

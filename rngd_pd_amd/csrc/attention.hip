@@ -32,6 +32,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "pdk_common.h"
 
 namespace {
@@ -46,6 +48,10 @@ constexpr int kMaxWaves = 8;
 constexpr int kSpan = 32;        // tokens per span
 constexpr int kMaxG = 16;
 constexpr int kMaxSplits = 32;
+// LDS row stride of the wavefront merge: kD + 4 puts lane groups g and g+1
+// (rows 4 apart) on different banks.
+constexpr int kOStride = kD + 4;
+constexpr int kMergeRows = 8;     // query rows merged per LDS pass
 
 __device__ __forceinline__ bf16x8_t as_bf(const v8& v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -178,14 +184,14 @@ __device__ __forceinline__ void attend_pair(const AttnArgs& a, Span& ra, Span& r
   float p[16], ps = 0.f;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    p[e] = exp2f(sc[e] - m_new);
+    p[e] = __builtin_amdgcn_exp2f(sc[e] - m_new);   // argument <= 0; exp2(-inf) = 0
     ps += p[e];
   }
   ps = column_sum(ps);
   if (first) {
     lsum = ps;
   } else {
-    const float alpha = exp2f(m - m_new);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
     lsum = lsum * alpha + ps;
     float ar[4];
 #pragma unroll
@@ -204,7 +210,7 @@ __device__ __forceinline__ void attend_pair(const AttnArgs& a, Span& ra, Span& r
 __global__ __launch_bounds__(512) void decode_attn_kernel(const AttnArgs a) {
   __shared__ float sm_m[kMaxWaves][kMaxG];
   __shared__ float sm_l[kMaxWaves][kMaxG];
-  __shared__ float sm_o[kMaxWaves][4][kD];      // rows of the group, 4 at a time
+  extern __shared__ float sm_o[];                // [W][min(G, kMergeRows)][kOStride]
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int W = blockDim.x >> 6;
@@ -256,42 +262,53 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(const AttnArgs a) {
     for (int sa = sa0 + 2 * stride; sa < s_end; sa += 2 * stride) two_spans(sa, false);
   }
 
-  // Merge the W wavefronts. Lane (g, j) holds O rows 4g..4g+3, dim 16n+j;
-  // rows go through LDS four at a time (one lane group g per pass).
+  // Merge the W wavefronts through LDS, one barrier per 8 query rows. Lane (g, j) holds
+  // O rows 4g..4g+3 (the group's query heads), dims 16n+j; the four lanes of
+  // column j hold the same (m, lsum). The combine reads all kMaxWaves slots
+  // unconditionally (in flight together) and drops slots w >= W by select:
+  // with a runtime trip count each read would wait for the one before it.
   if (g == 0 && j < G) {
     sm_m[wave][j] = m;
     sm_l[wave][j] = lsum;
   }
+  const int R = min(G, kMergeRows);              // rows per pass; one pass for G <= 8
   const int64_t bq0 = (int64_t)b * a.Hq + h * G;
-  for (int gg = 0; 4 * gg < G; ++gg) {
-    __syncthreads();                             // sm_m/sm_l written; sm_o free
-    if (g == gg) {
+  for (int r0 = 0; r0 < G; r0 += R) {
+    if (r0 > 0) __syncthreads();                 // the previous pass has read sm_o
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * g + i - r0;
+      if (row >= 0 && row < R && row + r0 < G) {
 #pragma unroll
-        for (int n = 0; n < 8; ++n) sm_o[wave][i][16 * n + j] = o[n][i];
+        for (int n = 0; n < 8; ++n) sm_o[(wave * R + row) * kOStride + 16 * n + j] = o[n][i];
+      }
     }
     __syncthreads();
-    const int rows = min(4, G - 4 * gg);
-    for (int idx = threadIdx.x; idx < rows * kD; idx += blockDim.x) {
-      const int i = idx / kD, d = idx - i * kD;
-      const int row = 4 * gg + i;
-      float M = -INFINITY;
-      for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w][row]);
-      float L = 0.f, O = 0.f;
-      if (M != -INFINITY) {
-        for (int w = 0; w < W; ++w) {
-          const float mw = sm_m[w][row];
-          if (mw != -INFINITY) {
-            const float c = exp2f(mw - M);
-            L += sm_l[w][row] * c;
-            O += sm_o[w][i][d] * c;
-          }
-        }
+    for (int idx = threadIdx.x; idx < R * kD; idx += blockDim.x) {
+      const int row = idx / kD, d = idx - row * kD;
+      float mw[kMaxWaves], M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kMaxWaves; ++w) {
+        const float x = sm_m[w][r0 + row];
+        mw[w] = w < W ? x : -INFINITY;
+        M = fmaxf(M, mw[w]);
       }
-      const int64_t bq = bq0 + row;
+      float L = 0.f, O = 0.f;
+#pragma unroll
+      for (int w = 0; w < kMaxWaves; ++w) {
+        const int wc = min(w, W - 1);            // slots past W read a live row, then drop it
+        const float lw = sm_l[w][r0 + row], ow = sm_o[(wc * R + row) * kOStride + d];
+        // exp2 of a non-positive argument; a wavefront without tokens (m = -inf)
+        // or an unused slot contributes nothing, also when M itself is -inf.
+        const bool live = mw[w] != -INFINITY;
+        const float c = live ? __builtin_amdgcn_exp2f(mw[w] - M) : 0.f;
+        L += live ? lw * c : 0.f;
+        O += live ? ow * c : 0.f;
+      }
+      const int64_t bq = bq0 + r0 + row;
       if (a.nsplit == 1) {
-        a.out[bq * kD + d] = (uint16_t)pdk::f32_to_bf16_rne(L > 0.f ? O / L : 0.f);
+        const float inv = L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
+        a.out[bq * kD + d] = (uint16_t)pdk::f32_to_bf16_rne(O * inv);
       } else {
         a.ws_o[(bq * a.nsplit + split) * kD + d] = O;
         if (d == 0) {
@@ -326,13 +343,13 @@ __global__ __launch_bounds__(128) void merge_kernel(const float* ws_ml, const fl
 #pragma unroll
     for (int s = 0; s < kMaxSplits; ++s) {
       if (s < nsplit && mv[s] != -INFINITY) {
-        const float c = exp2f(mv[s] - M);
+        const float c = __builtin_amdgcn_exp2f(mv[s] - M);   // argument <= 0
         L += lv[s] * c;
         O += ov[s] * c;
       }
     }
   }
-  out[bq * kD + d] = (uint16_t)pdk::f32_to_bf16_rne(L > 0.f ? O / L : 0.f);
+  out[bq * kD + d] = (uint16_t)pdk::f32_to_bf16_rne(L > 0.f ? O * __builtin_amdgcn_rcpf(L) : 0.f);
 }
 
 // New token's k/v into slot ctx[b]-1 (kernels/decode_batch.py:81-82 as a store).
@@ -354,34 +371,31 @@ __global__ void cache_append_kernel(const uint16_t* k_new, const uint16_t* v_new
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-// Launch plan: one split once B*Hkv workgroups reach 128 (each up to 8
-// wavefronts = 512 tokens in flight); below that, enough splits for ~256
-// workgroups, each at least 64 tokens.
+// Launch plan. One workgroup per (stream, KV head, split), up to 8
+// wavefronts of 64 tokens each in flight. The context is split across
+// workgroups until about 256 of them (one per CU) exist, in splits of at least
+// 128 tokens; once B*Hkv alone reaches 128 workgroups, only contexts of 1024
+// tokens or more are split, because below that the partial-result merge (an
+// extra launch) costs more than the CUs gained. Measured per layer on MI355X,
+// Hq=32, Hkv=8, cold cache: B=16 ctx 512 one split 10.5 us vs two 11.7 us;
+// B=16 ctx 2048 two splits 28.9 us vs one 32.3 us; B=4 ctx 512 four splits
+// 8.2 us vs eight 9.0 us.
 struct Plan {
   int nsplit, split_tokens, waves;
 };
 
-// Tuning knob: PDK_ATTN_SPLIT_BELOW (default 128) = the number of (stream, KV
-// head) workgroups below which the context is split across workgroups.
-int split_below() {
-  static const int v = [] {
-    const char* e = getenv("PDK_ATTN_SPLIT_BELOW");
-    const int x = e ? atoi(e) : 0;
-    return x > 0 ? x : 128;
-  }();
-  return v;
-}
+constexpr int kTargetWorkgroups = 256;
 
 Plan plan_for(int B, int Hkv, int max_ctx) {
   const int64_t pairs = (int64_t)B * Hkv;
-  int nsplit = 1;
-  if (pairs < split_below()) nsplit = (int)((2 * split_below() + pairs - 1) / pairs);
-  const int max_splits = max(1, (max_ctx + 63) / 64);
-  nsplit = min(min(nsplit, max_splits), kMaxSplits);
+  const int min_split = pairs >= 128 ? 1024 : 128;
+  int64_t nsplit = (kTargetWorkgroups + pairs - 1) / pairs;
+  nsplit = std::min<int64_t>(nsplit, (max_ctx + min_split - 1) / min_split);
+  nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, kMaxSplits));
   const int split_tokens = (int)round_up((max_ctx + nsplit - 1) / nsplit, kSpan);
-  nsplit = (max_ctx + split_tokens - 1) / split_tokens;
+  const int ns = (max_ctx + split_tokens - 1) / split_tokens;
   const int waves = max(1, min(kMaxWaves, (split_tokens + 2 * kSpan - 1) / (2 * kSpan)));
-  return {nsplit, split_tokens, waves};
+  return {ns, split_tokens, waves};
 }
 
 size_t ws_bytes(int B, int Hq, int nsplit) {
@@ -395,7 +409,7 @@ size_t ws_bytes(int B, int Hq, int nsplit) {
 extern "C" size_t pdk_decode_attn_workspace_bytes(int B, int n_q_heads, int max_ctx, int head_dim) {
   if (B <= 0 || n_q_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return 0;
   // The most splits a plan uses for any n_kv_heads <= n_q_heads.
-  return ws_bytes(B, n_q_heads, min(kMaxSplits, max(1, (max_ctx + 63) / 64)));
+  return ws_bytes(B, n_q_heads, min(kMaxSplits, max(1, (max_ctx + 127) / 128)));
 }
 
 extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
@@ -450,7 +464,8 @@ extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const
     a.ws_o = reinterpret_cast<float*>(base + round_up(bq * p.nsplit * 2 * 4, 256));
   }
   hipStream_t st = pdk::as_stream(stream);
-  hipLaunchKernelGGL(decode_attn_kernel, dim3(p.nsplit, n_kv_heads, B), dim3(64 * p.waves), 0, st,
+  const size_t lds = (size_t)p.waves * min(G, kMergeRows) * kOStride * sizeof(float);
+  hipLaunchKernelGGL(decode_attn_kernel, dim3(p.nsplit, n_kv_heads, B), dim3(64 * p.waves), lds, st,
                      a);
   int rc = pdk::check_launch("decode_attn_kernel");
   if (rc || p.nsplit == 1) return rc;
