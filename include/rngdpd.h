@@ -17,10 +17,18 @@
  *                             then the V frame [Hkv][S][D], columns >= P zero.
  *                             This is byte for byte the bf16 payload of the
  *                             reference's shm wire for one layer's (k, v).
- *   paged decode cache        K [L][num_blocks][Hkv][16][D]   (token rows)
+ *   paged decode cache        K [L][num_blocks][Hkv][16*D]    (tiled, below)
  *                             V [L][num_blocks][Hkv][D][16]   (dim rows)
  *                             block table int32 [n_table], block j holds
- *                             tokens 16j .. 16j+15 of the request
+ *                             tokens 16j .. 16j+15 of the request.
+ *                             A K block is 16-byte units of 8 consecutive
+ *                             dims of one token; token `slot` (0..15), dims
+ *                             d0..d0+7 (d0 % 8 == 0) is unit
+ *                               ((t*(D/32) + d0/32)*4 + (d0/8)%4)*8 + j8,
+ *                             t = (slot>>2)&1, j8 = (slot>>3)*4 + (slot&3):
+ *                             the order decode attention's QK tiles read, so
+ *                             each of those loads covers whole 128-byte lines.
+ *                             D % 32 == 0.
  *
  * Reference citations are file:line in ai-computing/rngd-pd.
  */

@@ -33,18 +33,52 @@ def cpu_attention(q, K, V, positions, k_new=None, v_new=None):
     return np.einsum("bkgs,bksh->bkgh", p, V).reshape(B, NH, HD)
 
 
+def k_block_index(D):
+    """int64 [16, D]: element offset of (token slot, dim) inside one K block of
+    the paged cache (16 tokens x D dims, D % 32 == 0).
+
+    The block is 16-byte units of 8 consecutive dims of one token; the unit of
+    (slot, d // 8) is ((t * (D // 32) + d // 32) * 4 + (d // 8) % 4) * 8 + j8
+    with t = (slot >> 2) & 1 and j8 = (slot >> 3) * 4 + (slot & 3). This is a
+    layout of this build, not of the reference (whose decode K is dense
+    [nl, B, NKV, HD, S], engines/decode_batch.py:305-330)."""
+    if D % 32:
+        raise ValueError(f"head_dim {D} is not a multiple of 32")
+    slot = np.arange(16)[:, None]
+    d = np.arange(D)[None, :]
+    t = (slot >> 2) & 1
+    j8 = (slot >> 3) * 4 + (slot & 3)
+    unit = ((t * (D // 32) + d // 32) * 4 + (d // 8) % 4) * 8 + j8
+    return (unit * 8 + d % 8).astype(np.int64)
+
+
+def k_block_rows(ck):
+    """Paged K blocks [..., 16, D] (tiled) -> token rows [..., 16, D]."""
+    D = ck.shape[-1]
+    flat = np.ascontiguousarray(ck).reshape(ck.shape[:-2] + (16 * D,))
+    return flat[..., k_block_index(D)]
+
+
+def k_block_tiled(rows):
+    """Token rows [..., 16, D] -> paged K blocks [..., 16, D] (tiled)."""
+    D = rows.shape[-1]
+    out = np.empty(rows.shape[:-2] + (16 * D,), rows.dtype)
+    out[..., k_block_index(D)] = rows
+    return out.reshape(rows.shape)
+
+
 def paged_from_dense(K, V, ctx, tables, num_blocks, bs=16):
     """Dense per-stream caches -> one layer of the paged cache.
 
     K [B, H, D, S], V [B, H, S, D] (any dtype); tables int [B, max_blocks].
-    Returns cache_k [nb, H, bs, D], cache_v [nb, H, D, bs] holding tokens
-    0..ctx[b]-1 of each stream (zeros elsewhere)."""
+    Returns cache_k [nb, H, bs, D] (tiled blocks, k_block_index), cache_v
+    [nb, H, D, bs] holding tokens 0..ctx[b]-1 of each stream (zeros elsewhere)."""
     B, H, D, S = K.shape
-    ck = np.zeros((num_blocks, H, bs, D), K.dtype)
+    rows = np.zeros((num_blocks, H, bs, D), K.dtype)
     cv = np.zeros((num_blocks, H, D, bs), V.dtype)
     for b in range(B):
         for t in range(ctx[b]):
             blk, slot = tables[b][t // bs], t % bs
-            ck[blk, :, slot, :] = K[b, :, :, t]
+            rows[blk, :, slot, :] = K[b, :, :, t]
             cv[blk, :, :, slot] = V[b, :, t, :]
-    return ck, cv
+    return k_block_tiled(rows), cv

@@ -64,13 +64,25 @@ int orc_pack_kv(const uint16_t* src_k, const uint16_t* src_v, int64_t layer_stri
   return 0;
 }
 
+/* Element offset, inside one (block, KV head) K block of 16*D values, of
+ * token `slot` (0..15) and dim d. The block is 16-byte units of 8 dims of one
+ * token in tiled order: the unit of (slot, d/8) is
+ * ((t*(D/32) + d/32)*4 + (d/8)%4)*8 + j8, t = (slot>>2)&1,
+ * j8 = (slot>>3)*4 + (slot&3). A layout of this build (the reference keeps
+ * dense per-stream K, engines/decode_batch.py:305-330). Needs D % 32 == 0. */
+static int64_t k_index(int slot, int d, int D) {
+  const int t = (slot >> 2) & 1, j8 = ((slot >> 3) << 2) | (slot & 3);
+  const int64_t unit = ((int64_t)(t * (D / 32) + d / 32) * 4 + (d / 8) % 4) * 8 + j8;
+  return unit * 8 + d % 8;
+}
+
 /* Decode-side placement of a delivered frame (connector/rngd_kv.py:160-165)
  * into a paged cache: token t of the request goes to block table[t/16],
  * slot t%16; slots >= P of the last block are zero. */
 int orc_scatter_paged(const uint16_t* frame, const int32_t* table, int n_table, int L, int P,
                       int S, int Hkv, int D, uint16_t* cache_k, uint16_t* cache_v,
                       int64_t cache_ls, int num_blocks) {
-  if (P < 0 || P > S || n_table < (P + BS - 1) / BS) return -22;
+  if (P < 0 || P > S || n_table < (P + BS - 1) / BS || D % 32 != 0) return -22;
   const int64_t F = (int64_t)Hkv * D * S;
   for (int j = 0; j < (P + BS - 1) / BS; ++j) {
     const int blk = table[j];
@@ -84,7 +96,7 @@ int orc_scatter_paged(const uint16_t* frame, const int32_t* table, int n_table, 
           for (int d = 0; d < D; ++d) {
             const uint16_t k = t < P ? fk[((int64_t)h * D + d) * S + t] : 0;
             const uint16_t v = t < P ? fv[((int64_t)h * S + t) * D + d] : 0;
-            cache_k[(int64_t)l * cache_ls + (((int64_t)blk * Hkv + h) * BS + slot) * D + d] = k;
+            cache_k[(int64_t)l * cache_ls + ((int64_t)blk * Hkv + h) * BS * D + k_index(slot, d, D)] = k;
             cache_v[(int64_t)l * cache_ls + (((int64_t)blk * Hkv + h) * D + d) * BS + slot] = v;
           }
         }
@@ -97,7 +109,7 @@ int orc_scatter_paged(const uint16_t* frame, const int32_t* table, int n_table, 
 int orc_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v, int64_t cache_ls,
                      int num_blocks, const int32_t* table, int n_table, int L, int P, int S,
                      int Hkv, int D, uint16_t* frame) {
-  if (P < 0 || P > S || n_table < (P + BS - 1) / BS) return -22;
+  if (P < 0 || P > S || n_table < (P + BS - 1) / BS || D % 32 != 0) return -22;
   const int64_t F = (int64_t)Hkv * D * S;
   memset(frame, 0, (size_t)L * 2 * F * sizeof(uint16_t));
   for (int l = 0; l < L; ++l) {
@@ -110,7 +122,7 @@ int orc_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v, int64_t c
       for (int h = 0; h < Hkv; ++h)
         for (int d = 0; d < D; ++d) {
           fk[((int64_t)h * D + d) * S + t] =
-              cache_k[(int64_t)l * cache_ls + (((int64_t)blk * Hkv + h) * BS + slot) * D + d];
+              cache_k[(int64_t)l * cache_ls + ((int64_t)blk * Hkv + h) * BS * D + k_index(slot, d, D)];
           fv[((int64_t)h * S + t) * D + d] =
               cache_v[(int64_t)l * cache_ls + (((int64_t)blk * Hkv + h) * D + d) * BS + slot];
         }
@@ -124,6 +136,7 @@ int orc_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v, int64_t c
 int orc_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* cache_k,
                      uint16_t* cache_v, int num_blocks, const int32_t* tables, int max_blocks,
                      const int32_t* ctx, int B, int Hkv, int D) {
+  if (D % 32 != 0) return -22;
   for (int b = 0; b < B; ++b) {
     const int t = ctx[b] - 1;
     if (t < 0 || t >= max_blocks * BS) continue;
@@ -132,7 +145,7 @@ int orc_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* cac
     for (int h = 0; h < Hkv; ++h)
       for (int d = 0; d < D; ++d) {
         const int64_t s = ((int64_t)b * Hkv + h) * D + d;
-        cache_k[(((int64_t)blk * Hkv + h) * BS + t % BS) * D + d] = k_new[s];
+        cache_k[((int64_t)blk * Hkv + h) * BS * D + k_index(t % BS, d, D)] = k_new[s];
         cache_v[(((int64_t)blk * Hkv + h) * D + d) * BS + t % BS] = v_new[s];
       }
   }
@@ -147,7 +160,7 @@ int orc_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* cac
 int orc_decode_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
                     int num_blocks, const int32_t* tables, int max_blocks, const int32_t* ctx,
                     int B, int Hq, int Hkv, int D, float scale, float* out) {
-  if (Hq % Hkv != 0) return -22;
+  if (Hq % Hkv != 0 || D % 32 != 0) return -22;
   const int G = Hq / Hkv;
   double* sc = (double*)malloc(sizeof(double) * (size_t)max_blocks * BS);
   if (!sc) return -12;
@@ -163,8 +176,8 @@ int orc_decode_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* 
         const int blk = tables[(int64_t)b * max_blocks + t / BS];
         double s = 0.0;
         if (blk >= 0 && blk < num_blocks) {
-          const uint16_t* kp = cache_k + (((int64_t)blk * Hkv + h) * BS + t % BS) * D;
-          for (int d = 0; d < D; ++d) s += (double)widen(qp[d]) * (double)widen(kp[d]);
+          const uint16_t* kb = cache_k + ((int64_t)blk * Hkv + h) * BS * D;
+          for (int d = 0; d < D; ++d) s += (double)widen(qp[d]) * (double)widen(kb[k_index(t % BS, d, D)]);
         }
         sc[t] = s * scale;
         if (sc[t] > mx) mx = sc[t];

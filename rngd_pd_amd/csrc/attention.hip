@@ -16,12 +16,13 @@
 //   4. PV: 8 v_mfma_f32_16x16x32_bf16 (one per 16-dim tile), A = P straight
 //      from the QK accumulators, B = V.
 // MFMA multiplies along the 8 contiguous elements a lane holds, so the cache
-// keeps K token-major ([blk][h][16][D]: a lane's 8 dims are 16 contiguous
-// bytes) and V dim-major ([blk][h][D][16]: a lane's 8 tokens are 16 contiguous
-// bytes). The reduction index of each product is permuted identically on both
-// operands (dims in QK, tokens in PV), which leaves the sums unchanged:
-//   QK  k-step s, lane group g, element e  <->  dim s*32 + g*8 + e
-//       (the four lanes of one token row read 64 contiguous bytes per step);
+// keeps K as 16-byte units of 8 dims of one token, tiled in the order the QK
+// tiles read them (pdk::k_unit: one K load instruction reads 512 contiguous
+// bytes of each of its two blocks), and V dim-major ([blk][h][D][16]: a
+// lane's 8 tokens are 16 contiguous bytes). The reduction index of each
+// product is permuted identically on both operands (dims in QK, tokens in
+// PV), which leaves the sums unchanged:
+//   QK  k-step s, lane group g, element e  <->  dim s*32 + g*8 + e;
 //   QK  tile 0 row r <-> token 8(r/4) + r%4, tile 1 row r <-> that + 4, so a
 //       lane's two accumulators hold tokens 8g..8g+7 of the span: exactly the
 //       A-operand row segment PV needs.
@@ -85,21 +86,23 @@ struct Span {
 // afterwards, K of such tokens needs nothing (their scores become -inf).
 __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, int g, int j,
                                           int blk_lo, int blk_hi, Span& r) {
-  const int tau0 = 8 * (j >> 2) + (j & 3);      // QK tile-0 row j -> token offset
-  const int ta = span + tau0, tb = ta + 4;      // both in blk_lo iff j < 8
+  // QK tile 0 row j is token span + 8(j/4) + j%4 and tile 1 row j that token
+  // + 4: slots (j%8 -> j8 = j%8) of blk_lo for j < 8, of blk_hi otherwise. In
+  // the tiled K block (pdk::k_unit) lanes j%8 = 0..7 of one dim group g read
+  // one 128-byte line, and the four groups g four consecutive lines.
   const int tv = span + 8 * g;                   // this lane's 8 V tokens; blk_lo iff g < 2
   const int bk = (j < 8) ? blk_lo : blk_hi;
   const int bv = (g < 2) ? blk_lo : blk_hi;
   const int cbk = (bk >= 0 && bk < a.num_blocks) ? bk : 0;
   r.v_ok = bv >= 0 && bv < a.num_blocks;
   const int cbv = r.v_ok ? bv : 0;
-  const uint16_t* pa = a.ck + (((int64_t)cbk * a.Hkv + h) * 16 + (ta & 15)) * kD + g * 8;
-  const uint16_t* pb = a.ck + (((int64_t)cbk * a.Hkv + h) * 16 + (tb & 15)) * kD + g * 8;
+  const uint16_t* pk = a.ck + ((int64_t)cbk * a.Hkv + h) * 16 * kD + (g * 8 + (j & 7)) * 8;
   const uint16_t* pv = a.cv + ((int64_t)cbv * a.Hkv + h) * kD * 16 + (tv & 15) + j * 16;
+  // unit(t, s) = ((t * 4 + s) * 4 + g) * 8 + j8 with kD / 32 = 4 dim groups per tile
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    r.ka[s] = pdk::ld16(pa + 32 * s);
-    r.kb[s] = pdk::ld16(pb + 32 * s);
+    r.ka[s] = pdk::ld16(pk + (s * 4 * 8) * 8);
+    r.kb[s] = pdk::ld16(pk + ((4 + s) * 4 * 8) * 8);
   }
 #pragma unroll
   for (int n = 0; n < 8; ++n) r.vf[n] = pdk::ld16(pv + 16 * 16 * n);
@@ -362,9 +365,10 @@ __global__ void cache_append_kernel(const uint16_t* k_new, const uint16_t* v_new
   const int blk = tables[(int64_t)b * max_blocks + (t >> 4)];
   if (blk < 0 || blk >= num_blocks) return;
   const int slot = t & 15;
+  uint16_t* kb = ck + ((int64_t)blk * Hkv + h) * 16 * D;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     const int64_t src = ((int64_t)b * Hkv + h) * D + d;
-    ck[(((int64_t)blk * Hkv + h) * 16 + slot) * D + d] = k_new[src];
+    kb[pdk::k_unit(slot, d & ~7, D) * 8 + (d & 7)] = k_new[src];
     cv[(((int64_t)blk * Hkv + h) * D + d) * 16 + slot] = v_new[src];
   }
 }
@@ -483,7 +487,8 @@ extern "C" int pdk_cache_append(const uint16_t* k_new, const uint16_t* v_new, ui
               "null pointer argument");
   PDK_REQUIRE(B >= 1 && B <= 65535 && n_kv_heads >= 1 && n_kv_heads <= 65535,
               "B/n_kv_heads out of range");
-  PDK_REQUIRE(head_dim >= 1 && head_dim <= 4096, "head_dim out of range");
+  PDK_REQUIRE(head_dim >= 32 && head_dim % 32 == 0 && head_dim <= 4096,
+              "head_dim must be a multiple of 32 in [32, 4096] (got %d)", head_dim);
   PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1, "num_blocks and max_blocks must be >= 1");
   hipLaunchKernelGGL(cache_append_kernel, dim3(B, n_kv_heads), dim3(128), 0,
                      pdk::as_stream(stream), k_new, v_new, cache_k, cache_v, num_blocks,

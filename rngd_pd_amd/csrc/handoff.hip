@@ -110,8 +110,9 @@ struct ScatterArgs {
   int n_req, num_blocks, S, Hkv, D, nD;
 };
 
-// Frame -> paged cache. K cache block [Hkv][16][D] (token rows), V cache block
-// [Hkv][D][16] (dim rows): both need an 8x8 transpose from the frame.
+// Frame -> paged cache. K cache block [Hkv][16 x D] in the tiled token order of
+// pdk::k_unit (8 dims of one token per 16-byte unit), V cache block [Hkv][D][16]
+// (dim rows): both need an 8x8 transpose from the frame.
 __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
   const int64_t unit = wave_unit();
   if (unit >= a.off[a.n_req]) return;
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
   uint16_t* cv = a.cache_v + (int64_t)l * a.cache_ls + ((int64_t)blk * a.Hkv + h) * D * 16;
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    pdk::st16(ck + (int64_t)(slot0 + c) * D + d0, kout[c]);
+    pdk::st16(ck + (int64_t)pdk::k_unit(slot0 + c, d0, D) * 8, kout[c]);
     pdk::st16(cv + (int64_t)(d0 + c) * 16 + slot0, vout[c]);
   }
 }
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const GatherArgs a) {
   v8 kin[8], vin[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
-    kin[r] = pdk::ld16(ck + (int64_t)(slot0 + r) * D + d0);
+    kin[r] = pdk::ld16(ck + (int64_t)pdk::k_unit(slot0 + r, d0, D) * 8);
     vin[r] = pdk::ld16(cv + (int64_t)(d0 + r) * 16 + slot0);
   }
 #pragma unroll

@@ -52,6 +52,21 @@ __device__ __forceinline__ void st16_stream(uint16_t* p, const v8& v) {
 
 __device__ __forceinline__ v8 zero8() { return v8{{0u, 0u, 0u, 0u}}; }
 
+// Paged K-cache block layout. One (block, KV head) holds 16 tokens x D dims of
+// bf16 (D % 32 == 0) as 16-byte units of 8 consecutive dims of one token, in
+// the order the decode-attention QK tiles read them, so that each of those
+// load instructions reads whole 128-byte lines. The unit of token `slot`
+// (0..15) and dims d0..d0+7 (d0 % 8 == 0) is
+//   ((t * (D / 32) + s) * 4 + g) * 8 + j8,
+//   t = (slot >> 2) & 1,  j8 = (slot >> 3) * 4 + (slot & 3),
+//   s = d0 / 32,          g = (d0 / 8) % 4.
+// Tile t holds the 8 tokens whose slot has bit 2 equal to t; within it, the
+// 8 tokens of one 8-dim group are contiguous (128 bytes).
+__host__ __device__ __forceinline__ int k_unit(int slot, int d0, int D) {
+  const int t = (slot >> 2) & 1, j8 = ((slot >> 3) << 2) | (slot & 3);
+  return ((t * (D >> 5) + (d0 >> 5)) * 4 + ((d0 >> 3) & 3)) * 8 + j8;
+}
+
 // Zero the elements e with first + e >= limit (first..first+7 are the token
 // indices of the 8 elements).
 __device__ __forceinline__ void mask_tail(v8& v, int first, int limit) {

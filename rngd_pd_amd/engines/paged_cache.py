@@ -6,9 +6,11 @@ blocks shared by every request: a request holds ceil(tokens/16) blocks in any
 order, listed in its block table (the same table for every layer). Capacity
 is then set by HBM, not by a compiled S.
 
-Layout (bf16): K [L, num_blocks, Hkv, 16, D] (token rows, contiguous head_dim)
-and V [L, num_blocks, Hkv, D, 16] (dim rows, contiguous tokens): the operand
-orders the decode-attention MFMA tiles read directly.
+Layout (bf16): K [L, num_blocks, Hkv, 16, D] and V [L, num_blocks, Hkv, D, 16]
+(dim rows, contiguous tokens). A K block holds its 16 tokens x D dims as
+16-byte units of 8 dims of one token, tiled in the order the decode-attention
+QK tiles read them (k_block_index); V is already in the order the PV tiles
+read. k_block_rows / k_block_tiled convert K blocks to and from token rows.
 """
 import threading
 
@@ -18,6 +20,36 @@ import torch
 from ..kernels import handoff as _h
 
 BLOCK = 16
+
+
+def k_block_index(head_dim, device=None):
+    """int64 [16, head_dim]: position of (token slot, dim) inside one K block.
+
+    Unit (16 bytes, 8 dims) of slot s and dims d0..d0+7 is
+    ((t * head_dim/32 + d0/32) * 4 + (d0/8) % 4) * 8 + j8 with t = bit 2 of s
+    and j8 = (s // 8) * 4 + s % 4 -- the order of rngdpd.h's paged cache."""
+    if head_dim % 32:
+        raise ValueError(f"head_dim {head_dim} is not a multiple of 32")
+    s = torch.arange(BLOCK, device=device).view(BLOCK, 1)
+    d = torch.arange(head_dim, device=device).view(1, head_dim)
+    unit = ((((s >> 2) & 1) * (head_dim // 32) + d // 32) * 4 + (d // 8) % 4) * 8 \
+        + (s >> 3) * 4 + (s & 3)
+    return unit * 8 + d % 8
+
+
+def k_block_rows(blocks):
+    """K blocks [..., 16, D] in cache order -> token rows [..., 16, D]."""
+    D = blocks.shape[-1]
+    flat = blocks.reshape(*blocks.shape[:-2], BLOCK * D)
+    return flat[..., k_block_index(D, blocks.device)]
+
+
+def k_block_tiled(rows):
+    """Token rows [..., 16, D] -> K blocks [..., 16, D] in cache order."""
+    D = rows.shape[-1]
+    out = torch.empty(*rows.shape[:-2], BLOCK * D, dtype=rows.dtype, device=rows.device)
+    out[..., k_block_index(D, rows.device).reshape(-1)] = rows.reshape(*rows.shape[:-2], BLOCK * D)
+    return out.view(rows.shape)
 
 
 class BlockAllocator:

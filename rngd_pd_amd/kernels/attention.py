@@ -51,7 +51,7 @@ def decode_attention(q, cache_k, cache_v, block_tables, ctx_lens, max_ctx, scale
     """GQA decode attention for one layer.
 
     q [B, Hq, D] bf16 (query head h reads KV head h // (Hq/Hkv)); cache_k
-    [nb, Hkv, 16, D], cache_v [nb, Hkv, D, 16]; block_tables int32 [B, max_blocks]
+    [nb, Hkv, 16, D] (tiled K blocks), cache_v [nb, Hkv, D, 16]; block_tables int32 [B, max_blocks]
     and ctx_lens int32 [B] on the device; ``max_ctx`` >= every ctx_lens[b]."""
     _need(q, "q")
     nb, H, D = _check_layer_cache(cache_k, cache_v)

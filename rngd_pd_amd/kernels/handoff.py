@@ -7,7 +7,10 @@ Shapes (bf16 CUDA tensors):
   frame        [L, 2, Hkv*D*S]: per layer the K frame [Hkv, D, S] then the V
                frame [Hkv, S, D], columns >= P zero -- the bf16 payload the
                reference's ser() writes for that layer (connector/transport.py:29-37).
-  paged cache  cache_k [L, nb, Hkv, 16, D], cache_v [L, nb, Hkv, D, 16].
+  paged cache  cache_k [L, nb, Hkv, 16, D], cache_v [L, nb, Hkv, D, 16]. A K block's
+               16*D values are in the tiled token order of the C header (16-byte
+               units of 8 dims of one token, ordered for the attention's QK reads);
+               engines.paged_cache.k_block_rows converts a block to token rows.
 """
 import ctypes
 

@@ -5,11 +5,16 @@
                       of tests/test_airm.py:169 (seed 1, shape (2, 2, 4, 2, 8)),
                       as written by numpy 2.x.
   attention_small.npz one decode-attention case (B=2, Hq=8, Hkv=2, D=32,
-                      ctx 19 and 40, permuted blocks) and its float32 output.
+                      ctx 19 and 40, permuted block tables) as dense per-stream
+                      K [B, Hkv, D, S] / V [B, Hkv, S, D] bf16 bits, and its
+                      output from oracle.attention.cpu_attention (the numpy
+                      restatement of cpu_layer, kernels/decode_batch.py:147-156)
+                      evaluated in float64.
 
-Inputs come from numpy generators; the outputs from the CPU oracle, whose
-functions are pinned independently in tests/test_oracle.py. The fixtures then
-pin the oracle (and the numpy pickle envelope) against silent drift.
+Inputs come from numpy generators. The wire blobs come from the oracle's
+pickle restatement; the attention output does not depend on the paged-cache
+layout, so the test that reads it pins the C oracle's paged attention against
+the dense reference formula.
 """
 import math
 import os
@@ -20,7 +25,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
-from oracle import native as orc  # noqa: E402
+from oracle import attention as oatt  # noqa: E402
 from oracle import wire as owire  # noqa: E402
 
 
@@ -32,7 +37,7 @@ def main():
              adapter_in=adapter, adapter_blob=np.frombuffer(owire.ser(adapter, "bf16"), np.uint8))
 
     rng = np.random.default_rng(11)
-    B, Hq, H, D = 2, 8, 2, 32
+    B, Hq, H, D, S = 2, 8, 2, 32, 48
     ctx = np.array([19, 40], np.int32)
     nb = 7
     tables = np.full((B, 3), -1, np.int32)
@@ -41,11 +46,11 @@ def main():
     tables[1, :3] = perm[2:5]
     bits = lambda shape: (rng.standard_normal(shape).astype(np.float32).view(np.uint32)  # noqa: E731
                           >> 16).astype(np.uint16)
-    ck, cv, q = bits((nb, H, 16, D)), bits((nb, H, D, 16)), bits((B, Hq, D))
-    scale = 1 / math.sqrt(D)
-    out = orc.decode_attn(q, ck, cv, tables, ctx, scale)
-    np.savez(os.path.join(HERE, "attention_small.npz"), q=q, ck=ck, cv=cv, tables=tables,
-             ctx=ctx, scale=np.float32(scale), out=out)
+    k_dense, v_dense, q = bits((B, H, D, S)), bits((B, H, S, D)), bits((B, Hq, D))
+    wide = lambda u: (u.astype(np.uint32) << 16).view(np.float32).astype(np.float64)  # noqa: E731
+    out = oatt.cpu_attention(wide(q), wide(k_dense), wide(v_dense), ctx - 1).astype(np.float32)
+    np.savez(os.path.join(HERE, "attention_small.npz"), q=q, k_dense=k_dense, v_dense=v_dense,
+             tables=tables, ctx=ctx, scale=np.float32(1 / math.sqrt(D)), out=out)
 
 
 if __name__ == "__main__":

@@ -152,7 +152,7 @@ def test_planted_transpose_mistake_is_caught():
 @pytest.mark.parametrize("P", [1, 15, 16, 17, 40, 64])
 def test_scatter_matches_numpy_indexing_and_round_trips(P):
     rng = np.random.default_rng(P)
-    L, H, D, S = 2, 2, 16, 64
+    L, H, D, S = 2, 2, 32, 64
     nb = 9
     k = _bits(_bf16_valued(rng, (L, S, H, D)))
     v = _bits(_bf16_valued(rng, (L, S, H, D)))
@@ -165,11 +165,12 @@ def test_scatter_matches_numpy_indexing_and_round_trips(P):
         K = frame[l, 0].reshape(1, H, D, S)
         V = frame[l, 1].reshape(1, H, S, D)
         wk, wv = oatt.paged_from_dense(K, V, [P], table[None, :], nb)
+        kr, wkr = oatt.k_block_rows(ck[l]), oatt.k_block_rows(wk)   # token rows
         for j, blk in enumerate(table):
             n = min(16, P - 16 * j)
-            np.testing.assert_array_equal(ck[l, blk, :, :n], wk[blk, :, :n])
+            np.testing.assert_array_equal(kr[blk, :, :n], wkr[blk, :, :n])
             np.testing.assert_array_equal(cv[l, blk, :, :, :n], wv[blk, :, :, :n])
-            assert (ck[l, blk, :, n:] == 0).all() and (cv[l, blk, :, :, n:] == 0).all()
+            assert (kr[blk, :, n:] == 0).all() and (cv[l, blk, :, :, n:] == 0).all()
         untouched = sorted(set(range(nb)) - set(table.tolist()))
         assert (ck[l, untouched] == 7).all() and (cv[l, untouched] == 7).all()
     np.testing.assert_array_equal(orc.gather_paged(ck, cv, table, P, S), frame)
@@ -198,7 +199,7 @@ def _torch_f64_attention(q, ck, cv, tables, ctx, scale):
     H = ck.shape[1]
     G = Hq // H
     w = lambda u: torch.from_numpy(orc.bf16_widen(u)).double()   # noqa: E731
-    Q, CK, CV = w(q), w(ck), w(cv)
+    Q, CK, CV = w(q), w(oatt.k_block_rows(ck)), w(cv)             # K as token rows
     out = torch.zeros((B, Hq, D), dtype=torch.float64)
     for b in range(B):
         t = torch.arange(int(ctx[b]))
@@ -245,15 +246,16 @@ def test_attention_matches_cpu_layer_restatement():
 
 def test_attention_special_cases():
     rng = np.random.default_rng(13)
-    q, ck, cv, tables, _ = _attn_case(rng, 1, 4, 1, [32], 16)
+    q, ck, cv, tables, _ = _attn_case(rng, 1, 4, 1, [32], 32)
     blk0 = tables[0, 0]
     # one key: the output is that key's value row exactly
     out = orc.decode_attn(q, ck, cv, tables, np.array([1], np.int32), 0.3)
     np.testing.assert_array_equal(out[0, 0], orc.bf16_widen(cv[blk0, 0, :, 0]))
     # identical keys: uniform weights -> the mean of the values
-    ck2 = ck.copy()
-    ck2[tables[0, 0], 0] = ck2[tables[0, 0], 0, 0]
-    ck2[tables[0, 1], 0] = ck2[tables[0, 0], 0, 0]
+    rows = oatt.k_block_rows(ck)
+    rows[tables[0, 0], 0] = rows[tables[0, 0], 0, 0]
+    rows[tables[0, 1], 0] = rows[tables[0, 0], 0, 0]
+    ck2 = oatt.k_block_tiled(rows)
     out = orc.decode_attn(q, ck2, cv, tables, np.array([32], np.int32), 0.3)
     vals = np.concatenate([orc.bf16_widen(cv[tables[0, j], 0]) for j in range(2)], axis=1)
     np.testing.assert_allclose(out[0, 0], vals.mean(axis=1), rtol=1e-6, atol=1e-6)
@@ -261,21 +263,55 @@ def test_attention_special_cases():
 
 def test_cache_append_places_token():
     rng = np.random.default_rng(14)
-    q, ck, cv, tables, ctx = _attn_case(rng, 2, 4, 2, [20, 33], 16)
-    k_new = _bits(_bf16_valued(rng, (2, 2, 16)))
-    v_new = _bits(_bf16_valued(rng, (2, 2, 16)))
+    q, ck, cv, tables, ctx = _attn_case(rng, 2, 4, 2, [20, 33], 32)
+    k_new = _bits(_bf16_valued(rng, (2, 2, 32)))
+    v_new = _bits(_bf16_valued(rng, (2, 2, 32)))
+    before = oatt.k_block_rows(ck)
     orc.cache_append(k_new, v_new, ck, cv, tables, ctx)
+    rows = oatt.k_block_rows(ck)
     for b in range(2):
         t = ctx[b] - 1
         blk = tables[b, t // 16]
-        np.testing.assert_array_equal(ck[blk, :, t % 16, :], k_new[b])
+        np.testing.assert_array_equal(rows[blk, :, t % 16, :], k_new[b])
+        before[blk, :, t % 16, :] = k_new[b]
         np.testing.assert_array_equal(cv[blk, :, :, t % 16], v_new[b])
+    np.testing.assert_array_equal(rows, before)     # no other K element moved
 
 
 def test_golden_attention():
+    """Dense fixture (tests/golden/make_golden.py): the paged cache built from
+    it and read by the C oracle reproduces cpu_layer's output."""
     z = np.load(os.path.join(GOLDEN, "attention_small.npz"))
-    got = orc.decode_attn(z["q"], z["ck"], z["cv"], z["tables"], z["ctx"], float(z["scale"]))
-    np.testing.assert_allclose(got, z["out"], rtol=1e-6, atol=1e-7)
+    ck, cv = oatt.paged_from_dense(z["k_dense"], z["v_dense"], z["ctx"], z["tables"], 7)
+    got = orc.decode_attn(z["q"], ck, cv, z["tables"], z["ctx"], float(z["scale"]))
+    np.testing.assert_allclose(got, z["out"], rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------- K block layout ----
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+def test_k_block_layout_is_a_tiled_permutation(D):
+    idx = oatt.k_block_index(D)
+    assert sorted(idx.ravel().tolist()) == list(range(16 * D))           # a permutation
+    assert (np.diff(idx, axis=1)[:, np.arange(D - 1) % 8 != 7] == 1).all()   # 8-dim runs
+    # The QK tile reads: for tile t, dim group d0, its 8 tokens fill one 128-byte line.
+    for t in (0, 1):
+        toks = [s for s in range(16) if (s >> 2) & 1 == t]
+        toks.sort(key=lambda s: (s >> 3) * 4 + (s & 3))
+        for d0 in range(0, D, 8):
+            starts = idx[toks, d0]
+            assert starts[0] % 64 == 0 and (np.diff(starts) == 8).all()
+
+
+def test_k_block_layout_matches_the_kernel_formula():
+    """The formula the C oracle and the HIP kernels share, spelled out for a few
+    (slot, d) against k_block_index."""
+    D = 128
+    idx = oatt.k_block_index(D)
+    assert idx[0, 0] == 0 and idx[1, 0] == 8 and idx[3, 7] == 31
+    assert idx[8, 0] == 32              # j8 = 4
+    assert idx[4, 0] == 1024            # t = 1: after tile 0 (8 tokens x 128 dims)
+    assert idx[0, 8] == 64              # g = 1
+    assert idx[0, 32] == 256            # s = 1
 
 
 # --------------------------------------------------------------- argmax ----

@@ -40,3 +40,17 @@ def test_tables_and_growth():
     assert v.table.numel() == 2 and v.num_tokens == 20
     assert np.asarray(c.k.shape).tolist() == [2, 12, 2, 16, 64]
     assert np.asarray(c.v.shape).tolist() == [2, 12, 2, 64, 16]
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_k_block_helpers_match_the_oracle_layout(D):
+    """The product's torch helpers and the oracle's numpy restatement of the K
+    block order agree, and rows -> blocks -> rows is the identity."""
+    import torch
+    from oracle import attention as oatt
+    from rngd_pd_amd.engines.paged_cache import k_block_index, k_block_rows, k_block_tiled
+    np.testing.assert_array_equal(k_block_index(D).numpy(), oatt.k_block_index(D))
+    rows = torch.randint(-2**15, 2**15, (3, 2, 16, D), dtype=torch.int16)
+    blocks = k_block_tiled(rows)
+    np.testing.assert_array_equal(blocks.numpy(), oatt.k_block_tiled(rows.numpy()))
+    assert torch.equal(k_block_rows(blocks), rows)
