@@ -13,13 +13,17 @@
 // end to end over grid.x, so a launch moves up to PDK_MAX_BATCH requests of any
 // mix of lengths without a device-side descriptor buffer or an allocation.
 //
-// Cache policy, measured on the 8-request Llama-3.1-8B batch (pack then
-// scatter, 283 us per pair with ordinary accesses, 258 us with these): pack
-// reads the prefill KV and writes whole frame lines with streaming
-// (non-temporal) accesses, gather writes frame lines the same way, scatter
-// reads the read-once frame with streaming loads but keeps ordinary stores:
-// its V-block stores are 32-byte pieces of a line that the L2 must combine
-// before they reach HBM (streaming them costs 104 -> 177 us).
+// Cache policy. A launch that moves more bytes than the last-level cache holds
+// (kStreamBytes) uses streaming (non-temporal) accesses on its read-once side:
+// pack streams its prefill reads and whole-line frame writes, gather its frame
+// writes, scatter its frame reads. Scatter keeps ordinary stores: its V-block
+// stores are 32-byte pieces of a line that the L2 must combine before they
+// reach HBM (streaming them took the batch below from 104 to 177 us). Measured
+// on 8 Llama-3.1-8B requests (728 MiB packed, 452 MiB scattered; pack then
+// scatter): 283 us per pair with ordinary accesses, 258 us streaming. A
+// smaller launch keeps ordinary accesses, so a just-written frame can still be
+// in the cache when its consumer (a copy or the scatter) reads it: one
+// 512-token request packs in 22 us that way and in 28 us streaming.
 
 #include "pdk_common.h"
 
@@ -30,6 +34,7 @@ using pdk::v8;
 constexpr int kWaves = 4;        // wavefronts per workgroup
 constexpr int kTileT = 64;       // tokens per wavefront tile
 constexpr int kTileD = 64;       // dims per wavefront tile
+constexpr int64_t kStreamBytes = 256ll << 20;   // the MI355X last-level (Infinity) cache
 
 // Requests of a batched launch are laid end to end over grid.x: request r owns
 // wavefront tiles off[r] .. off[r+1]-1, so a launch holds only tiles with
@@ -54,6 +59,7 @@ __device__ __forceinline__ int64_t wave_unit() {
 
 // Frame layout per request: [L][2][F], F = Hkv*D*S; K frame [Hkv][D][S],
 // V frame [Hkv][S][D]; columns t >= P are zero (engines/prefill_full.py:378-379).
+template <bool kStream>
 __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
   const int64_t unit = wave_unit();
   if (unit >= a.off[a.n_req]) return;
@@ -78,8 +84,8 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
   for (int r = 0; r < 8; ++r) {
     const int t = t0 + r;
     if (t < P) {
-      kin[r] = pdk::ld16_stream(sk + (int64_t)t * R.tok_stride);
-      vin[r] = pdk::ld16_stream(sv + (int64_t)t * R.tok_stride);
+      kin[r] = pdk::ld16_as<kStream>(sk + (int64_t)t * R.tok_stride);
+      vin[r] = pdk::ld16_as<kStream>(sv + (int64_t)t * R.tok_stride);
     } else {
       kin[r] = pdk::zero8();
       vin[r] = pdk::zero8();
@@ -92,12 +98,12 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
   uint16_t* fv = fk + F;
 #pragma unroll
   for (int r = 0; r < 8; ++r)
-    if (!narrow || t0 + r < P) pdk::st16_stream(fv + ((int64_t)h * S + t0 + r) * D + d0, vin[r]);
+    if (!narrow || t0 + r < P) pdk::st16_as<kStream>(fv + ((int64_t)h * S + t0 + r) * D + d0, vin[r]);
   v8 kout[8];
   pdk::transpose8x8(kin, kout);  // kout[c]: dim d0+c, tokens t0..t0+7
 #pragma unroll
   for (int c = 0; c < 8; ++c)
-    pdk::st16_stream(fk + ((int64_t)h * D + d0 + c) * S + t0, kout[c]);
+    pdk::st16_as<kStream>(fk + ((int64_t)h * D + d0 + c) * S + t0, kout[c]);
 }
 
 struct ScatterArgs {
@@ -113,6 +119,7 @@ struct ScatterArgs {
 // Frame -> paged cache. K cache block [Hkv][16 x D] in the tiled token order of
 // pdk::k_unit (8 dims of one token per 16-byte unit), V cache block [Hkv][D][16]
 // (dim rows): both need an 8x8 transpose from the frame.
+template <bool kStream>
 __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
   const int64_t unit = wave_unit();
   if (unit >= a.off[a.n_req]) return;
@@ -146,8 +153,8 @@ __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     // K frame row d0+r holds tokens contiguously; V frame row t0+r holds dims.
-    kin[r] = pdk::ld16_stream(fk + ((int64_t)h * D + d0 + r) * S + t0);
-    vin[r] = pdk::ld16_stream(fv + ((int64_t)h * S + t0 + r) * D + d0);
+    kin[r] = pdk::ld16_as<kStream>(fk + ((int64_t)h * D + d0 + r) * S + t0);
+    vin[r] = pdk::ld16_as<kStream>(fv + ((int64_t)h * S + t0 + r) * D + d0);
   }
   // Keeps the compiler from hoisting the block-id test (and its wait for the
   // table load) above the frame loads.
@@ -183,6 +190,7 @@ struct GatherArgs {
 };
 
 // Paged cache -> S-wide frame (zero for t >= P).
+template <bool kStream>
 __global__ __launch_bounds__(256) void gather_kernel(const GatherArgs a) {
   const int64_t unit = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (unit >= a.units) return;
@@ -226,8 +234,8 @@ __global__ __launch_bounds__(256) void gather_kernel(const GatherArgs a) {
   pdk::transpose8x8(vin, vout);  // vout[c]: token t0+c, dims d0..d0+7
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    pdk::st16_stream(fk + ((int64_t)h * D + d0 + c) * S + t0, kout[c]);
-    pdk::st16_stream(fv + ((int64_t)h * S + t0 + c) * D + d0, vout[c]);
+    pdk::st16_as<kStream>(fk + ((int64_t)h * D + d0 + c) * S + t0, kout[c]);
+    pdk::st16_as<kStream>(fv + ((int64_t)h * S + t0 + c) * D + d0, vout[c]);
   }
 }
 
@@ -287,7 +295,15 @@ extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_lay
   if (a.off[n_reqs] == 0) return PDK_OK;
   const int64_t gx = grid_x(a.off[n_reqs]);
   PDK_REQUIRE(gx < (1ll << 31), "launch too large");
-  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
+  // Bytes the launch moves: valid tokens read, frame columns written.
+  int64_t moved = 0;
+  for (int i = 0; i < n_reqs; ++i)
+    moved += (int64_t)n_layers * 2 * n_kv_heads * head_dim * 2 *
+             (a.req[i].P + (int64_t)a.nT[i] * kTileT);
+  if (moved > kStreamBytes)
+    hipLaunchKernelGGL(pack_kernel<true>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(pack_kernel<false>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
   return pdk::check_launch("pack_kernel");
 }
 
@@ -347,7 +363,13 @@ extern "C" int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs, 
   }
   const int64_t gx = grid_x(a.off[n_reqs]);
   PDK_REQUIRE(gx < (1ll << 31), "launch too large");
-  hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
+  int64_t moved = 0;                             // valid frame columns read, blocks written
+  for (int i = 0; i < n_reqs; ++i)
+    moved += (int64_t)n_layers * 2 * n_kv_heads * head_dim * 2 * 2 * a.req[i].P;
+  if (moved > kStreamBytes)
+    hipLaunchKernelGGL(scatter_kernel<true>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(scatter_kernel<false>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
   return pdk::check_launch("scatter_kernel");
 }
 
@@ -393,6 +415,10 @@ extern "C" int pdk_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v
   a.units = (int64_t)n_layers * n_kv_heads * a.nC * a.nD;
   const int64_t gx = grid_x(a.units);
   PDK_REQUIRE(gx < (1ll << 31), "launch too large");
-  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
+  const int64_t moved = (int64_t)n_layers * 2 * n_kv_heads * head_dim * 2 * ((int64_t)P + S);
+  if (moved > kStreamBytes)
+    hipLaunchKernelGGL(gather_kernel<true>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(gather_kernel<false>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
   return pdk::check_launch("gather_kernel");
 }

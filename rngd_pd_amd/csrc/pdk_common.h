@@ -50,6 +50,17 @@ __device__ __forceinline__ void st16_stream(uint16_t* p, const v8& v) {
   __builtin_nontemporal_store(x, reinterpret_cast<u32x4_t*>(p));
 }
 
+template <bool kStream>
+__device__ __forceinline__ v8 ld16_as(const uint16_t* p) {
+  return kStream ? ld16_stream(p) : ld16(p);
+}
+
+template <bool kStream>
+__device__ __forceinline__ void st16_as(uint16_t* p, const v8& v) {
+  if (kStream) st16_stream(p, v);
+  else st16(p, v);
+}
+
 __device__ __forceinline__ v8 zero8() { return v8{{0u, 0u, 0u, 0u}}; }
 
 // Paged K-cache block layout. One (block, KV head) holds 16 tokens x D dims of

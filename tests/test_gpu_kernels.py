@@ -291,3 +291,46 @@ def test_decode_attention_graph_replays(cuda):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {i} differs"
+
+
+def test_streaming_launches_match_cached_launches(cuda):
+    """Launches that move more than 256 MiB use streaming loads/stores; smaller
+    ones do not. At full Llama-3.1-8B size, a 4-request batched pack and scatter
+    (512 MiB each, streaming) must equal the same requests launched one at a
+    time (128 MiB each, ordinary accesses, oracle-checked at small sizes
+    above), and a 2048-token gather (512 MiB, streaming) the oracle."""
+    from rngd_pd_amd.kernels import (gather_paged, pack_kv, pack_kv_batch, scatter_paged,
+                                     scatter_paged_batch)
+    L, S, H, D, n = 32, 512, 8, 128, 4
+    gen = torch.Generator(device=cuda).manual_seed(21)
+    pre = [torch.randn((L, S, 2, H, D), generator=gen, device=cuda).to(torch.bfloat16)
+           for _ in range(n)]
+    Ps = [512, 509, 497, 512]
+    one = [pack_kv(p[:, :, 0], p[:, :, 1], P, S) for p, P in zip(pre, Ps)]
+    many = [torch.empty_like(f) for f in one]
+    pack_kv_batch([(p[:, :, 0], p[:, :, 1], P, f) for p, P, f in zip(pre, Ps, many)], S)
+    torch.cuda.synchronize()
+    for a, b in zip(one, many):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    nb = n * (S // 16) + 3
+    perm = torch.from_numpy(np.random.default_rng(21).permutation(nb).astype(np.int32)).to(cuda)
+    tables = [perm[i * (S // 16):(i + 1) * (S // 16)] for i in range(n)]
+    ck1 = torch.zeros((L, nb, H, 16, D), dtype=torch.bfloat16, device=cuda)
+    cv1 = torch.zeros((L, nb, H, D, 16), dtype=torch.bfloat16, device=cuda)
+    ck2, cv2 = ck1.clone(), cv1.clone()
+    for f, t, P in zip(one, tables, Ps):
+        scatter_paged(f, t, P, S, ck1, cv1)
+    scatter_paged_batch(list(zip(one, tables, Ps)), S, ck2, cv2)
+    torch.cuda.synchronize()
+    assert torch.equal(ck1.view(torch.int16), ck2.view(torch.int16))
+    assert torch.equal(cv1.view(torch.int16), cv2.view(torch.int16))
+    del pre, many, ck1, cv1
+    # 2048 tokens: one gather moves 512 MiB.
+    S2 = 2048
+    nb2 = S2 // 16 + 1
+    t2 = np.random.default_rng(22).permutation(nb2)[:S2 // 16].astype(np.int32)
+    ck = rand_bf16(np.random.default_rng(23), (L, nb2, H, 16, D))
+    cv = rand_bf16(np.random.default_rng(24), (L, nb2, H, D, 16))
+    got = gather_paged(to_dev(ck), to_dev(cv), torch.from_numpy(t2).to(cuda), 2000, S2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(got), orc.gather_paged(ck, cv, t2, 2000, S2))
