@@ -392,7 +392,8 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
             "step_us_graph": round(graphed * 1e6, 1),
             "step_us_eager": round(eager * 1e6, 1),
             "layer_call_us": round(kern * 1e6, 2),
-            "roofline": roofline(kv_bytes, kern),
+            "roofline": roofline(kv_bytes, kern,
+                                 measured_traffic("decode_attn_B16") if B == 16 else None),
             "step_hbm_frac_graph": round(L * kv_bytes / graphed / 1e9 / HBM_PEAK_GBS, 4),
         }
         log(f"decode B={B}: graph {graphed*1e6:.1f} us/step ({B/graphed:.0f} tok/s), "

@@ -119,12 +119,26 @@ struct ScatterArgs {
 // Frame -> paged cache. K cache block [Hkv][16 x D] in the tiled token order of
 // pdk::k_unit (8 dims of one token per 16-byte unit), V cache block [Hkv][D][16]
 // (dim rows): both need an 8x8 transpose from the frame.
+//
+// A lane's 8 transposed K rows are 8 consecutive tokens, but each 128-byte line
+// of the tiled K block holds tokens from two lanes, and a V dim row (32 bytes)
+// holds a quarter line. Stored directly, every instruction would write 16-byte
+// pieces of 32 lines. So each wavefront stages its tile through LDS (8 KiB):
+// lanes write their vectors at their destination positions, then read them
+// back in destination order, and each store instruction writes 1 KiB of one
+// block contiguously. An XOR swizzle of the 16-byte slot index keeps both the
+// writes and the reads free of bank conflicts.
+__device__ __forceinline__ int swizzle_k(int i) { return i ^ ((i >> 3) & 7); }
+__device__ __forceinline__ int swizzle_v(int i) { return i ^ ((i >> 4) & 7); }
+
 template <bool kStream>
 __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
+  __shared__ uint4 stage[kWaves][512];
   const int64_t unit = wave_unit();
-  if (unit >= a.off[a.n_req]) return;
+  if (unit >= a.off[a.n_req]) return;           // uniform across the wavefront
   const int r = request_of(a.off, a.n_req, unit);
   const pdk_scatter_req& R = a.req[r];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   uint32_t u = (uint32_t)(unit - a.off[r]);
   const int dt = (int)(u % (uint32_t)a.nD); u /= (uint32_t)a.nD;
@@ -132,50 +146,89 @@ __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
   const int h = (int)(u % (uint32_t)a.Hkv); u /= (uint32_t)a.Hkv;
   const int l = (int)u;
   const int ti = lane >> 3, di = lane & 7;
-  const int S = a.S, D = a.D, P = R.P;
+  const int S = a.S, D = a.D, P = R.P;           // P >= 1: a request with P = 0 has no tiles
+  const int rP = (P + 15) & ~15;                 // tokens of the request's blocks, <= S
   const int t0 = ct * kTileT + ti * 8;
-  if (t0 >= ((P + 15) & ~15)) return;          // beyond the request's last block
-  const int j = t0 >> 4;
-  if (j >= R.n_table) return;
-  const int slot0 = t0 & 15;
+  const int tl = min(t0, rP - 8);                // lanes past the last block load in bounds
   const int d0 = dt * kTileD + di * 8;
   const int64_t F = (int64_t)a.Hkv * D * S;
   const uint16_t* fk = R.frame + (int64_t)(2 * l) * F;
   const uint16_t* fv = fk + F;
 
-  // The frame loads do not depend on the block id: issue them with it. They
-  // are unconditional (t0 + 8 <= round16(P) <= S keeps every address inside
-  // the frame) and the tokens >= P are zeroed afterwards: a load whose
-  // register is later overwritten by a select's zero in a divergent branch
-  // makes the compiler wait for that load before issuing the next one.
-  const int blk = R.table[j];
+  // The frame loads are unconditional and tokens >= P are zeroed afterwards:
+  // a load whose register a divergent branch later overwrites with zero makes
+  // the compiler wait for it before the next load.
   v8 kin[8], vin[8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    // K frame row d0+r holds tokens contiguously; V frame row t0+r holds dims.
-    kin[r] = pdk::ld16_as<kStream>(fk + ((int64_t)h * D + d0 + r) * S + t0);
-    vin[r] = pdk::ld16_as<kStream>(fv + ((int64_t)h * S + t0 + r) * D + d0);
+  for (int i = 0; i < 8; ++i) {
+    // K frame row d0+i holds tokens contiguously; V frame row tl+i holds dims.
+    kin[i] = pdk::ld16_as<kStream>(fk + ((int64_t)h * D + d0 + i) * S + tl);
+    vin[i] = pdk::ld16_as<kStream>(fv + ((int64_t)h * S + tl + i) * D + d0);
   }
-  // Keeps the compiler from hoisting the block-id test (and its wait for the
-  // table load) above the frame loads.
-  asm volatile("" ::: "memory");
-  if (blk < 0 || blk >= a.num_blocks) return;
+  // Block ids of the chunk's four blocks: uniform scalar loads from clamped,
+  // in-bounds indices (no branch, so nothing waits on them before the stores);
+  // blocks past the request's last one are dropped afterwards.
+  const int nblk = min(rP >> 4, R.n_table);
+  const int j0 = ct * (kTileT / 16);
+  int blk[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int id = R.table[min(j0 + q, nblk - 1)];
+    blk[q] = (j0 + q < nblk && id >= 0 && id < a.num_blocks) ? id : -1;
+  }
   if (t0 + 8 > P) {              // a narrow frame leaves tokens >= P unwritten
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      pdk::mask_tail(kin[r], t0, P);
-      if (t0 + r >= P) vin[r] = pdk::zero8();
+    for (int i = 0; i < 8; ++i) {
+      pdk::mask_tail(kin[i], t0, P);
+      if (t0 + i >= P) vin[i] = pdk::zero8();
     }
   }
   v8 kout[8], vout[8];
   pdk::transpose8x8(kin, kout);  // kout[c]: token t0+c, dims d0..d0+7
   pdk::transpose8x8(vin, vout);  // vout[c]: dim d0+c, tokens t0..t0+7
-  uint16_t* ck = a.cache_k + (int64_t)l * a.cache_ls + ((int64_t)blk * a.Hkv + h) * 16 * D;
-  uint16_t* cv = a.cache_v + (int64_t)l * a.cache_ls + ((int64_t)blk * a.Hkv + h) * D * 16;
+  // Materialise vout here. Computed later (next to its use, after the K
+  // stores), its first input would need a wait that also covers every K
+  // store issued meanwhile, as loads and stores share one counter.
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    asm volatile("" ::"v"(vout[c].w[0]), "v"(vout[c].w[1]), "v"(vout[c].w[2]), "v"(vout[c].w[3]));
+  uint4* st = stage[wave];
+  const int q_lane = ti >> 1;                    // the lane's block within the chunk
+
+  // K: run (q, t) of 64 units = tile t of block q for this wavefront's two
+  // 32-dim groups; inside it unit di*8 + j8 (pdk::k_unit with s, g from di).
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    pdk::st16(ck + (int64_t)pdk::k_unit(slot0 + c, d0, D) * 8, kout[c]);
-    pdk::st16(cv + (int64_t)(d0 + c) * 16 + slot0, vout[c]);
+    const int i = (q_lane * 2 + (c >> 2)) * 64 + di * 8 + (ti & 1) * 4 + (c & 3);
+    st[swizzle_k(i)] = make_uint4(kout[c].w[0], kout[c].w[1], kout[c].w[2], kout[c].w[3]);
+  }
+  const int nS = D >> 5;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint4 x = st[swizzle_k(k * 64 + lane)];
+    const int b = blk[k >> 1];
+    if (b >= 0) {
+      uint16_t* ck = a.cache_k + (int64_t)l * a.cache_ls + ((int64_t)b * a.Hkv + h) * 16 * D;
+      pdk::st16_as<kStream>(ck + ((int64_t)((k & 1) * nS + 2 * dt) * 32 + lane) * 8,
+                            v8{{x.x, x.y, x.z, x.w}});
+    }
+  }
+  // V: block q's dims d0 of this wavefront are 128 contiguous units (2 per dim
+  // row); lane vector c is unit (8di + c)*2 + (ti & 1).
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int i = q_lane * 128 + (8 * di + c) * 2 + (ti & 1);
+    st[swizzle_v(i)] = make_uint4(vout[c].w[0], vout[c].w[1], vout[c].w[2], vout[c].w[3]);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint4 x = st[swizzle_v(k * 64 + lane)];
+    const int b = blk[k >> 1];
+    if (b >= 0) {
+      uint16_t* cv = a.cache_v + (int64_t)l * a.cache_ls + ((int64_t)b * a.Hkv + h) * D * 16;
+      pdk::st16_as<kStream>(cv + ((int64_t)dt * 128 + (k & 1) * 64 + lane) * 8,
+                            v8{{x.x, x.y, x.z, x.w}});
+    }
   }
 }
 
