@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU baseline sample (0 skips it)")
-    ap.add_argument("--only", choices=["all", "handoff", "decode", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "handoff", "decode", "long", "copy"], default="all",
                     help="restrict the run (for profiler passes)")
     ap.add_argument("--copy-mib", type=int, default=1024,
                     help="bytes moved by --only copy (traffic-counter calibration)")
@@ -403,6 +403,77 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
     out["kernels"] = dict(out.get("kernels", {}), decode_attn_B16=res[f"B{batches[-1]}"]["roofline"])
 
 
+def bench_long(args, torch, dev, out, n_req=16, T=2048, hidden=4096):
+    """Long-context layer-pipelined save: n_req requests of T tokens (Llama-3.1-8B
+    KV), 32 layers. Per layer the "prefill" runs a bf16 GEMM [n_req*T, hidden] x
+    [hidden, hidden] on the compute stream, then save_kv_layer for every request
+    (the connector's device path: side-stream pack -> pinned D2H -> one ordered
+    writer thread per request publishing byte-identical wire files into /dev/shm).
+    Times the GEMMs alone, the saves alone and both; overlap % = hidden share of
+    the shorter leg. T = 2048 tokens per request is this workload's choice (the
+    prefill GEMM's row count is not fixed by the reference)."""
+    import shutil
+    from rngd_pd_amd.connector.rngd_kv import KVConnectorRole, RngdKVConnector
+    from rngd_pd_amd.connector.transport import ShmTransport
+    gen = torch.Generator(device=dev).manual_seed(4)
+    kv = [torch.randn((L, 2, T, H, D), generator=gen, device=dev).to(torch.bfloat16)
+          for _ in range(n_req)]
+    x = torch.randn((n_req * T, hidden), generator=gen, device=dev).to(torch.bfloat16)
+    w = torch.randn((hidden, hidden), generator=gen, device=dev).to(torch.bfloat16)
+    y = torch.empty((n_req * T, hidden), dtype=torch.bfloat16, device=dev)
+    wire_bytes = n_req * L * 2 * H * D * T * 2
+
+    def run(gemm, save, tag):
+        root = tempfile.mkdtemp(prefix="rngd_long_", dir="/dev/shm" if os.path.isdir("/dev/shm")
+                                else None)
+        conns = [RngdKVConnector(KVConnectorRole.WORKER, req_id=f"{tag}{i}",
+                                 transport=ShmTransport(root), n_layers=L, frame_tokens=T)
+                 for i in range(n_req)] if save else []
+        try:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for l in range(L):
+                if gemm:
+                    torch.matmul(x, w, out=y)
+                for i, c in enumerate(conns):
+                    c.save_kv_layer(f"layer.{l}", (kv[i][l, 0], kv[i][l, 1]), num_tokens=T)
+            for c in conns:
+                c.wait_for_save()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            if save:
+                n_files = len(os.listdir(root))
+                if n_files != n_req * L * 2:
+                    raise RuntimeError(f"long-context save published {n_files} files, "
+                                       f"expected {n_req * L * 2}")
+            return dt
+        finally:
+            for c in conns:
+                c.close()
+            shutil.rmtree(root, ignore_errors=True)
+
+    run(True, True, "warm")                         # allocations, envelopes, clocks
+    reps = {"g": [], "s": [], "b": []}
+    for rep in range(3):                            # interleaved; the save leg is host-bound
+        reps["g"].append(run(True, False, f"g{rep}-"))
+        reps["s"].append(run(False, True, f"s{rep}-"))
+        reps["b"].append(run(True, True, f"b{rep}-"))
+    t_gemm, t_save, t_both = (statistics.median(reps[k]) for k in ("g", "s", "b"))
+    overlap = (t_gemm + t_save - t_both) / min(t_gemm, t_save)
+    flops = 2.0 * n_req * T * hidden * hidden * L
+    res = {"repeats": 3, "requests": n_req, "tokens_per_request": T, "gemm": f"[{n_req * T},{hidden}]x[{hidden},{hidden}] bf16 per layer",
+           "wire_bytes": wire_bytes, "ms_gemm_only": round(t_gemm * 1e3, 2),
+           "ms_save_only": round(t_save * 1e3, 2), "ms_both": round(t_both * 1e3, 2),
+           "overlap_pct": round(100 * max(0.0, min(1.0, overlap)), 1),
+           "save_gbps": round(wire_bytes / t_save / 1e9, 2),
+           "save_gbps_with_gemm": round(wire_bytes / t_both / 1e9, 2),
+           "gemm_tflops": round(flops / t_gemm / 1e12, 1)}
+    out["extra"]["long_context"] = res
+    log(f"long context: gemm {res['ms_gemm_only']} ms, save {res['ms_save_only']} ms, "
+        f"both {res['ms_both']} ms, overlap {res['overlap_pct']} %, save {res['save_gbps']} GB/s")
+    del kv, x, w, y
+
+
 def bench_cpu(args, out):
     """The reference CPU shm path (oracle restatement), bounded to ~cpu_seconds."""
     from oracle import wire
@@ -494,6 +565,8 @@ def main():
         bench_handoff(args, torch, K, lib, dev, out)
     if args.only in ("all", "decode"):
         bench_decode(args, torch, K, lib, dev, out)
+    if args.only in ("all", "long"):
+        bench_long(args, torch, dev, out)
     if args.only == "all" and args.cpu_seconds > 0:
         bench_cpu(args, out)
     if args.only == "decode":

@@ -2,8 +2,9 @@
 
 FrameSaver (prefill side) replaces the download + encode + write of
 engines/prefill_full.py:378-384 and serving/cluster.py:187-218:
-  side stream: wait for the producer's stream -> pack one layer into a device
-  frame slot -> copy it into a pinned host slot -> event;
+  side stream: wait for the producer's stream -> pack one layer straight into
+  a pinned host slot (device-visible memory: the pack kernel's stores carry the
+  download, with no device staging slot and no copy) -> event;
   one writer thread, in save order (the reference's single ordered writer):
   wait for the event -> publish "<req>/<layer>/k" and ".../v" as
   header + payload + trailer straight from pinned memory (byte-identical to
@@ -37,6 +38,24 @@ def _align(x, a=ALIGN):
     return (x + a - 1) // a * a
 
 
+_SIDE_STREAMS = {}
+_SIDE_LOCK = threading.Lock()
+
+
+def side_stream(device, role="save"):
+    """The process-wide side stream of ``device`` for ``role`` ("save" or
+    "load"). Every request's copies and kernels of that role share it: with one
+    stream per request, requests would outnumber the hardware queues (4 per
+    process here), and a queue shared with the compute stream would hold copies
+    behind later compute kernels."""
+    key = (torch.device(device).index or 0, role)
+    with _SIDE_LOCK:
+        st = _SIDE_STREAMS.get(key)
+        if st is None:
+            st = _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
+        return st
+
+
 class FrameSaver:
     """Asynchronous, ordered device -> /dev/shm saver for one request."""
 
@@ -47,8 +66,7 @@ class FrameSaver:
         self.F = n_kv_heads * head_dim * S                # elements per K (or V) frame
         self.slot_bytes = 2 * self.F * 2
         self.n_slots = n_slots
-        self.stream = torch.cuda.Stream(device=self.device)
-        self.dev = torch.empty((n_slots, 1, 2, self.F), dtype=torch.bfloat16, device=self.device)
+        self.stream = side_stream(self.device)
         self.pinned = PinnedBuffer(n_slots * self.slot_bytes)
         self.events = EventArray(n_slots)
         self._free = queue.Queue()
@@ -74,9 +92,12 @@ class FrameSaver:
         with torch.cuda.stream(self.stream):
             for t in (k, v):
                 t.record_stream(self.stream)
-            _h.pack_kv(k, v, num_tokens, self.S, frame=self.dev[slot], stream=self.stream)
-            _lib.call("pdk_memcpy_d2h", self.pinned.ptr + slot * self.slot_bytes,
-                      self.dev[slot].data_ptr(), self.slot_bytes, self.stream.cuda_stream)
+            # The runtime's own device-to-host copy is a blit kernel under some
+            # HIP builds; its 256 workgroups then wait for CUs whenever a prefill
+            # GEMM fills the chip. Packing into the pinned slot needs one launch
+            # of half as many workgroups and no device slot.
+            _h.pack_kv(k, v, num_tokens, self.S, stream=self.stream,
+                       frame_ptr=self.pinned.ptr + slot * self.slot_bytes)
             _lib.call("pdk_event_record", self.events[slot], self.stream.cuda_stream)
         self._jobs.put((slot, layer_name))
 
@@ -153,7 +174,7 @@ class FrameLoader:
         self._used = [False] * n_slots
         self._next = 0
         self.frame = torch.empty((n_layers, 2, self.F), dtype=torch.bfloat16, device=self.device)
-        self.stream = torch.cuda.Stream(device=self.device)
+        self.stream = side_stream(self.device, "load")
 
     def _read_blob(self, key, which, base, shape):
         """Pull one blob into pinned memory at ``base``; returns the payload's pinned offset."""

@@ -15,6 +15,9 @@ void clear_error();
 int hip_fail(hipError_t e, const char* what);
 // Reports a launch error (hipGetLastError) after a kernel launch.
 int check_launch(const char* what);
+// Asynchronous copy between pinned or pageable host memory and device memory
+// on stream st (DMA engines when the host range is pinned).
+int copy_host_device(void* host, void* dev, size_t bytes, bool to_host, hipStream_t st);
 
 inline hipStream_t as_stream(uintptr_t s) { return reinterpret_cast<hipStream_t>(s); }
 inline hipEvent_t as_event(uintptr_t e) { return reinterpret_cast<hipEvent_t>(e); }

@@ -9,6 +9,39 @@
 
 namespace pdk {
 
+// Device-visible alias of [host, host + bytes) when the whole range is pinned
+// host memory (hipHostMalloc), else null. A failed lookup leaves an error in
+// the runtime's last-error slot, which is cleared here.
+static void* pinned_alias(void* host, size_t bytes) {
+  hipPointerAttribute_t a0{}, a1{};
+  char* last = static_cast<char*>(host) + bytes - 1;
+  const bool ok = hipPointerGetAttributes(&a0, host) == hipSuccess &&
+                  hipPointerGetAttributes(&a1, last) == hipSuccess;
+  (void)hipGetLastError();
+  // Both ends pinned, and mapped contiguously (one allocation).
+  if (!ok || a0.type != hipMemoryTypeHost || a1.type != hipMemoryTypeHost || !a0.devicePointer ||
+      static_cast<char*>(a1.devicePointer) != static_cast<char*>(a0.devicePointer) + (bytes - 1))
+    return nullptr;
+  return a0.devicePointer;
+}
+
+int copy_host_device(void* host, void* dev, size_t bytes, bool to_host, hipStream_t st) {
+  if (bytes == 0) return PDK_OK;
+  // Pinned memory is device-visible: copy on the DMA engines (the "no compute
+  // unit" kind), so the transfer takes nothing from kernels on other streams.
+  // Through the host kinds some runtimes copy with a blit kernel, which waits
+  // for CUs whenever a large kernel (a prefill GEMM) fills the chip.
+  if (void* alias = pinned_alias(host, bytes)) {
+    PDK_TRY_HIP(hipMemcpyAsync(to_host ? alias : dev, to_host ? dev : alias, bytes,
+                               hipMemcpyDeviceToDeviceNoCU, st));
+  } else {
+    PDK_TRY_HIP(hipMemcpyAsync(to_host ? host : dev, to_host ? dev : host, bytes,
+                               to_host ? hipMemcpyDeviceToHost : hipMemcpyHostToDevice, st));
+  }
+  return PDK_OK;
+}
+
+
 static thread_local char g_err[512] = {0};
 
 void set_error(const char* fmt, ...) {
@@ -147,17 +180,15 @@ int pdk_dev_free(void* p) {
 int pdk_memcpy_d2h(void* host_dst, const void* dev_src, size_t bytes, uintptr_t stream) {
   pdk::clear_error();
   PDK_REQUIRE(host_dst && dev_src, "null pointer argument");
-  PDK_TRY_HIP(hipMemcpyAsync(host_dst, dev_src, bytes, hipMemcpyDeviceToHost,
-                             pdk::as_stream(stream)));
-  return PDK_OK;
+  return pdk::copy_host_device(host_dst, const_cast<void*>(dev_src), bytes, true,
+                               pdk::as_stream(stream));
 }
 
 int pdk_memcpy_h2d(void* dev_dst, const void* host_src, size_t bytes, uintptr_t stream) {
   pdk::clear_error();
   PDK_REQUIRE(dev_dst && host_src, "null pointer argument");
-  PDK_TRY_HIP(hipMemcpyAsync(dev_dst, host_src, bytes, hipMemcpyHostToDevice,
-                             pdk::as_stream(stream)));
-  return PDK_OK;
+  return pdk::copy_host_device(const_cast<void*>(host_src), dev_dst, bytes, false,
+                               pdk::as_stream(stream));
 }
 
 int pdk_memcpy_d2d(void* dev_dst, const void* dev_src, size_t bytes, uintptr_t stream) {

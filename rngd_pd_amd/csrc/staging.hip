@@ -50,15 +50,18 @@ extern "C" int pdk_copy_layers(void* dst, const void* src, size_t layer_bytes, i
   if (rc) return rc;
   rc = check_events(done_events, n_layers, "done_events");
   if (rc) return rc;
-  const hipMemcpyKind kind = direction == PDK_COPY_D2H   ? hipMemcpyDeviceToHost
-                             : direction == PDK_COPY_H2D ? hipMemcpyHostToDevice
-                                                         : hipMemcpyDeviceToDevice;
   hipStream_t st = pdk::as_stream(stream);
   for (int l = 0; l < n_layers; ++l) {
     if (wait_events) PDK_TRY_HIP(hipStreamWaitEvent(st, pdk::as_event(wait_events[l]), 0));
-    PDK_TRY_HIP(hipMemcpyAsync(static_cast<char*>(dst) + (size_t)l * layer_bytes,
-                               static_cast<const char*>(src) + (size_t)l * layer_bytes,
-                               layer_bytes, kind, st));
+    char* d = static_cast<char*>(dst) + (size_t)l * layer_bytes;
+    char* s = const_cast<char*>(static_cast<const char*>(src)) + (size_t)l * layer_bytes;
+    if (direction == PDK_COPY_D2D) {
+      PDK_TRY_HIP(hipMemcpyAsync(d, s, layer_bytes, hipMemcpyDeviceToDevice, st));
+    } else {
+      const bool to_host = direction == PDK_COPY_D2H;
+      rc = pdk::copy_host_device(to_host ? d : s, to_host ? s : d, layer_bytes, to_host, st);
+      if (rc) return rc;
+    }
     if (done_events) PDK_TRY_HIP(hipEventRecord(pdk::as_event(done_events[l]), st));
   }
   return PDK_OK;

@@ -63,23 +63,32 @@ def _as_layers(k, v):
     return k, v
 
 
-def pack_kv(k, v, num_tokens, S, frame=None, stream=None):
+def pack_kv(k, v, num_tokens, S, frame=None, stream=None, frame_ptr=None):
     """Pack the first ``num_tokens`` tokens of every layer into an S-wide frame.
 
     Replaces engines/prefill_full.py:378-382 (zero-pad to S, download) and the
-    bf16 encode of connector/transport.py:33-35."""
+    bf16 encode of connector/transport.py:33-35. ``frame_ptr`` (instead of
+    ``frame``) packs into any device-visible memory of the frame's size, such
+    as a pinned host buffer: the kernel's own stores then carry the download,
+    with no staging copy. Returns the frame tensor, or None with frame_ptr."""
     _need(k, "k")
     _need(v, "v")
     k, v = _as_layers(k, v)
     L, T, H, D = k.shape
     if not 0 <= num_tokens <= min(T, S):
         raise ValueError(f"num_tokens={num_tokens} outside [0, min(T={T}, S={S})]")
-    if frame is None:
-        frame = torch.empty(frame_shape(L, H, D, S), dtype=BF16, device=k.device)
-    elif tuple(frame.shape) != frame_shape(L, H, D, S) or not frame.is_contiguous():
-        raise ValueError(f"frame must be contiguous {frame_shape(L, H, D, S)}")
+    if frame_ptr is not None:
+        if frame is not None:
+            raise ValueError("pass frame or frame_ptr, not both")
+        ptr = int(frame_ptr)
+    else:
+        if frame is None:
+            frame = torch.empty(frame_shape(L, H, D, S), dtype=BF16, device=k.device)
+        elif tuple(frame.shape) != frame_shape(L, H, D, S) or not frame.is_contiguous():
+            raise ValueError(f"frame must be contiguous {frame_shape(L, H, D, S)}")
+        ptr = frame.data_ptr()
     _lib.call("pdk_pack_kv", k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), L,
-              int(num_tokens), S, H, D, frame.data_ptr(), stream_handle(stream))
+              int(num_tokens), S, H, D, ptr, stream_handle(stream))
     return frame
 
 
