@@ -136,9 +136,17 @@ class RngdKVConnector(KVConnectorBase_V1):
             T, H, D = k.shape
             P = int(kwargs.get("num_tokens", T))
             if self._saver is None:
-                from .gpu_stage import FrameSaver
-                self._saver = FrameSaver(self.t, self.req_id, H, D, self.frame_tokens or T,
-                                         device=k.device)
+                if getattr(self.t, "device_ipc", False):
+                    # Same-GPU consumer: pack into an exported frame slot (no host copy).
+                    from .ipc import IpcSaver
+                    if not self.n_layers:
+                        raise ValueError("the ipc transport needs n_layers to size the frame")
+                    pool = self.t.pool(self.n_layers, H, D, self.frame_tokens or T, k.device)
+                    self._saver = IpcSaver(self.t, self.req_id, pool)
+                else:
+                    from .gpu_stage import FrameSaver
+                    self._saver = FrameSaver(self.t, self.req_id, H, D, self.frame_tokens or T,
+                                             device=k.device)
             self._saver.save(layer_name, k, v, P)
             self._saved[layer_name] = True
             return
@@ -166,12 +174,14 @@ class RngdKVConnector(KVConnectorBase_V1):
         from ..engines.paged_cache import PagedRequestView
         if isinstance(self._kv_caches, PagedRequestView):
             if self._loader is None:
-                from .gpu_stage import FrameLoader
                 view = self._kv_caches
-                self._loader = FrameLoader(self.t, self.req_id, view,
-                                           view.cache.n_layers, view.cache.n_kv_heads,
-                                           view.cache.head_dim, device=view.cache.device,
-                                           timeout=t)
+                if getattr(self.t, "device_ipc", False):
+                    from .ipc import IpcLoader as Loader
+                else:
+                    from .gpu_stage import FrameLoader as Loader
+                self._loader = Loader(self.t, self.req_id, view, view.cache.n_layers,
+                                      view.cache.n_kv_heads, view.cache.head_dim,
+                                      device=view.cache.device, timeout=t)
             return self._loader.load(layer_name, li)
         k = deser(self.t.pull(f"{self.req_id}/{layer_name}/k", timeout=t))
         v = deser(self.t.pull(f"{self.req_id}/{layer_name}/v", timeout=t))

@@ -237,7 +237,8 @@ class FencedTransport(Transport):
 
 
 # Our own adapters, used when the registry has no entry point of that name.
-_OWN = {"shm": "rngd_pd_amd.airm:ShmTransport"}
+_OWN = {"shm": "rngd_pd_amd.airm:ShmTransport",
+        "ipc": "rngd_pd_amd.connector.ipc:IpcTransport"}   # same-GPU frames in HBM
 _NOT_HERE = ("tcp", "nixl-ucx", "nixl")
 _CLASSES = {}          # name -> implementation class, resolved once per process
 _FENCED = {}           # name -> the process's one FencedTransport
@@ -290,12 +291,15 @@ def select_transport(name=None, **kw) -> Transport:
 
 
 def make_transport(backend="shm", **kw) -> Transport:
-    """Factory by backend name: inproc, shm, nixl (raises)."""
+    """Factory by backend name: inproc, shm, ipc, nixl (raises)."""
     b = backend.lower()
     if b == "inproc":
         return InProcTransport()
     if b == "shm":
         return ShmTransport(**kw)
+    if b == "ipc":
+        from .ipc import IpcTransport
+        return IpcTransport(**kw)
     if b == "nixl":
         return NixlTransport(**kw)
     if b in ("tcp", "nixl-ucx"):
