@@ -15,6 +15,9 @@ decode_batch tokens/s alongside.
             events (the reference's device->host->device staging).
   decode    GQA decode attention, 32 layers x B streams at context 512, per-layer
             launches, eager and replayed from a HIP graph.
+  step      the full Llama-3.1-8B decode step (random-init weights) at B=4 and
+            B=16, context 512, eager and from a HIP graph, beside the
+            reference's published 21.54 / 35.54 ms per step.
   cpu       the oracle's restatement of the reference CPU shm path (ser -> /dev/shm
             -> deser -> f32 place) on a bounded sample of the same requests.
 
@@ -46,7 +49,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU baseline sample (0 skips it)")
-    ap.add_argument("--only", choices=["all", "handoff", "decode", "long", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "handoff", "decode", "step", "long", "copy"],
+                    default="all",
                     help="restrict the run (for profiler passes)")
     ap.add_argument("--copy-mib", type=int, default=1024,
                     help="bytes moved by --only copy (traffic-counter calibration)")
@@ -403,6 +407,83 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
     out["kernels"] = dict(out.get("kernels", {}), decode_attn_B16=res[f"B{batches[-1]}"]["roofline"])
 
 
+def bench_step(args, torch, dev, out, batches=(4, 16), ctx=512):
+    """Full Llama-3.1-8B decode step (32 layers, random-init bf16 weights, no
+    checkpoint): embed -> per layer RMSNorm, fused QKV GEMM, RoPE + cache write,
+    paged decode attention, o GEMM + residual, RMSNorm, gate|up GEMM, SwiGLU,
+    down GEMM + residual -> final norm, lm_head GEMM, greedy argmax. Every
+    stream at context ctx (its new token at slot ctx-1; the reference's S=512
+    step attends over the whole S). Bytes per step = every weight read once
+    (16.06 GB; the embedding contributes B rows) + the K/V of all layers."""
+    from rngd_pd_amd.engines.llama_decode import LlamaConfig, LlamaDecoder, LlamaWeights
+    from rngd_pd_amd.engines.paged_cache import PagedKVCache
+    published = {4: 21.54, 16: 35.54}           # ms/step, bench/profile_solo_S512_B{4,16}.json
+    cfg = LlamaConfig()
+    t0 = time.perf_counter()
+    w = LlamaWeights.random(cfg, seed=8, device=dev)
+    bmax = max(batches)
+    per = (ctx + BS - 1) // BS
+    cache = PagedKVCache(cfg.n_layers, bmax * per, H, D, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(9)
+    for li in range(cfg.n_layers):
+        cache.k[li].copy_(torch.randn(cache.k[li].shape, generator=gen, device=dev))
+        cache.v[li].copy_(torch.randn(cache.v[li].shape, generator=gen, device=dev))
+    dec = LlamaDecoder(w, cache, max_batch=bmax)
+    perm = np.random.default_rng(9).permutation(bmax * per).astype(np.int32).reshape(bmax, per)
+    tables_all = torch.from_numpy(perm).to(dev)
+    torch.cuda.synchronize()
+    log(f"step: weights {w.nbytes() / 1e9:.2f} GB ready in {time.perf_counter() - t0:.1f} s")
+    weight_bytes = w.nbytes() - w.embed.numel() * 2
+    res = {}
+    for B in batches:
+        tables = tables_all[:B].contiguous()
+        ctx_d = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        tok = torch.randint(0, cfg.vocab, (B,), generator=gen, device=dev)
+        for _ in range(args.warmup):
+            dec.step(tok, ctx_d, tables, ctx)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            dec.step(tok, ctx_d, tables, ctx)
+        torch.cuda.synchronize()
+        eager = (time.perf_counter() - t0) / args.steps
+        want = dec.tokens[:B].clone()
+        g = dec.capture(tok, ctx_d, tables, ctx)
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(dec.tokens[:B], want):
+            raise RuntimeError("graph replay of the decode step differs from the eager step")
+        ta, tb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ta.record()
+        for _ in range(args.steps):
+            g.replay()
+        tb.record()
+        torch.cuda.synchronize()
+        graphed = (time.perf_counter() - t0) / args.steps
+        dev_ms = ta.elapsed_time(tb) / args.steps
+        step_bytes = weight_bytes + B * H * 2 + cfg.n_layers * B * ctx * H * D * 2 * 2
+        ms = graphed * 1e3
+        res[f"B{B}"] = {
+            "ms_per_step_graph": round(ms, 3),
+            "ms_per_step_eager": round(eager * 1e3, 3),
+            "tokens_per_s_graph": round(B / graphed, 1),
+            "bytes_per_step": step_bytes,
+            "hbm_gbps": round(step_bytes / (dev_ms / 1e3) / 1e9, 1),
+            "hbm_frac": round(step_bytes / (dev_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "reference_ms_per_step": published[B],
+            "speedup_vs_reference": round(published[B] / ms, 2),
+        }
+        log(f"step B={B} ctx={ctx}: graph {ms:.3f} ms ({B / graphed:.0f} tok/s, "
+            f"{res[f'B{B}']['hbm_frac'] * 100:.1f}% of HBM), eager {eager * 1e3:.3f} ms; "
+            f"reference {published[B]} ms")
+        del g
+    out["extra"]["decode_step_llama8b"] = res
+    del dec, cache, w
+    torch.cuda.empty_cache()
+
+
 def bench_long(args, torch, dev, out, n_req=16, T=2048, hidden=4096):
     """Long-context layer-pipelined save: n_req requests of T tokens (Llama-3.1-8B
     KV), 32 layers. Per layer the "prefill" runs a bf16 GEMM [n_req*T, hidden] x
@@ -565,10 +646,16 @@ def main():
         bench_handoff(args, torch, K, lib, dev, out)
     if args.only in ("all", "decode"):
         bench_decode(args, torch, K, lib, dev, out)
+    if args.only in ("all", "step"):
+        bench_step(args, torch, dev, out)
     if args.only in ("all", "long"):
         bench_long(args, torch, dev, out)
     if args.only == "all" and args.cpu_seconds > 0:
         bench_cpu(args, out)
+    if args.only == "step":
+        b = out["extra"]["decode_step_llama8b"]["B16"]
+        out.update(value=b["tokens_per_s_graph"], unit="tokens/s",
+                   ms_per_step=b["ms_per_step_graph"])
     if args.only == "decode":
         b = out["extra"]["decode_batch"]["B16"]
         out.update(value=b["tokens_per_s_graph"], unit="tokens/s",

@@ -194,6 +194,38 @@ int pdk_cache_append(const uint16_t* k_new, const uint16_t* v_new,
 int pdk_greedy_argmax(const uint16_t* logits, int B, int V, int64_t ld,
                       int32_t* out, uintptr_t stream);
 
+/* ---- decode step: the non-GEMM operations of one Llama layer ----------------
+ * The rest of the reference's DecodeLayer.forward (kernels/decode_batch.py:73-91)
+ * around the attention above; the projections and the lm_head are plain GEMMs
+ * for the caller's BLAS. bf16 in and out, fp32 inside. */
+
+/* RMSNorm of B rows of H (H % 8 == 0, H <= 8192): out = x * rsqrt(mean(x^2) +
+ * eps) * weight (rms_dsl, kernels/dsl_batch.py:22-41, engines/model.py:53-54).
+ * With add != NULL the residual add comes first and is written back:
+ * x = bf16(x + add) (zipadd_dsl, kernels/dsl_batch.py:43-53). */
+int pdk_rmsnorm(uint16_t* x, const uint16_t* add, const uint16_t* weight, int B,
+                int H, float eps, uint16_t* out, uintptr_t stream);
+
+/* RoPE at position ctx[b]-1 and the new token's cache write, from one
+ * projection row per stream: qkv [B][qkv_ld] holds q (n_q_heads heads), k and
+ * v (n_kv_heads each) of head_dim. Rotate-half with angle pos*inv_freq[i]
+ * (inv_freq fp32 [head_dim/2]; engines/model.py:32-48,57-65, the llama3
+ * scaling applied by the caller). Writes rotated q to q_out [B][n_q_heads]
+ * [head_dim], and the rotated k and v into slot ctx[b]-1 of the paged cache
+ * (one layer, block_tables [B][max_blocks]): the one-hot injection of
+ * kernels/decode_batch.py:81-82 as a store. head_dim % 32 == 0. */
+int pdk_rope_cache_append(const uint16_t* qkv, int64_t qkv_ld, uint16_t* q_out,
+                          const float* inv_freq, const int32_t* ctx_lens,
+                          const int32_t* block_tables, int max_blocks,
+                          uint16_t* cache_k, uint16_t* cache_v, int num_blocks,
+                          int B, int n_q_heads, int n_kv_heads, int head_dim,
+                          uintptr_t stream);
+
+/* out [B][M] = silu(g) * u for gate_up [B][2M] = [g | u] (swiglu_dsl,
+ * kernels/dsl_batch.py:55-71). M % 8 == 0. */
+int pdk_swiglu(const uint16_t* gate_up, int B, int M, uint16_t* out,
+               uintptr_t stream);
+
 /* ---- staging and device memory ----------------------------------------------
  * Pinned host staging replaces the synchronous .cpu() download
  * (engines/prefill_full.py:381-382) and .to(dev) upload

@@ -1,0 +1,218 @@
+// The non-GEMM kernels of the Llama decode step for gfx950: RMSNorm with the
+// residual add fused in, RoPE fused with the new token's paged-cache write,
+// and SwiGLU. The projections and the lm_head are plain GEMMs (the caller's
+// BLAS); attention is decode_attn_kernel.
+//
+// Each is bound by the bytes it moves (a few KiB per stream per layer); they
+// exist to keep the step to one launch per operation with fp32 arithmetic
+// inside and bf16 at every tensor boundary, as the reference's step keeps its
+// activations in bf16 (kernels/decode_batch.py:73-91).
+
+#include <math.h>
+
+#include "pdk_common.h"
+
+namespace {
+
+using pdk::v8;
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// One workgroup per row of H (H % 8 == 0, H <= 8192), 256 threads, 8 bf16 per
+// 16-byte access, the row held in registers between the two passes. kAdd:
+// x <- bf16(x + add), written back (the residual add, zipadd_dsl of
+// kernels/dsl_batch.py), before the norm. Then
+// out = bf16(x * rsqrt(mean(x^2) + eps) * w) (rms_dsl: x * (sum x^2 + eps*H)^-1/2
+// * w*sqrt(H), the same value).
+constexpr int kNormThreads = 256, kNormChunks = 4;     // 8 elements per chunk
+
+template <bool kAdd>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(uint16_t* x, const uint16_t* add,
+                                                               const uint16_t* w, float eps,
+                                                               int H, uint16_t* out) {
+  __shared__ float part[kNormThreads / 64];
+  const int64_t row = (int64_t)blockIdx.x * H;
+  const int n8 = H >> 3;
+  v8 keep[kNormChunks];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kNormChunks; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    keep[j] = pdk::zero8();
+    if (c < n8) {
+      v8 a = pdk::ld16(x + row + 8 * c);
+      if (kAdd) {
+        const v8 b = pdk::ld16(add + row + 8 * c);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float lo = pdk::bf16_to_f32(a.w[k] & 0xffffu) + pdk::bf16_to_f32(b.w[k] & 0xffffu);
+          const float hi = pdk::bf16_to_f32(a.w[k] >> 16) + pdk::bf16_to_f32(b.w[k] >> 16);
+          a.w[k] = pdk::f32_to_bf16_rne(lo) | (pdk::f32_to_bf16_rne(hi) << 16);
+        }
+        pdk::st16(x + row + 8 * c, a);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float lo = pdk::bf16_to_f32(a.w[k] & 0xffffu), hi = pdk::bf16_to_f32(a.w[k] >> 16);
+        ss += lo * lo + hi * hi;
+      }
+      keep[j] = a;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
+  const float r = rsqrtf(tot / (float)H + eps);
+#pragma unroll
+  for (int j = 0; j < kNormChunks; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    if (c < n8) {
+      const v8 a = keep[j];
+      const v8 g = pdk::ld16(w + 8 * c);
+      v8 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float lo = pdk::bf16_to_f32(a.w[k] & 0xffffu) * r * pdk::bf16_to_f32(g.w[k] & 0xffffu);
+        const float hi = pdk::bf16_to_f32(a.w[k] >> 16) * r * pdk::bf16_to_f32(g.w[k] >> 16);
+        o.w[k] = pdk::f32_to_bf16_rne(lo) | (pdk::f32_to_bf16_rne(hi) << 16);
+      }
+      pdk::st16(out + row + 8 * c, o);
+    }
+  }
+}
+
+__device__ __forceinline__ float bf(uint16_t h) { return pdk::bf16_to_f32(h); }
+__device__ __forceinline__ uint16_t to_bf(float f) { return (uint16_t)pdk::f32_to_bf16_rne(f); }
+
+// Grid (NH + 2*NKV, B), HD/2 threads. Row b of qkv holds q (NH heads), k (NKV)
+// and v (NKV), HD each. Rotate-half RoPE at position pos = ctx[b]-1 (HF's
+// rotate_half, engines/model.py:55-64; angle pos*inv_freq[i] in fp32 as the
+// reference's tables, engines/decode_batch.py:244-255): q heads go to q_out
+// [B][NH][HD]; the rotated k and the v of the new token go to slot pos of the
+// paged cache (the one-hot injection of kernels/decode_batch.py:81-82 as a
+// store), K in the tiled block order of pdk::k_unit.
+__global__ void rope_append_kernel(const uint16_t* qkv, int64_t ld, uint16_t* q_out,
+                                   const float* inv_freq, const int32_t* ctx,
+                                   const int32_t* tables, int max_blocks, uint16_t* ck,
+                                   uint16_t* cv, int num_blocks, int NH, int NKV, int HD) {
+  const int head = blockIdx.x, b = blockIdx.y, i = threadIdx.x, half = HD >> 1;
+  const int pos = ctx[b] - 1;
+  const uint16_t* row = qkv + (int64_t)b * ld;
+  int blk = -1;
+  if (pos >= 0 && pos < max_blocks * 16) {
+    const int id = tables[(int64_t)b * max_blocks + (pos >> 4)];
+    if (id >= 0 && id < num_blocks) blk = id;
+  }
+  const int slot = pos & 15;
+  if (head < NH + NKV) {
+    const uint16_t* src = row + (int64_t)head * HD;
+    const float a = bf(src[i]), c = bf(src[i + half]);
+    float s, co;
+    sincosf((float)max(pos, 0) * inv_freq[i], &s, &co);
+    const uint16_t o0 = to_bf(a * co - c * s), o1 = to_bf(c * co + a * s);
+    if (head < NH) {
+      uint16_t* q = q_out + ((int64_t)b * NH + head) * HD;
+      q[i] = o0;
+      q[i + half] = o1;
+    } else if (blk >= 0) {
+      uint16_t* kb = ck + ((int64_t)blk * NKV + (head - NH)) * 16 * HD;
+      kb[pdk::k_unit(slot, i & ~7, HD) * 8 + (i & 7)] = o0;
+      kb[pdk::k_unit(slot, (i + half) & ~7, HD) * 8 + ((i + half) & 7)] = o1;
+    }
+  } else if (blk >= 0) {
+    const int vh = head - NH - NKV;
+    const uint16_t* src = row + (int64_t)(NH + NKV + vh) * HD;
+    uint16_t* vb = cv + ((int64_t)blk * NKV + vh) * HD * 16;
+    vb[(int64_t)i * 16 + slot] = src[i];
+    vb[(int64_t)(i + half) * 16 + slot] = src[i + half];
+  }
+}
+
+// out[b][m] = bf16(silu(g) * u), g = gu[b][m], u = gu[b][M+m], fp32 inside
+// (swiglu_dsl of kernels/dsl_batch.py: g * sigmoid(g) * u). 8 per thread.
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* gu, int M, int64_t n8,
+                                                     uint16_t* out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n8) return;
+  const int64_t per_row = M >> 3;
+  const int64_t b = t / per_row, c = t - b * per_row;
+  const v8 g = pdk::ld16(gu + b * 2 * M + 8 * c);
+  const v8 u = pdk::ld16(gu + b * 2 * M + M + 8 * c);
+  v8 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float g0 = pdk::bf16_to_f32(g.w[k] & 0xffffu), g1 = pdk::bf16_to_f32(g.w[k] >> 16);
+    const float u0 = pdk::bf16_to_f32(u.w[k] & 0xffffu), u1 = pdk::bf16_to_f32(u.w[k] >> 16);
+    const float r0 = g0 / (1.f + expf(-g0)) * u0, r1 = g1 / (1.f + expf(-g1)) * u1;
+    o.w[k] = pdk::f32_to_bf16_rne(r0) | (pdk::f32_to_bf16_rne(r1) << 16);
+  }
+  pdk::st16(out + b * M + 8 * c, o);
+}
+
+}  // namespace
+
+extern "C" int pdk_rmsnorm(uint16_t* x, const uint16_t* add, const uint16_t* weight, int B,
+                           int H, float eps, uint16_t* out, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(x && weight && out, "null pointer argument");
+  PDK_REQUIRE(B >= 1 && B <= 65535, "B must be in [1, 65535] (got %d)", B);
+  PDK_REQUIRE(H >= 8 && H % 8 == 0 && H <= kNormThreads * kNormChunks * 8,
+              "H must be a multiple of 8 in [8, %d] (got %d)", kNormThreads * kNormChunks * 8, H);
+  PDK_REQUIRE(pdk::aligned16(x) && pdk::aligned16(weight) && pdk::aligned16(out) &&
+                  (!add || pdk::aligned16(add)),
+              "tensors must be 16-byte aligned");
+  PDK_REQUIRE(eps >= 0.f, "eps must be >= 0");
+  hipStream_t st = pdk::as_stream(stream);
+  if (add)
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(B), dim3(kNormThreads), 0, st, x, add, weight, eps, H,
+                       out);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(B), dim3(kNormThreads), 0, st, x, add, weight, eps, H,
+                       out);
+  return pdk::check_launch("rmsnorm_kernel");
+}
+
+extern "C" int pdk_rope_cache_append(const uint16_t* qkv, int64_t qkv_ld, uint16_t* q_out,
+                                     const float* inv_freq, const int32_t* ctx_lens,
+                                     const int32_t* block_tables, int max_blocks,
+                                     uint16_t* cache_k, uint16_t* cache_v, int num_blocks, int B,
+                                     int n_q_heads, int n_kv_heads, int head_dim,
+                                     uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(qkv && q_out && inv_freq && ctx_lens && block_tables && cache_k && cache_v,
+              "null pointer argument");
+  PDK_REQUIRE(B >= 1 && B <= 65535, "B must be in [1, 65535] (got %d)", B);
+  PDK_REQUIRE(n_q_heads >= 1 && n_kv_heads >= 1 && n_q_heads + 2 * n_kv_heads <= 65535,
+              "head counts out of range");
+  PDK_REQUIRE(head_dim >= 32 && head_dim % 32 == 0 && head_dim <= 2048,
+              "head_dim must be a multiple of 32 in [32, 2048] (got %d)", head_dim);
+  PDK_REQUIRE(qkv_ld >= (int64_t)(n_q_heads + 2 * n_kv_heads) * head_dim,
+              "qkv_ld=%lld shorter than a (q, k, v) row", (long long)qkv_ld);
+  PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1, "num_blocks and max_blocks must be >= 1");
+  hipLaunchKernelGGL(rope_append_kernel, dim3(n_q_heads + 2 * n_kv_heads, B),
+                     dim3(head_dim / 2), 0, pdk::as_stream(stream), qkv, qkv_ld, q_out, inv_freq,
+                     ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads,
+                     n_kv_heads, head_dim);
+  return pdk::check_launch("rope_append_kernel");
+}
+
+extern "C" int pdk_swiglu(const uint16_t* gate_up, int B, int M, uint16_t* out,
+                          uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(gate_up && out, "null pointer argument");
+  PDK_REQUIRE(B >= 1 && M >= 8 && M % 8 == 0, "B >= 1 and M a positive multiple of 8");
+  PDK_REQUIRE(pdk::aligned16(gate_up) && pdk::aligned16(out), "tensors must be 16-byte aligned");
+  const int64_t n8 = (int64_t)B * (M / 8);
+  const int64_t blocks = (n8 + 255) / 256;
+  PDK_REQUIRE(blocks < (1ll << 31), "launch too large");
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     pdk::as_stream(stream), gate_up, M, n8, out);
+  return pdk::check_launch("swiglu_kernel");
+}

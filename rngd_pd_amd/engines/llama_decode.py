@@ -1,0 +1,217 @@
+"""The full Llama decode step on MI355X: one token for each of B streams.
+
+Replaces the reference's BatchDecodeEngine.step / step_logits
+(engines/decode_batch.py:422-442) and its compiled DecodeLayer
+(kernels/decode_batch.py:56-91) plus the batched lm_head and greedy argmax
+(engines/decode_batch.py:162-171). Per layer:
+
+  rmsnorm(x [+ previous residual]) -> h            pdk_rmsnorm (residual add fused)
+  h @ Wqkv -> qkv                                  GEMM (hipBLASLt via torch)
+  RoPE(q, k) + new k, v into the paged cache        pdk_rope_cache_append
+  attention over slots 0..pos                      pdk_decode_attn
+  ao @ Wo -> o; x += o; rmsnorm -> h2              GEMM, pdk_rmsnorm
+  h2 @ [Wg | Wu] -> gu; silu(g) * u -> a           GEMM, pdk_swiglu
+  a @ Wd -> residual for the next layer            GEMM
+
+then the final norm (with the last residual), the lm_head GEMM and the
+first-maximum argmax (pdk_greedy_argmax). Weights are stored [in, out]
+contiguous, with q, k, v and gate, up fused, so every projection is one plain
+2-D GEMM. Activations are bf16 at every tensor boundary, as the reference's
+are; the kernels compute in fp32 inside.
+"""
+import contextlib
+import math
+
+import torch
+
+from .. import _lib
+from ..kernels import attention as _attn
+from ..kernels.handoff import stream_handle
+
+BF16 = torch.bfloat16
+
+
+class LlamaConfig:
+    """Llama-3.1-8B by default (engines/model.py:14-31 reads these from the HF config)."""
+
+    def __init__(self, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, inter=14336,
+                 vocab=128256, n_layers=32, eps=1e-5, theta=500000.0,
+                 rope_scaling=(8.0, 1.0, 4.0, 8192)):
+        self.hidden, self.n_heads, self.n_kv_heads, self.head_dim = hidden, n_heads, n_kv_heads, head_dim
+        self.inter, self.vocab, self.n_layers, self.eps = inter, vocab, n_layers, eps
+        self.theta = theta
+        self.rope_scaling = rope_scaling   # (factor, low_freq_factor, high_freq_factor, original_max_pos) or None
+
+    @property
+    def qkv_dim(self):
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+    def inv_freq(self):
+        """float32 [head_dim/2]: theta^(-2i/d), with the llama3 band scaling
+        (engines/model.py:32-48): long wavelengths divided by `factor`, short ones
+        kept, the band between interpolated."""
+        d = self.head_dim
+        inv = [1.0 / (self.theta ** (2 * i / d)) for i in range(d // 2)]
+        if self.rope_scaling:
+            factor, lo, hi, orig = self.rope_scaling
+            low_wl, high_wl = orig / lo, orig / hi
+            out = []
+            for f in inv:
+                wl = 2 * math.pi / f
+                if wl > low_wl:
+                    out.append(f / factor)
+                elif wl < high_wl:
+                    out.append(f)
+                else:
+                    s = (orig / wl - lo) / (hi - lo)
+                    out.append((1 - s) * f / factor + s * f)
+            inv = out
+        return torch.tensor(inv, dtype=torch.float64).to(torch.float32)
+
+
+class LlamaWeights:
+    """Decode-step weights, [in, out] contiguous bf16 on one device."""
+
+    def __init__(self, cfg, norm1, wqkv, wo, norm2, wgu, wd, embed, norm_f, lm_head):
+        self.cfg = cfg
+        self.norm1, self.wqkv, self.wo, self.norm2 = norm1, wqkv, wo, norm2
+        self.wgu, self.wd = wgu, wd
+        self.embed, self.norm_f, self.lm_head = embed, norm_f, lm_head
+
+    @classmethod
+    def random(cls, cfg, seed=0, device="cuda", std=0.02):
+        """Random-init weights of the given shape (no checkpoint is fetched):
+        projections N(0, std), norms 1 + N(0, 0.05), embedding N(0, 1)."""
+        g = torch.Generator(device=device).manual_seed(seed)
+        L, H, M = cfg.n_layers, cfg.hidden, cfg.inter
+
+        def w(*shape, scale=std, mean=0.0):
+            return (torch.randn(shape, generator=g, device=device) * scale + mean).to(BF16)
+
+        return cls(cfg,
+                   norm1=w(L, H, scale=0.05, mean=1.0),
+                   wqkv=w(L, H, cfg.qkv_dim),
+                   wo=w(L, cfg.n_heads * cfg.head_dim, H),
+                   norm2=w(L, H, scale=0.05, mean=1.0),
+                   wgu=w(L, H, 2 * M),
+                   wd=w(L, M, H),
+                   embed=w(cfg.vocab, H, scale=1.0),
+                   norm_f=w(H, scale=0.05, mean=1.0),
+                   lm_head=w(H, cfg.vocab))
+
+    def nbytes(self):
+        return sum(t.numel() * t.element_size() for t in
+                   (self.norm1, self.wqkv, self.wo, self.norm2, self.wgu, self.wd, self.embed,
+                    self.norm_f, self.lm_head))
+
+
+class LlamaDecoder:
+    """B-stream decode steps over a PagedKVCache (same n_layers, Hkv, head_dim)."""
+
+    def __init__(self, weights, cache, max_batch):
+        cfg = self.cfg = weights.cfg
+        if (cache.n_layers, cache.n_kv_heads, cache.head_dim) != (cfg.n_layers, cfg.n_kv_heads,
+                                                                  cfg.head_dim):
+            raise ValueError("cache shape does not match the model")
+        self.w, self.cache = weights, cache
+        dev = self.device = cache.device
+        B, H = max_batch, cfg.hidden
+        self.max_batch = B
+        e = lambda *s: torch.empty(s, dtype=BF16, device=dev)   # noqa: E731
+        self.x, self.h = e(B, H), e(B, H)
+        self.qkv = e(B, cfg.qkv_dim)
+        self.q = e(B, cfg.n_heads, cfg.head_dim)
+        self.ao = e(B, cfg.n_heads, cfg.head_dim)
+        self.o = e(B, H)
+        self.gu, self.act = e(B, 2 * cfg.inter), e(B, cfg.inter)
+        self.mlp = e(B, H)
+        self.logits = e(B, cfg.vocab)
+        self.tokens = torch.empty(B, dtype=torch.int32, device=dev)
+        self.inv = cfg.inv_freq().to(dev)
+        self.scale = 1.0 / math.sqrt(cfg.head_dim)
+        self._ws = None
+        # Per-layer operands resolved once: the step loop makes no views.
+        w = weights
+        self._layers = [(w.norm1[i].data_ptr(), w.wqkv[i], w.wo[i], w.norm2[i].data_ptr(),
+                         w.wgu[i], w.wd[i], cache.k[i].data_ptr(), cache.v[i].data_ptr())
+                        for i in range(cfg.n_layers)]
+
+    def _workspace(self, B, max_ctx):
+        need = _attn.workspace_bytes(B, self.cfg.n_heads, max_ctx, self.cfg.head_dim)
+        if need and (self._ws is None or self._ws.numel() * 4 < need):
+            self._ws = torch.zeros(need // 4 + 64, dtype=torch.float32, device=self.device)
+        return self._ws if need else None
+
+    def step(self, tokens, ctx_lens, tables, max_ctx, stream=None):
+        """tokens int64/int32 [B] on the device (this step's input token per
+        stream), ctx_lens int32 [B] = position + 1 (the new token's slot is
+        ctx_lens-1, attention covers 0..ctx_lens-1), tables int32 [B, max_blocks]
+        holding at least ceil(ctx/16) blocks each; max_ctx (<= max_blocks*16)
+        sizes the attention's split plan and should cover every ctx_lens. Returns
+        the next token per stream (int32 [B], device) and leaves the final hidden
+        state in self.x[:B] (before the final norm), the logits in
+        self.logits[:B]. ``stream``: a torch stream for every launch (default:
+        the current stream)."""
+        cfg, w, cache = self.cfg, self.w, self.cache
+        B = tokens.shape[0]
+        if B > self.max_batch:
+            raise ValueError(f"B={B} above max_batch={self.max_batch}")
+        for t, name in ((tokens, "tokens"), (ctx_lens, "ctx_lens"), (tables, "tables")):
+            if not t.is_cuda or t.device != self.device:
+                raise ValueError(f"{name} must be on {self.device}")
+        if ctx_lens.dtype != torch.int32 or ctx_lens.numel() != B:
+            raise ValueError("ctx_lens must be int32 [B]")
+        if tables.dtype != torch.int32 or tables.dim() != 2 or tables.shape[0] != B \
+                or not tables.is_contiguous():
+            raise ValueError("tables must be contiguous int32 [B, max_blocks]")
+        st = stream_handle(stream)
+        H, NH, NKV, HD = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        x, h, qkv, q, ao = self.x[:B], self.h[:B], self.qkv[:B], self.q[:B], self.ao[:B]
+        o, gu, act, mlp = self.o[:B], self.gu[:B], self.act[:B], self.mlp[:B]
+        ao2 = ao.view(B, NH * HD)
+        ws = self._workspace(B, max_ctx)
+        ws_ptr = ws.data_ptr() if ws is not None else None
+        ws_bytes = ws.numel() * 4 if ws is not None else 0
+        mb, nb = tables.shape[1], cache.num_blocks
+        tp, cp = tables.data_ptr(), ctx_lens.data_ptr()
+        xp, hp, qkvp, qp, aop = x.data_ptr(), h.data_ptr(), qkv.data_ptr(), q.data_ptr(), ao.data_ptr()
+        op, mlpp, inv, ldq = o.data_ptr(), mlp.data_ptr(), self.inv.data_ptr(), qkv.stride(0)
+        call = _lib.call
+        with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+            torch.index_select(w.embed, 0, tokens.long(), out=x)
+            for li, (n1, wqkv, wo, n2, wgu, wd, ck, cv) in enumerate(self._layers):
+                call("pdk_rmsnorm", xp, mlpp if li else None, n1, B, H, cfg.eps, hp, st)
+                torch.matmul(h, wqkv, out=qkv)
+                call("pdk_rope_cache_append", qkvp, ldq, qp, inv, cp, tp, mb, ck, cv, nb, B, NH,
+                     NKV, HD, st)
+                call("pdk_decode_attn", qp, ck, cv, nb, tp, mb, cp, int(max_ctx), B, NH, NKV, HD,
+                     self.scale, ws_ptr, ws_bytes, aop, st)
+                torch.matmul(ao2, wo, out=o)
+                call("pdk_rmsnorm", xp, op, n2, B, H, cfg.eps, hp, st)
+                torch.matmul(h, wgu, out=gu)
+                call("pdk_swiglu", gu.data_ptr(), B, cfg.inter, act.data_ptr(), st)
+                torch.matmul(act, wd, out=mlp)
+            call("pdk_rmsnorm", xp, mlpp, w.norm_f.data_ptr(), B, H, cfg.eps, hp, st)
+            logits = self.logits[:B]
+            torch.matmul(h, w.lm_head, out=logits)
+            call("pdk_greedy_argmax", logits.data_ptr(), B, cfg.vocab, logits.stride(0),
+                 self.tokens.data_ptr(), st)
+        return self.tokens[:B]
+
+    def capture(self, tokens, ctx_lens, tables, max_ctx):
+        """One step captured as a HIP graph over these device tensors.
+
+        replay() re-runs the step on whatever tokens, ctx_lens and tables hold
+        then (the caller updates them in place; max_ctx is fixed at capture, so
+        pass the tables' capacity to allow any context). One warm step runs
+        first, eagerly, on the capture stream: it is a real step (it writes the
+        cache slot of each stream's current position)."""
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.step(tokens, ctx_lens, tables, max_ctx)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.step(tokens, ctx_lens, tables, max_ctx)
+        return graph

@@ -1,0 +1,78 @@
+"""torch-facing wrappers of the decode step's non-GEMM kernels.
+
+Replace rms_dsl + zipadd_dsl (kernels/dsl_batch.py:22-53), the RoPE rotation
+and one-hot cache injection of DecodeLayer.forward (kernels/decode_batch.py:
+69-82) and swiglu_dsl (kernels/dsl_batch.py:55-71). bf16 tensors on the
+device; fp32 arithmetic inside the kernels.
+"""
+import torch
+
+from .. import _lib
+from .attention import _check_layer_cache
+from .handoff import _need, stream_handle
+
+
+def rmsnorm(x, weight, eps, add=None, out=None, stream=None):
+    """out = rmsnorm(x) * weight over the last dim of x [B, H].
+
+    With ``add`` [B, H], x is first replaced in place by bf16(x + add) (the
+    residual add), and the norm is taken of that sum."""
+    _need(x, "x")
+    _need(weight, "weight")
+    if x.dim() != 2 or not x.is_contiguous():
+        raise ValueError(f"x must be contiguous [B, H], got {tuple(x.shape)}")
+    B, H = x.shape
+    if weight.numel() != H or not weight.is_contiguous():
+        raise ValueError(f"weight must hold H={H} contiguous values")
+    if add is not None:
+        _need(add, "add")
+        if add.shape != x.shape or not add.is_contiguous():
+            raise ValueError("add must be contiguous and shaped like x")
+    if out is None:
+        out = torch.empty_like(x)
+    _lib.call("pdk_rmsnorm", x.data_ptr(), add.data_ptr() if add is not None else None,
+              weight.data_ptr(), B, H, float(eps), out.data_ptr(), stream_handle(stream))
+    return out
+
+
+def rope_cache_append(qkv, inv_freq, ctx_lens, block_tables, cache_k, cache_v, n_q_heads,
+                      q_out=None, stream=None):
+    """RoPE at position ctx_lens[b]-1 and the new token's cache write.
+
+    qkv [B, >= (n_q + 2 n_kv) * D] bf16 rows (unit column stride) holding q, k,
+    v; inv_freq float32 [D/2]; cache_k [nb, Hkv, 16, D] and cache_v
+    [nb, Hkv, D, 16] (one layer). Returns rotated q [B, n_q, D]."""
+    _need(qkv, "qkv")
+    _need(inv_freq, "inv_freq", torch.float32)
+    _need(ctx_lens, "ctx_lens", torch.int32)
+    _need(block_tables, "block_tables", torch.int32)
+    nb, Hkv, D = _check_layer_cache(cache_k, cache_v)
+    if qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be [B, N] with unit column stride")
+    B = qkv.shape[0]
+    if qkv.shape[1] < (n_q_heads + 2 * Hkv) * D:
+        raise ValueError(f"qkv rows hold {qkv.shape[1]} values, need {(n_q_heads + 2 * Hkv) * D}")
+    if inv_freq.numel() != D // 2:
+        raise ValueError(f"inv_freq must hold head_dim/2 = {D // 2} values")
+    if ctx_lens.numel() != B or block_tables.dim() != 2 or block_tables.shape[0] != B \
+            or not block_tables.is_contiguous():
+        raise ValueError("ctx_lens [B] and contiguous block_tables [B, max_blocks] expected")
+    if q_out is None:
+        q_out = torch.empty((B, n_q_heads, D), dtype=qkv.dtype, device=qkv.device)
+    _lib.call("pdk_rope_cache_append", qkv.data_ptr(), qkv.stride(0), q_out.data_ptr(),
+              inv_freq.data_ptr(), ctx_lens.data_ptr(), block_tables.data_ptr(),
+              block_tables.shape[1], cache_k.data_ptr(), cache_v.data_ptr(), nb, B, n_q_heads,
+              Hkv, D, stream_handle(stream))
+    return q_out
+
+
+def swiglu(gate_up, out=None, stream=None):
+    """gate_up [B, 2M] = [g | u] -> silu(g) * u [B, M]."""
+    _need(gate_up, "gate_up")
+    if gate_up.dim() != 2 or not gate_up.is_contiguous() or gate_up.shape[1] % 2:
+        raise ValueError("gate_up must be contiguous [B, 2M]")
+    B, M = gate_up.shape[0], gate_up.shape[1] // 2
+    if out is None:
+        out = torch.empty((B, M), dtype=gate_up.dtype, device=gate_up.device)
+    _lib.call("pdk_swiglu", gate_up.data_ptr(), B, M, out.data_ptr(), stream_handle(stream))
+    return out

@@ -1,0 +1,251 @@
+"""The decode step on the GPU against the oracle's restatement of cpu_layer.
+
+Kernel by kernel (RMSNorm with the residual add, RoPE with the cache write,
+SwiGLU), then whole steps of the Llama decoder over a paged cache holding
+random prefilled KV. The whole-step bar is the reference's own
+(kernels/decode_batch.py:285-294: hidden-state rel L2 below 0.08 against the
+fp32 CPU layer); the test also holds a tighter bound that bf16 activations
+meet, and greedy tokens must equal the oracle's wherever the oracle's top-two
+logit margin exceeds the measured logit error.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import decode as od
+from tests._util import rand_bf16, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+HALF_ULP = 2.0 ** -8            # bf16 round-to-nearest: relative error at most 2^-8
+LLAMA3 = (8.0, 1.0, 4.0, 8192)
+REL_REFERENCE_BAR = 0.08        # kernels/decode_batch.py:294
+REL_TIGHT = 0.02
+
+
+def _f32(u16):
+    return (np.asarray(u16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _bf16_bits_rne(x_f32):
+    t = torch.from_numpy(np.ascontiguousarray(x_f32, np.float32)).to(BF16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+# ---- kernels -----------------------------------------------------------------
+
+@pytest.mark.parametrize("B,H", [(1, 4096), (5, 512), (3, 8192), (2, 8)])
+def test_rmsnorm_and_residual_add(cuda, B, H):
+    from rngd_pd_amd import kernels as K
+    rng = np.random.default_rng(B * 7 + H)
+    x, add = rand_bf16(rng, (B, H), 2.0), rand_bf16(rng, (B, H), 2.0)
+    w = rand_bf16(rng, (H,))
+    xd, addd, wd = to_dev(x), to_dev(add), to_dev(w)
+    print(f"rmsnorm B={B} H={H}", flush=True)
+    out = K.rmsnorm(xd, wd, 1e-5)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(xd), x)                 # no add: x untouched
+    np.testing.assert_allclose(_f32(to_host(out)), od.rmsnorm(_f32(x), _f32(w), 1e-5),
+                               rtol=HALF_ULP, atol=1e-6)
+    out = K.rmsnorm(xd, wd, 1e-5, add=addd)
+    torch.cuda.synchronize()
+    summed = _bf16_bits_rne(_f32(x) + _f32(add))                  # one fp32 add, then RNE
+    np.testing.assert_array_equal(to_host(xd), summed)
+    np.testing.assert_allclose(_f32(to_host(out)), od.rmsnorm(_f32(summed), _f32(w), 1e-5),
+                               rtol=HALF_ULP, atol=1e-6)
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_rope_and_cache_write(cuda, D):
+    from rngd_pd_amd import kernels as K
+    NH, NKV = 8, 2
+    positions = [0, 15, 16, 33, 4095, 99999]
+    B = len(positions)
+    rng = np.random.default_rng(D)
+    max_blocks = max(positions) // 16 + 1
+    nb = 2 * B + 1
+    tables = np.zeros((B, max_blocks), np.int32)                  # unused entries name block 0
+    own = rng.permutation(np.arange(1, nb))[:B]                   # one distinct block per stream
+    for b, p in enumerate(positions):
+        tables[b, p // 16] = own[b]
+    N = (NH + 2 * NKV) * D
+    qkv_full = rand_bf16(rng, (B, N + 24))                        # row stride wider than a row
+    ck0, cv0 = rand_bf16(rng, (nb, NKV, 16, D)), rand_bf16(rng, (nb, NKV, D, 16))
+    ck, cv = to_dev(ck0), to_dev(cv0)
+    inv = od.inv_freq(D, 500000.0, LLAMA3)
+    print(f"rope_cache_append D={D} positions={positions}", flush=True)
+    q = K.rope_cache_append(to_dev(qkv_full)[:, :N], torch.from_numpy(inv).to(cuda),
+                            torch.tensor([p + 1 for p in positions], dtype=torch.int32,
+                                         device=cuda),
+                            torch.from_numpy(tables).to(cuda), ck, cv, NH)
+    torch.cuda.synchronize()
+    qkv = _f32(qkv_full[:, :N])
+    want_q = od.rope(qkv[:, :NH * D].reshape(B, NH, D), positions, inv)
+    np.testing.assert_allclose(_f32(to_host(q)), want_q, rtol=HALF_ULP, atol=1e-5)
+    want_k = od.rope(qkv[:, NH * D:(NH + NKV) * D].reshape(B, NKV, D), positions, inv)
+    v_bits = qkv_full[:, (NH + NKV) * D:N].reshape(B, NKV, D)
+    got_k, got_v = to_host(ck), to_host(cv)
+    rows_got, rows_0 = oatt.k_block_rows(got_k), oatt.k_block_rows(ck0)
+    expect_k, expect_v = rows_0.copy(), cv0.copy()
+    for b, p in enumerate(positions):
+        blk, slot = own[b], p % 16
+        np.testing.assert_allclose(_f32(rows_got[blk, :, slot, :]), want_k[b], rtol=HALF_ULP,
+                                   atol=1e-5)
+        expect_k[blk, :, slot, :] = rows_got[blk, :, slot, :]
+        expect_v[blk, :, :, slot] = v_bits[b]                      # v is copied bit for bit
+    np.testing.assert_array_equal(rows_got, expect_k)              # nothing else changed
+    np.testing.assert_array_equal(got_v, expect_v)
+
+
+@pytest.mark.parametrize("B,M", [(3, 14336), (1, 8), (16, 1024)])
+def test_swiglu(cuda, B, M):
+    from rngd_pd_amd import kernels as K
+    rng = np.random.default_rng(M + B)
+    gu = rand_bf16(rng, (B, 2 * M), 4.0)
+    gu[0, :4] = _bf16_bits_rne(np.array([100.0, -100.0, 0.0, -0.0], np.float32))
+    print(f"swiglu B={B} M={M}", flush=True)
+    out = K.swiglu(to_dev(gu))
+    torch.cuda.synchronize()
+    got = _f32(to_host(out))
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, od.swiglu(_f32(gu)), rtol=HALF_ULP, atol=1e-6)
+
+
+# ---- whole steps -------------------------------------------------------------
+
+class _OCfg:
+    def __init__(self, cfg):
+        self.n_heads, self.n_kv_heads, self.eps = cfg.n_heads, cfg.n_kv_heads, cfg.eps
+        self.inv = cfg.inv_freq().numpy()
+
+
+def _oracle_weights(w):
+    f = lambda t: t.float().cpu().numpy()   # noqa: E731
+    return {"embed": f(w.embed), "norm_f": f(w.norm_f), "lm_head": f(w.lm_head),
+            "layers": [(f(w.norm1[i]), f(w.wqkv[i]), f(w.wo[i]), f(w.norm2[i]), f(w.wgu[i]),
+                        f(w.wd[i])) for i in range(w.cfg.n_layers)]}
+
+
+def _prefilled(cuda, cfg, ctx, steps, rng):
+    """A paged cache whose streams hold random KV at positions 0..ctx[b]-2 (the
+    step writes ctx[b]-1), with the same values in dense oracle caches."""
+    from rngd_pd_amd.engines.paged_cache import PagedKVCache
+    B, L, NKV, HD = len(ctx), cfg.n_layers, cfg.n_kv_heads, cfg.head_dim
+    S = max(ctx) + steps
+    per = (S + 15) // 16
+    nb = B * per + 3
+    tables = rng.permutation(nb)[:B * per].astype(np.int32).reshape(B, per)
+    cache = PagedKVCache(L, nb, NKV, HD, device=cuda)
+    Ks, Vs = [], []
+    have = [c - 1 for c in ctx]
+    for li in range(L):
+        k = rand_bf16(rng, (B, NKV, S, HD))
+        v = rand_bf16(rng, (B, NKV, S, HD))
+        for b, h in enumerate(have):
+            k[b, :, h:] = 0
+            v[b, :, h:] = 0
+        ck, cv = oatt.paged_from_dense(np.transpose(k, (0, 1, 3, 2)), v, have, tables, nb)
+        cache.k[li].copy_(to_dev(ck))
+        cache.v[li].copy_(to_dev(cv))
+        Ks.append(_f32(k))
+        Vs.append(_f32(v))
+    return cache, torch.from_numpy(tables).to(cuda), Ks, Vs
+
+
+def _check_step(dec, B, want_tok, want_x, want_logits, label):
+    got_x = dec.x[:B].float().cpu().numpy()
+    got_logits = dec.logits[:B].float().cpu().numpy()
+    got_tok = dec.tokens[:B].cpu().numpy()
+    rel = od.rel_l2(got_x, want_x)
+    rel_logits = od.rel_l2(got_logits, want_logits)
+    print(f"{label}: hidden rel {rel:.5f} logits rel {rel_logits:.5f}", flush=True)
+    assert rel < REL_REFERENCE_BAR, f"{label}: hidden rel {rel}"
+    assert rel < REL_TIGHT, f"{label}: hidden rel {rel}"
+    assert rel_logits < REL_TIGHT, f"{label}: logits rel {rel_logits}"
+    np.testing.assert_array_equal(got_tok, np.argmax(got_logits, -1))   # first maximum
+    checked = 0
+    for b in range(B):
+        top2 = np.sort(want_logits[b])[-2:]
+        err = np.abs(got_logits[b] - want_logits[b]).max()
+        if top2[1] - top2[0] > 2 * err:
+            assert got_tok[b] == want_tok[b], f"{label}: stream {b} token"
+            checked += 1
+    return got_tok, checked
+
+
+def _run_steps(cuda, cfg, ctx, steps, seed):
+    from rngd_pd_amd.engines.llama_decode import LlamaDecoder, LlamaWeights
+    rng = np.random.default_rng(seed)
+    B = len(ctx)
+    w = LlamaWeights.random(cfg, seed=seed, device=cuda)
+    ow, ocfg = _oracle_weights(w), _OCfg(cfg)
+    cache, tables, Ks, Vs = _prefilled(cuda, cfg, ctx, steps, rng)
+    dec = LlamaDecoder(w, cache, max_batch=B)
+    tok = rng.integers(0, cfg.vocab, B)
+    checked = 0
+    for s in range(steps):
+        pos = [c - 1 + s for c in ctx]
+        ctx_d = torch.tensor([p + 1 for p in pos], dtype=torch.int32, device=cuda)
+        dec.step(torch.from_numpy(tok).to(cuda), ctx_d, tables, max(pos) + 1)
+        torch.cuda.synchronize()
+        want_tok, want_x, want_logits = od.decode_step(tok, ow, Ks, Vs, pos, ocfg)
+        got_tok, n = _check_step(dec, B, want_tok, want_x, want_logits, f"step {s}")
+        checked += n
+        tok = got_tok.astype(np.int64)                # both sides continue from the same tokens
+    assert checked >= steps * B // 2, f"only {checked} tokens had a clear margin"
+    return dec
+
+
+def test_small_model_steps(cuda):
+    from rngd_pd_amd.engines.llama_decode import LlamaConfig
+    cfg = LlamaConfig(hidden=512, n_heads=8, n_kv_heads=2, head_dim=128, inter=1024,
+                      vocab=1000, n_layers=3)
+    print("small model: 3 layers, ctx [1, 16, 17, 200, 513]", flush=True)
+    _run_steps(cuda, cfg, [1, 16, 17, 200, 513], steps=3, seed=11)
+
+
+def test_llama8b_shape_two_layers(cuda):
+    """Llama-3.1-8B dimensions (hidden 4096, 32/8 heads, MLP 14336, vocab
+    128256) with 2 of the 32 layers, B=16 at mixed context lengths."""
+    from rngd_pd_amd.engines.llama_decode import LlamaConfig
+    cfg = LlamaConfig(n_layers=2)
+    ctx = [512, 1, 511, 300, 17, 16, 64, 129, 512, 2, 480, 33, 256, 99, 400, 512]
+    print("llama-8b shape: 2 layers, B=16", flush=True)
+    _run_steps(cuda, cfg, ctx, steps=2, seed=5)
+
+
+def test_graph_replays_match_eager(cuda):
+    """The step captured as a HIP graph replays the eager result, with eager
+    work and synchronisation between replays."""
+    from rngd_pd_amd.engines.llama_decode import LlamaConfig, LlamaDecoder, LlamaWeights
+    cfg = LlamaConfig(hidden=512, n_heads=8, n_kv_heads=2, head_dim=128, inter=1024,
+                      vocab=1000, n_layers=2)
+    rng = np.random.default_rng(3)
+    ctx = [40, 300, 7, 129]
+    B = len(ctx)
+    w = LlamaWeights.random(cfg, seed=3, device=cuda)
+    cache, tables, _, _ = _prefilled(cuda, cfg, ctx, 1, rng)
+    dec = LlamaDecoder(w, cache, max_batch=B)
+    tok = torch.from_numpy(rng.integers(0, cfg.vocab, B)).to(cuda)
+    ctx_d = torch.tensor(ctx, dtype=torch.int32, device=cuda)
+    cap = tables.shape[1] * 16
+    print("graph capture: 2 layers, B=4", flush=True)
+    dec.step(tok, ctx_d, tables, cap)
+    torch.cuda.synchronize()
+    want_x, want_tok = dec.x[:B].clone(), dec.tokens[:B].clone()
+    graph = dec.capture(tok, ctx_d, tables, cap)
+    for r in range(3):
+        dec.x.zero_()
+        dec.tokens.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        rel = od.rel_l2(dec.x[:B].float().cpu().numpy(), want_x.float().cpu().numpy())
+        print(f"replay {r}: rel {rel:.2e}", flush=True)
+        assert rel < 1e-3
+        assert torch.equal(dec.tokens[:B], want_tok)
+        _ = torch.randn(1000, device=cuda).sum().item()           # eager work between replays
