@@ -226,6 +226,35 @@ int pdk_rope_cache_append(const uint16_t* qkv, int64_t qkv_ld, uint16_t* q_out,
 int pdk_swiglu(const uint16_t* gate_up, int B, int M, uint16_t* out,
                uintptr_t stream);
 
+/* ---- decode step: weight-streaming GEMMs ------------------------------------
+ * The projections of the reference's DecodeLayer.forward (kernels/decode_batch.py:
+ * 73-91: q/k/v, o, gate/up and down matmuls, each followed there by a bf16
+ * result) and the batched lm_head (engines/decode_batch.py:162-171), for the
+ * decode batch sizes where every weight is read once per step:
+ *   y [B][N] = x [B][K] . w [N][K]^T (+ residual [B][N]),  1 <= B <= 64,
+ * w in [out][in] layout, K % 128 == 0, N >= 1, fp32 accumulation, one
+ * bf16 rounding. With residual != NULL the sum is y = residual + x.w^T
+ * (zipadd_dsl, kernels/dsl_batch.py:43-53, fused); residual may alias y. */
+int pdk_linear(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+               const uint16_t* residual, uint16_t* y, uintptr_t stream);
+
+/* y [B][M] = silu(x . wg^T) * (x . wu^T), w_gate_up = [wg; wu] as [2M][K]
+ * (the gate and up matmuls and swiglu_dsl, kernels/dsl_batch.py:55-71, in one
+ * pass over the weights). M >= 1, K % 128 == 0, 1 <= B <= 64. */
+int pdk_linear_swiglu(const uint16_t* x, const uint16_t* w_gate_up, int B, int K,
+                      int M, uint16_t* y, uintptr_t stream);
+
+/* The lm_head GEMM with greedy sampling fused: logits = x . w^T as in
+ * pdk_linear (written to `logits` [B][N] unless it is NULL), and tokens[b] =
+ * the first-maximum argmax of row b of the bf16 logits, NaN ranking first
+ * (the same result as pdk_greedy_argmax on those logits; greedy_tokens,
+ * engines/decode_batch.py:162-171). keys: device uint64 [B] scratch that
+ * must read zero before the first call; every call leaves it zero. Calls
+ * sharing one keys array must not overlap. */
+int pdk_linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                      uint16_t* logits, uint64_t* keys, int32_t* tokens,
+                      uintptr_t stream);
+
 /* ---- staging and device memory ----------------------------------------------
  * Pinned host staging replaces the synchronous .cpu() download
  * (engines/prefill_full.py:381-382) and .to(dev) upload

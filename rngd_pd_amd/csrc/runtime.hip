@@ -68,6 +68,8 @@ int check_launch(const char* what) {
 
 namespace {
 
+using pdk::v8;
+
 // First-maximum argmax of one bf16 row; NaN ranks above every number (the
 // torch.argmax convention greedy_tokens relies on).
 struct Best {
@@ -82,24 +84,49 @@ __device__ __forceinline__ bool better(const Best& x, const Best& y) {
   return x.i < y.i;
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* logits, int V, int64_t ld,
-                                                     int32_t* out) {
-  __shared__ Best red[256];
+// One workgroup of 1024 threads per row. kVec: the row is 16-byte aligned
+// and V % 8 == 0, read as 8 values per load; otherwise one value per load.
+// `better` is a total order (value, then NaN rank, then lower index), so the
+// order in which threads visit elements does not matter.
+constexpr int kArgThreads = 1024;
+
+__device__ __forceinline__ void consider(Best& best, float x, int i) {
+  const Best c{x, i, x != x ? 1 : 0};
+  if (better(c, best)) best = c;
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const uint16_t* logits, int V,
+                                                             int64_t ld, int32_t* out) {
+  __shared__ Best red[kArgThreads / 64];
   const uint16_t* row = logits + (int64_t)blockIdx.x * ld;
   Best best{-INFINITY, 0x7fffffff, 0};
-  for (int i = threadIdx.x; i < V; i += blockDim.x) {
-    const float x = pdk::bf16_to_f32(row[i]);
-    const Best c{x, i, x != x ? 1 : 0};
+  if (kVec) {
+    const int n8 = V >> 3;
+#pragma unroll 4
+    for (int c = threadIdx.x; c < n8; c += kArgThreads) {
+      const v8 v = pdk::ld16(row + 8 * c);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        consider(best, pdk::bf16_to_f32(v.w[k] & 0xffffu), 8 * c + 2 * k);
+        consider(best, pdk::bf16_to_f32(v.w[k] >> 16), 8 * c + 2 * k + 1);
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < V; i += kArgThreads) consider(best, pdk::bf16_to_f32(row[i]), i);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const Best c{__shfl_xor(best.v, o), __shfl_xor(best.i, o), __shfl_xor(best.nan, o)};
     if (better(c, best)) best = c;
   }
-  red[threadIdx.x] = best;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
   __syncthreads();
-  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s && better(red[threadIdx.x + s], red[threadIdx.x]))
-      red[threadIdx.x] = red[threadIdx.x + s];
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int q = 1; q < kArgThreads / 64; ++q)
+      if (better(red[q], best)) best = red[q];
+    out[blockIdx.x] = best.i;
   }
-  if (threadIdx.x == 0) out[blockIdx.x] = red[0].i;
 }
 
 __global__ __launch_bounds__(256) void copy_kernel(uint4* dst, const uint4* src, int64_t n) {
@@ -134,8 +161,13 @@ int pdk_greedy_argmax(const uint16_t* logits, int B, int V, int64_t ld, int32_t*
   pdk::clear_error();
   PDK_REQUIRE(logits && out, "null pointer argument");
   PDK_REQUIRE(B >= 1 && V >= 1 && ld >= V, "bad shape B=%d V=%d ld=%lld", B, V, (long long)ld);
-  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, pdk::as_stream(stream), logits, V, ld,
-                     out);
+  const bool vec = pdk::aligned16(logits) && ld % 8 == 0 && V % 8 == 0;
+  if (vec)
+    hipLaunchKernelGGL(argmax_kernel<true>, dim3(B), dim3(kArgThreads), 0, pdk::as_stream(stream),
+                       logits, V, ld, out);
+  else
+    hipLaunchKernelGGL(argmax_kernel<false>, dim3(B), dim3(kArgThreads), 0, pdk::as_stream(stream),
+                       logits, V, ld, out);
   return pdk::check_launch("argmax_kernel");
 }
 

@@ -1,0 +1,262 @@
+// Weight-streaming GEMMs of the decode step for gfx950:
+//   Y[B][N] = X[B][K] . W[N][K]^T            (+ R[B][N] when a residual is given)
+//   Y[B][M] = silu(X . Wg^T) * (X . Wu^T)     (W = [Wg; Wu], 2M rows: gate then up)
+// for B <= 64 streams. W is [out][in] (torch Linear layout), bf16; fp32
+// accumulation on the matrix cores; bf16 out.
+//
+// At decode batch sizes each weight element is used B times, so these GEMMs
+// are bound by HBM: the kernel's job is to read W once, as fast as HBM
+// delivers it, and keep the few activation rows in cache. Mapping:
+//   * one workgroup per kCols tiles of 16 output columns, kWaves waves
+//     splitting K in steps of 128 (wave w takes steps w, w + kWaves, ...);
+//   * per step a lane loads 4 x 16 bytes of one W row, (column lane % 16, k
+//     offsets 32c + 8 (lane / 16)), and the same k offsets of one X row (row
+//     lane % 16 of each 16-row tile), then issues 4 v_mfma_f32_16x16x32_bf16
+//     per tile: the 16x16 result tile is [stream][column];
+//   * rows past B read row B-1 and columns past N read column N-1 (in bounds,
+//     results dropped), so no masking;
+//   * the waves' partial tiles meet in LDS, and the epilogue (residual add or
+//     SwiGLU) runs on the fp32 sums before the single bf16 rounding.
+// W is read with ordinary loads: non-temporal ones measured 10-25 % slower
+// here, although a decode step streams every weight once.
+
+#include <math.h>
+
+#include "pdk_common.h"
+
+namespace {
+
+using pdk::v8;
+
+
+typedef __bf16 bf16x8_t __attribute__((__vector_size__(16)));
+typedef float f32x4 __attribute__((__vector_size__(16)));
+
+__device__ __forceinline__ f32x4 mfma(const v8& a, const v8& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+constexpr int kStepK = 128;        // k per wave step: 4 MFMA of 32
+constexpr int kWaves = 8;
+
+enum Epilogue { kPlain = 0, kResidual = 1, kSwiGLU = 2, kArgmax = 3 };
+
+// Greedy-token key of one bf16 logit: the value in an order-preserving code
+// above the complement of the column, so the unsigned maximum is the largest
+// value at its lowest column (torch.argmax: NaN above every number, the first
+// of equal values; -0 counts as +0). 0 is below every key.
+__device__ __forceinline__ uint64_t argmax_key(uint32_t h, int n) {
+  h &= 0xffffu;
+  if (h == 0x8000u) h = 0;                                   // -0 -> +0
+  uint32_t ord;
+  if ((h & 0x7fffu) > 0x7f80u) ord = 0xffffu;               // NaN
+  else ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - (uint32_t)n);
+}
+
+// Loads in flight per wave: kDepth steps of W (and X), at most 2 (deeper
+// buffers measured no faster and cost occupancy) and no more than about 160
+// VGPRs of load buffers.
+constexpr int depth_for(int tiles) {
+  return 160 / (16 * tiles) < 1 ? 1 : 160 / (16 * tiles) > 2 ? 2 : 160 / (16 * tiles);
+}
+
+// kTiles = ceil(B / 16) row tiles; kCols = 16-column tiles per workgroup (all
+// its waves share them and split K); kEpi selects the epilogue. For kSwiGLU the
+// workgroup also computes the matching up columns (rows n and M + n of W) and
+// writes silu(g) * u.
+template <int kTiles, int kCols, int kEpi>
+__global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w, int B,
+                                                            int K, int N,
+                                                            const uint16_t* r, uint16_t* y,
+                                                            uint64_t* keys) {
+  constexpr int kPairs = kEpi == kSwiGLU ? 2 : 1;
+  constexpr int kW = kPairs * kCols;                 // W tiles per step
+  constexpr int kDepth = depth_for(kTiles + kW);
+  __shared__ float red[kWaves][kW][256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, kg = lane >> 4;
+  const int n0 = blockIdx.x * 16 * kCols;
+  const uint16_t* wp[kW];
+#pragma unroll
+  for (int p = 0; p < kPairs; ++p)
+#pragma unroll
+    for (int c = 0; c < kCols; ++c)
+      wp[p * kCols + c] = w + ((int64_t)p * N + min(n0 + 16 * c + col, N - 1)) * K + kg * 8;
+  const uint16_t* xp[kTiles];
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) xp[t] = x + (int64_t)min(t * 16 + col, B - 1) * K + kg * 8;
+
+  f32x4 acc[kW][kTiles];
+#pragma unroll
+  for (int q = 0; q < kW; ++q)
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[q][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // This wave's steps are wave, wave + kWaves, ...: n_mine of them. Buffers
+  // cycle through kDepth slots; a slot past the wave's last step loads that
+  // last step again (a valid address) and its X operand is zeroed, so every
+  // load is unconditional and the tail adds nothing.
+  const int steps = K / kStepK;
+  const int n_mine = steps > wave ? (steps - wave + kWaves - 1) / kWaves : 0;
+  const int last = wave + (max(n_mine, 1) - 1) * kWaves;
+  v8 wv[kDepth][kW][4], xv[kDepth][kTiles][4];
+  auto load = [&](int slot, int j) {
+    const int k = min(wave + j * kWaves, last) * kStepK;
+#pragma unroll
+    for (int q = 0; q < kW; ++q)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) wv[slot][q][c] = pdk::ld16(wp[q] + k + 32 * c);
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xv[slot][t][c] = pdk::ld16(xp[t] + k + 32 * c);
+  };
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) load(d, d);
+  for (int j0 = 0; j0 < n_mine; j0 += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      const int j = j0 + d;
+      if (j >= n_mine) {                       // wave-uniform: zero the stale operand
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) xv[d][t][c] = pdk::zero8();
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int q = 0; q < kW; ++q)
+#pragma unroll
+          for (int t = 0; t < kTiles; ++t) acc[q][t] = mfma(xv[d][t][c], wv[d][q][c], acc[q][t]);
+      if (j + kDepth < n_mine) load(d, j + kDepth);
+    }
+  }
+
+  // acc[q][t][i] = partial Y[t*16 + 4*kg + i][column tile q, column col]; one
+  // row tile at a time through LDS, summed over the waves.
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) {
+    if (t) __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kW; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][q][(4 * kg + i) * 16 + col] = acc[q][t][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < 256 * kCols; e += kWaves * 64) {
+      const int c = e >> 8, m = t * 16 + ((e >> 4) & 15), n = n0 + 16 * c + (e & 15);
+      const bool ok = m < B && n < N;
+      float v[kPairs];
+#pragma unroll
+      for (int p = 0; p < kPairs; ++p) {
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q) sum += red[q][p * kCols + c][e & 255];
+        v[p] = sum;
+      }
+      const int64_t at = (int64_t)m * N + n;
+      float out = v[0];
+      if (kEpi == kResidual && ok) out += pdk::bf16_to_f32(r[at]);
+      if (kEpi == kSwiGLU) out = v[0] / (1.f + expf(-v[0])) * v[kPairs - 1];
+      const uint32_t h = pdk::f32_to_bf16_rne(out);
+      if (ok && y) y[at] = (uint16_t)h;
+      if (kEpi == kArgmax) {
+        // The 16 lanes e .. e|15 hold one row's 16 columns of this tile: the
+        // best of them goes to keys[m] (an atomic only when it beats the
+        // value already there, so few of the workgroups write).
+        uint64_t key = ok ? argmax_key(h, n) : 0;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          const uint64_t other = __shfl_xor(key, o);
+          key = other > key ? other : key;
+        }
+        if ((e & 15) == 0 && ok) {
+          uint64_t* slot = keys + m;
+          if (key > __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            __hip_atomic_fetch_max(slot, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  }
+}
+
+// tokens[b] = the column of keys[b]; keys[b] back to 0 for the next call.
+__global__ void argmax_finish_kernel(uint64_t* keys, int B, int32_t* tokens) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const uint64_t k = keys[b];
+  tokens[b] = (int32_t)(0xffffffffu - (uint32_t)k);
+  keys[b] = 0;
+}
+
+template <int kCols, int kEpi>
+int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
+                uint16_t* y, uint64_t* keys, hipStream_t st) {
+  const dim3 grid((N + 16 * kCols - 1) / (16 * kCols)), block(kWaves * 64);
+  switch ((B + 15) / 16) {
+    case 1: hipLaunchKernelGGL((wgemm_kernel<1, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys); break;
+    case 2: hipLaunchKernelGGL((wgemm_kernel<2, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys); break;
+    case 3: hipLaunchKernelGGL((wgemm_kernel<3, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys); break;
+    default: hipLaunchKernelGGL((wgemm_kernel<4, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys); break;
+  }
+  return pdk::check_launch("wgemm_kernel");
+}
+
+// Column tiles per workgroup. Wider tiles read each X row once for more
+// columns (X traffic from L2 is (N / 16 kCols) * B * K * 2 bytes, as much as W
+// itself at B = 16 with one tile) but leave fewer workgroups. Measured at the
+// Llama-3.1-8B shapes: gate|up (M = 14336) and the lm_head at B > 8 run best
+// with 4 tiles; N = 4096 and 6144 need every workgroup one tile gives.
+template <int kEpi>
+int launch(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
+           uint16_t* y, uint64_t* keys, hipStream_t st) {
+  const int64_t wide = (N + 63) / 64;                // workgroups with 4 tiles
+  const bool four = kEpi == kSwiGLU ? wide >= 192 : (B > 8 && wide >= 1024);
+  if (four) return launch_cols<4, kEpi>(x, w, B, K, N, r, y, keys, st);
+  return launch_cols<1, kEpi>(x, w, B, K, N, r, y, keys, st);
+}
+
+int check_shape(const void* x, const void* w, const void* y, int B, int K, int N) {
+  PDK_REQUIRE(x && w && y, "null pointer argument");
+  PDK_REQUIRE(B >= 1 && B <= 64, "B must be in [1, 64] (got %d)", B);
+  PDK_REQUIRE(K >= kStepK && K % kStepK == 0, "K must be a positive multiple of %d (got %d)",
+              kStepK, K);
+  PDK_REQUIRE(N >= 1, "N must be positive (got %d)", N);
+  PDK_REQUIRE(pdk::aligned16(x) && pdk::aligned16(w), "x and w must be 16-byte aligned");
+  return PDK_OK;
+}
+
+}  // namespace
+
+extern "C" int pdk_linear(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                          const uint16_t* residual, uint16_t* y, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_shape(x, w, y, B, K, N)) return rc;
+  if (residual)
+    return launch<kResidual>(x, w, B, K, N, residual, y, nullptr, pdk::as_stream(stream));
+  return launch<kPlain>(x, w, B, K, N, nullptr, y, nullptr, pdk::as_stream(stream));
+}
+
+extern "C" int pdk_linear_swiglu(const uint16_t* x, const uint16_t* w_gate_up, int B, int K, int M,
+                                 uint16_t* y, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_shape(x, w_gate_up, y, B, K, M)) return rc;
+  return launch<kSwiGLU>(x, w_gate_up, B, K, M, nullptr, y, nullptr, pdk::as_stream(stream));
+}
+
+extern "C" int pdk_linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                                 uint16_t* logits, uint64_t* keys, int32_t* tokens,
+                                 uintptr_t stream) {
+  pdk::clear_error();
+  // y may be null here: check_shape only needs a non-null stand-in.
+  if (int rc = check_shape(x, w, keys, B, K, N)) return rc;
+  PDK_REQUIRE(tokens, "null pointer argument");
+  PDK_REQUIRE(((uintptr_t)keys & 7u) == 0, "keys must be 8-byte aligned");
+  hipStream_t st = pdk::as_stream(stream);
+  if (int rc = launch<kArgmax>(x, w, B, K, N, nullptr, logits, keys, st)) return rc;
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, keys, B, tokens);
+  return pdk::check_launch("argmax_finish_kernel");
+}

@@ -3,21 +3,22 @@
 Replaces the reference's BatchDecodeEngine.step / step_logits
 (engines/decode_batch.py:422-442) and its compiled DecodeLayer
 (kernels/decode_batch.py:56-91) plus the batched lm_head and greedy argmax
-(engines/decode_batch.py:162-171). Per layer:
+(engines/decode_batch.py:162-171). Per layer, one launch per line:
 
-  rmsnorm(x [+ previous residual]) -> h            pdk_rmsnorm (residual add fused)
-  h @ Wqkv -> qkv                                  GEMM (hipBLASLt via torch)
-  RoPE(q, k) + new k, v into the paged cache        pdk_rope_cache_append
-  attention over slots 0..pos                      pdk_decode_attn
-  ao @ Wo -> o; x += o; rmsnorm -> h2              GEMM, pdk_rmsnorm
-  h2 @ [Wg | Wu] -> gu; silu(g) * u -> a           GEMM, pdk_swiglu
-  a @ Wd -> residual for the next layer            GEMM
+  h = rmsnorm(x)                                   pdk_rmsnorm
+  qkv = h . Wqkv^T                                 pdk_linear
+  RoPE(q, k); new k, v into the paged cache         pdk_rope_cache_append
+  ao = attention over slots 0..pos                 pdk_decode_attn (+ its merge)
+  x = x + ao . Wo^T                                pdk_linear, residual fused
+  h = rmsnorm(x)                                   pdk_rmsnorm
+  a = silu(h . Wg^T) * (h . Wu^T)                  pdk_linear_swiglu
+  x = x + a . Wd^T                                 pdk_linear, residual fused
 
-then the final norm (with the last residual), the lm_head GEMM and the
-first-maximum argmax (pdk_greedy_argmax). Weights are stored [in, out]
-contiguous, with q, k, v and gate, up fused, so every projection is one plain
-2-D GEMM. Activations are bf16 at every tensor boundary, as the reference's
-are; the kernels compute in fp32 inside.
+then the final norm and the lm_head GEMM with the first-maximum argmax in its
+epilogue (pdk_linear_argmax). Weights are [out, in] contiguous (torch Linear
+layout) with q|k|v and gate|up stacked, so each projection is one pass over
+its weights. Activations are bf16 at every tensor boundary, as the
+reference's are; the kernels accumulate in fp32 and round once.
 """
 import contextlib
 import math
@@ -70,7 +71,9 @@ class LlamaConfig:
 
 
 class LlamaWeights:
-    """Decode-step weights, [in, out] contiguous bf16 on one device."""
+    """Decode-step weights, [out, in] contiguous bf16 on one device: wqkv
+    [L, (NH + 2 NKV) HD, H], wo [L, H, NH HD], wgu [L, 2M, H] (gate rows then
+    up rows), wd [L, H, M], embed [V, H], lm_head [V, H]."""
 
     def __init__(self, cfg, norm1, wqkv, wo, norm2, wgu, wd, embed, norm_f, lm_head):
         self.cfg = cfg
@@ -90,14 +93,14 @@ class LlamaWeights:
 
         return cls(cfg,
                    norm1=w(L, H, scale=0.05, mean=1.0),
-                   wqkv=w(L, H, cfg.qkv_dim),
-                   wo=w(L, cfg.n_heads * cfg.head_dim, H),
+                   wqkv=w(L, cfg.qkv_dim, H),
+                   wo=w(L, H, cfg.n_heads * cfg.head_dim),
                    norm2=w(L, H, scale=0.05, mean=1.0),
-                   wgu=w(L, H, 2 * M),
-                   wd=w(L, M, H),
+                   wgu=w(L, 2 * M, H),
+                   wd=w(L, H, M),
                    embed=w(cfg.vocab, H, scale=1.0),
                    norm_f=w(H, scale=0.05, mean=1.0),
-                   lm_head=w(H, cfg.vocab))
+                   lm_head=w(cfg.vocab, H))
 
     def nbytes(self):
         return sum(t.numel() * t.element_size() for t in
@@ -122,18 +125,19 @@ class LlamaDecoder:
         self.qkv = e(B, cfg.qkv_dim)
         self.q = e(B, cfg.n_heads, cfg.head_dim)
         self.ao = e(B, cfg.n_heads, cfg.head_dim)
-        self.o = e(B, H)
-        self.gu, self.act = e(B, 2 * cfg.inter), e(B, cfg.inter)
-        self.mlp = e(B, H)
+        self.act = e(B, cfg.inter)
         self.logits = e(B, cfg.vocab)
         self.tokens = torch.empty(B, dtype=torch.int32, device=dev)
+        self.keys = torch.zeros(B, dtype=torch.int64, device=dev)    # argmax scratch, kept zero
         self.inv = cfg.inv_freq().to(dev)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
         self._ws = None
         # Per-layer operands resolved once: the step loop makes no views.
         w = weights
-        self._layers = [(w.norm1[i].data_ptr(), w.wqkv[i], w.wo[i], w.norm2[i].data_ptr(),
-                         w.wgu[i], w.wd[i], cache.k[i].data_ptr(), cache.v[i].data_ptr())
+        if max_batch > 64:
+            raise ValueError("the decode GEMMs take at most 64 streams")
+        self._layers = [tuple(t.data_ptr() for t in (w.norm1[i], w.wqkv[i], w.wo[i], w.norm2[i],
+                                                     w.wgu[i], w.wd[i], cache.k[i], cache.v[i]))
                         for i in range(cfg.n_layers)]
 
     def _workspace(self, B, max_ctx):
@@ -149,8 +153,8 @@ class LlamaDecoder:
         holding at least ceil(ctx/16) blocks each; max_ctx (<= max_blocks*16)
         sizes the attention's split plan and should cover every ctx_lens. Returns
         the next token per stream (int32 [B], device) and leaves the final hidden
-        state in self.x[:B] (before the final norm), the logits in
-        self.logits[:B]. ``stream``: a torch stream for every launch (default:
+        state in self.x[:B] (the residual stream before the final norm) and the
+        logits in self.logits[:B]. ``stream``: a torch stream for every launch (default:
         the current stream)."""
         cfg, w, cache = self.cfg, self.w, self.cache
         B = tokens.shape[0]
@@ -165,37 +169,33 @@ class LlamaDecoder:
                 or not tables.is_contiguous():
             raise ValueError("tables must be contiguous int32 [B, max_blocks]")
         st = stream_handle(stream)
-        H, NH, NKV, HD = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
-        x, h, qkv, q, ao = self.x[:B], self.h[:B], self.qkv[:B], self.q[:B], self.ao[:B]
-        o, gu, act, mlp = self.o[:B], self.gu[:B], self.act[:B], self.mlp[:B]
-        ao2 = ao.view(B, NH * HD)
+        H, NH, NKV, HD, M = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.inter
+        QKV, eps = cfg.qkv_dim, cfg.eps
+        x = self.x[:B]
         ws = self._workspace(B, max_ctx)
         ws_ptr = ws.data_ptr() if ws is not None else None
         ws_bytes = ws.numel() * 4 if ws is not None else 0
         mb, nb = tables.shape[1], cache.num_blocks
         tp, cp = tables.data_ptr(), ctx_lens.data_ptr()
-        xp, hp, qkvp, qp, aop = x.data_ptr(), h.data_ptr(), qkv.data_ptr(), q.data_ptr(), ao.data_ptr()
-        op, mlpp, inv, ldq = o.data_ptr(), mlp.data_ptr(), self.inv.data_ptr(), qkv.stride(0)
+        xp, hp, qkvp, qp = x.data_ptr(), self.h.data_ptr(), self.qkv.data_ptr(), self.q.data_ptr()
+        aop, actp, inv = self.ao.data_ptr(), self.act.data_ptr(), self.inv.data_ptr()
         call = _lib.call
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
             torch.index_select(w.embed, 0, tokens.long(), out=x)
-            for li, (n1, wqkv, wo, n2, wgu, wd, ck, cv) in enumerate(self._layers):
-                call("pdk_rmsnorm", xp, mlpp if li else None, n1, B, H, cfg.eps, hp, st)
-                torch.matmul(h, wqkv, out=qkv)
-                call("pdk_rope_cache_append", qkvp, ldq, qp, inv, cp, tp, mb, ck, cv, nb, B, NH,
+            for n1, wqkv, wo, n2, wgu, wd, ck, cv in self._layers:
+                call("pdk_rmsnorm", xp, None, n1, B, H, eps, hp, st)
+                call("pdk_linear", hp, wqkv, B, H, QKV, None, qkvp, st)
+                call("pdk_rope_cache_append", qkvp, QKV, qp, inv, cp, tp, mb, ck, cv, nb, B, NH,
                      NKV, HD, st)
                 call("pdk_decode_attn", qp, ck, cv, nb, tp, mb, cp, int(max_ctx), B, NH, NKV, HD,
                      self.scale, ws_ptr, ws_bytes, aop, st)
-                torch.matmul(ao2, wo, out=o)
-                call("pdk_rmsnorm", xp, op, n2, B, H, cfg.eps, hp, st)
-                torch.matmul(h, wgu, out=gu)
-                call("pdk_swiglu", gu.data_ptr(), B, cfg.inter, act.data_ptr(), st)
-                torch.matmul(act, wd, out=mlp)
-            call("pdk_rmsnorm", xp, mlpp, w.norm_f.data_ptr(), B, H, cfg.eps, hp, st)
-            logits = self.logits[:B]
-            torch.matmul(h, w.lm_head, out=logits)
-            call("pdk_greedy_argmax", logits.data_ptr(), B, cfg.vocab, logits.stride(0),
-                 self.tokens.data_ptr(), st)
+                call("pdk_linear", aop, wo, B, NH * HD, H, xp, xp, st)
+                call("pdk_rmsnorm", xp, None, n2, B, H, eps, hp, st)
+                call("pdk_linear_swiglu", hp, wgu, B, H, M, actp, st)
+                call("pdk_linear", actp, wd, B, M, H, xp, xp, st)
+            call("pdk_rmsnorm", xp, None, w.norm_f.data_ptr(), B, H, eps, hp, st)
+            call("pdk_linear_argmax", hp, w.lm_head.data_ptr(), B, H, cfg.vocab,
+                 self.logits.data_ptr(), self.keys.data_ptr(), self.tokens.data_ptr(), st)
         return self.tokens[:B]
 
     def capture(self, tokens, ctx_lens, tables, max_ctx):

@@ -1,9 +1,10 @@
-"""torch-facing wrappers of the decode step's non-GEMM kernels.
+"""torch-facing wrappers of the decode step's kernels.
 
 Replace rms_dsl + zipadd_dsl (kernels/dsl_batch.py:22-53), the RoPE rotation
 and one-hot cache injection of DecodeLayer.forward (kernels/decode_batch.py:
-69-82) and swiglu_dsl (kernels/dsl_batch.py:55-71). bf16 tensors on the
-device; fp32 arithmetic inside the kernels.
+69-82), swiglu_dsl (kernels/dsl_batch.py:55-71) and the layer's projection
+matmuls (kernels/decode_batch.py:73-91). bf16 tensors on the device; fp32
+arithmetic inside the kernels.
 """
 import torch
 
@@ -76,3 +77,64 @@ def swiglu(gate_up, out=None, stream=None):
         out = torch.empty((B, M), dtype=gate_up.dtype, device=gate_up.device)
     _lib.call("pdk_swiglu", gate_up.data_ptr(), B, M, out.data_ptr(), stream_handle(stream))
     return out
+
+
+def _check_linear(x, w, rows_per_col=1):
+    _need(x, "x")
+    _need(w, "w")
+    if x.dim() != 2 or not x.is_contiguous() or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("x [B, K] and w [N, K] must be contiguous 2-D tensors")
+    if x.shape[1] != w.shape[1]:
+        raise ValueError(f"x has K={x.shape[1]}, w has K={w.shape[1]}")
+    if w.shape[0] % rows_per_col:
+        raise ValueError("w must hold 2M rows (gate rows, then up rows)")
+    return x.shape[0], x.shape[1], w.shape[0] // rows_per_col
+
+
+def linear(x, w, residual=None, out=None, stream=None):
+    """x [B, K] . w[N, K]^T (+ residual [B, N]) -> [B, N], B <= 64 (w in torch
+    Linear layout). ``out`` may be ``residual`` (an in-place residual add)."""
+    B, K, N = _check_linear(x, w)
+    if residual is not None:
+        _need(residual, "residual")
+        if tuple(residual.shape) != (B, N) or not residual.is_contiguous():
+            raise ValueError(f"residual must be contiguous [{B}, {N}]")
+    if out is None:
+        out = torch.empty((B, N), dtype=x.dtype, device=x.device)
+    elif tuple(out.shape) != (B, N) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{B}, {N}]")
+    _lib.call("pdk_linear", x.data_ptr(), w.data_ptr(), B, K, N,
+              residual.data_ptr() if residual is not None else None, out.data_ptr(),
+              stream_handle(stream))
+    return out
+
+
+def linear_swiglu(x, w_gate_up, out=None, stream=None):
+    """silu(x . wg^T) * (x . wu^T) -> [B, M] for w_gate_up = [wg; wu] [2M, K]."""
+    B, K, M = _check_linear(x, w_gate_up, rows_per_col=2)
+    if out is None:
+        out = torch.empty((B, M), dtype=x.dtype, device=x.device)
+    elif tuple(out.shape) != (B, M) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{B}, {M}]")
+    _lib.call("pdk_linear_swiglu", x.data_ptr(), w_gate_up.data_ptr(), B, K, M, out.data_ptr(),
+              stream_handle(stream))
+    return out
+
+
+def linear_argmax(x, w, keys, tokens=None, logits=None, stream=None):
+    """Greedy tokens of x . w^T (the lm_head): the first-maximum argmax of each
+    row of the bf16 logits, computed in the GEMM's epilogue. ``keys`` is an
+    int64 [>= B] device scratch holding zeros (left zero); ``logits`` [B, N]
+    receives the logits when given. Returns int32 [B] tokens."""
+    B, K, N = _check_linear(x, w)
+    if not isinstance(keys, torch.Tensor) or not keys.is_cuda or keys.dtype != torch.int64 \
+            or keys.numel() < B or not keys.is_contiguous():
+        raise ValueError(f"keys must be a contiguous CUDA int64 tensor of >= {B} zeros")
+    if tokens is None:
+        tokens = torch.empty(B, dtype=torch.int32, device=x.device)
+    if logits is not None and (tuple(logits.shape) != (B, N) or not logits.is_contiguous()):
+        raise ValueError(f"logits must be contiguous [{B}, {N}]")
+    _lib.call("pdk_linear_argmax", x.data_ptr(), w.data_ptr(), B, K, N,
+              logits.data_ptr() if logits is not None else None, keys.data_ptr(),
+              tokens.data_ptr(), stream_handle(stream))
+    return tokens

@@ -115,6 +115,75 @@ def test_swiglu(cuda, B, M):
     np.testing.assert_allclose(got, od.swiglu(_f32(gu)), rtol=HALF_ULP, atol=1e-6)
 
 
+@pytest.mark.parametrize("B,K,N", [(1, 128, 16), (4, 4096, 6144), (16, 14336, 4096),
+                                   (17, 512, 48), (33, 1024, 256), (64, 256, 32),
+                                   (5, 256, 1000), (2, 128, 7)])
+def test_linear(cuda, B, K, N):
+    """y = x . w^T, then y = r + x . w^T in place: fp32 sums, one bf16 rounding."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B * 1000 + N)
+    x, w, r = rand_bf16(rng, (B, K)), rand_bf16(rng, (N, K), 0.05), rand_bf16(rng, (B, N), 4.0)
+    xd, wd, rd = to_dev(x), to_dev(w), to_dev(r)
+    print(f"linear B={B} K={K} N={N}", flush=True)
+    y = K_.linear(xd, wd)
+    K_.linear(xd, wd, residual=rd, out=rd)
+    torch.cuda.synchronize()
+    want = _f32(x).astype(np.float64) @ _f32(w).astype(np.float64).T
+    tol = 1e-5 * np.abs(want).max()                 # fp32 summation order
+    np.testing.assert_allclose(_f32(to_host(y)), want, rtol=HALF_ULP, atol=tol)
+    np.testing.assert_allclose(_f32(to_host(rd)), want + _f32(r), rtol=HALF_ULP, atol=tol)
+
+
+@pytest.mark.parametrize("B,K,M", [(4, 4096, 14336), (16, 128, 16), (40, 512, 64), (3, 256, 24)])
+def test_linear_swiglu(cuda, B, K, M):
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B + K + M)
+    x, w = rand_bf16(rng, (B, K)), rand_bf16(rng, (2 * M, K), 0.05)
+    print(f"linear_swiglu B={B} K={K} M={M}", flush=True)
+    y = K_.linear_swiglu(to_dev(x), to_dev(w))
+    torch.cuda.synchronize()
+    gu = _f32(x).astype(np.float64) @ _f32(w).astype(np.float64).T
+    want = od.swiglu(gu)
+    tol = 1e-5 * np.abs(gu).max() ** 2
+    np.testing.assert_allclose(_f32(to_host(y)), want, rtol=HALF_ULP, atol=tol)
+
+
+@pytest.mark.parametrize("B,K,N", [(16, 4096, 128256), (4, 4096, 128256), (3, 256, 1000),
+                                   (1, 128, 7)])
+def test_linear_argmax(cuda, B, K, N):
+    """The fused lm_head argmax equals pdk_greedy_argmax over the same bf16
+    logits: duplicated weight rows make exact ties (the first column wins), a
+    NaN row wins outright, and a second call sees the scratch left at zero."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B + N)
+    x, w = rand_bf16(rng, (B, K)), rand_bf16(rng, (N, K), 0.05)
+    wd = to_dev(w)
+    if N > 500:
+        logits = K_.linear(to_dev(x), wd).float().cpu().numpy()
+        top = int(np.argmax(logits[0]))
+        wd[top - 3 if top >= 3 else top + 1].copy_(wd[top])          # a tie with row 0's best
+        wd[N - 1].fill_(float("nan"))                               # NaN in every row
+    keys = torch.zeros(B, dtype=torch.int64, device=cuda)
+    xd = to_dev(x)
+    print(f"linear_argmax B={B} K={K} N={N}", flush=True)
+    for call in range(2):
+        lg = torch.empty((B, N), dtype=torch.bfloat16, device=cuda)
+        tok = K_.linear_argmax(xd, wd, keys, logits=lg)
+        ref = K_.greedy_argmax(lg)
+        torch.cuda.synchronize()
+        assert torch.equal(keys, torch.zeros_like(keys))
+        np.testing.assert_array_equal(tok.cpu().numpy(), ref.cpu().numpy())
+        np.testing.assert_array_equal(to_host(lg), to_host(K_.linear(xd, wd)))
+        if N > 500 and call == 0:
+            assert (tok.cpu().numpy() == N - 1).all()
+            wd[N - 1].zero_()                                      # second call: the tie decides
+            torch.cuda.synchronize()
+        elif N > 500:
+            assert tok[0].item() == min(top - 3 if top >= 3 else top, top)
+        else:
+            xd = xd.flip(0).contiguous()
+
+
 # ---- whole steps -------------------------------------------------------------
 
 class _OCfg:
@@ -124,10 +193,12 @@ class _OCfg:
 
 
 def _oracle_weights(w):
+    """The engine's [out, in] bf16 weights as the oracle's [in, out] float32."""
     f = lambda t: t.float().cpu().numpy()   # noqa: E731
-    return {"embed": f(w.embed), "norm_f": f(w.norm_f), "lm_head": f(w.lm_head),
-            "layers": [(f(w.norm1[i]), f(w.wqkv[i]), f(w.wo[i]), f(w.norm2[i]), f(w.wgu[i]),
-                        f(w.wd[i])) for i in range(w.cfg.n_layers)]}
+    T = lambda t: np.ascontiguousarray(f(t).T)   # noqa: E731
+    return {"embed": f(w.embed), "norm_f": f(w.norm_f), "lm_head": T(w.lm_head),
+            "layers": [(f(w.norm1[i]), T(w.wqkv[i]), T(w.wo[i]), f(w.norm2[i]), T(w.wgu[i]),
+                        T(w.wd[i])) for i in range(w.cfg.n_layers)]}
 
 
 def _prefilled(cuda, cfg, ctx, steps, rng):

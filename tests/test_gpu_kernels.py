@@ -212,17 +212,26 @@ def test_cache_append_then_attend(cuda):
     np.testing.assert_allclose(out.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
 
 
-def test_greedy_argmax(cuda):
+@pytest.mark.parametrize("B,V,ld", [(16, 128256, 128256), (3, 1001, 1001), (2, 1000, 1024),
+                                    (1, 8, 8)])
+def test_greedy_argmax(cuda, B, V, ld):
+    """16-byte vector path (aligned rows, V % 8 == 0) and the scalar path."""
     from rngd_pd_amd.kernels import greedy_argmax
-    rng = np.random.default_rng(2)
-    B, V = 16, 128256
-    x = rand_bf16(rng, (B, V), scale=3.0)
-    x[3, 1000] = x[3, 5] = 0x4300        # a tie (128.0): the first index wins
-    x[5, 77] = 0x7FC0                     # NaN ranks first
-    want = orc.greedy_argmax(x)
-    got = greedy_argmax(to_dev(x)).cpu().numpy()
+    rng = np.random.default_rng(2 + V)
+    full = rand_bf16(rng, (B, ld), scale=3.0)
+    x = full[:, :V]
+    x[0, V - 1] = 0x4380                  # 256.0 in the last column
+    if B > 3:
+        x[3, V - 2] = x[3, 5] = 0x4400    # a tie (512.0): the first index wins
+    if B > 5:
+        x[5, 900] = 0x7FC0                # NaN ranks first, and the first NaN wins
+        x[5, 77] = 0xFFC1
+    want = orc.greedy_argmax(np.ascontiguousarray(x))
+    got = greedy_argmax(to_dev(full)[:, :V]).cpu().numpy()
     np.testing.assert_array_equal(got, want)
-    assert want[3] == 5 and want[5] == 77
+    assert want[0] == V - 1
+    if B > 5:
+        assert want[3] == 5 and want[5] == 77
 
 
 def test_pack_narrow_leaves_tail(cuda):
