@@ -18,6 +18,8 @@ decode_batch tokens/s alongside.
   step      the full Llama-3.1-8B decode step (random-init weights) at B=4 and
             B=16, context 512, eager and from a HIP graph, beside the
             reference's published 21.54 / 35.54 ms per step.
+  serve     2 prefill producers + 1 decode consumer on this GPU (config 5):
+            64 requests, Poisson(20/s), prompts U[128,1024], 128 greedy tokens.
   cpu       the oracle's restatement of the reference CPU shm path (ser -> /dev/shm
             -> deser -> f32 place) on a bounded sample of the same requests.
 
@@ -49,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU baseline sample (0 skips it)")
-    ap.add_argument("--only", choices=["all", "handoff", "decode", "step", "long", "copy"],
+    ap.add_argument("--only", choices=["all", "handoff", "decode", "step", "long", "serve", "copy"],
                     default="all",
                     help="restrict the run (for profiler passes)")
     ap.add_argument("--copy-mib", type=int, default=1024,
@@ -484,6 +486,26 @@ def bench_step(args, torch, dev, out, batches=(4, 16), ctx=512):
     torch.cuda.empty_cache()
 
 
+def bench_serve(args, out):
+    """Config 5: two prefill producer processes and one decode consumer on this
+    GPU (same-GPU IPC handoff, continuous batching at width 16), 64 requests
+    with Poisson(20/s) arrivals, prompts U[128,1024], 128 greedy tokens each,
+    random-init Llama-3.1-8B weights. Runs rngd_pd_amd.serving.pd_one_gpu as a
+    child process and records its summary."""
+    import subprocess
+    cmd = [sys.executable, "-u", "-m", "rngd_pd_amd.serving.pd_one_gpu", "run",
+           "--requests", "64", "--rate", "20", "--min-len", "128", "--max-len", "1024",
+           "--max-new", "128", "--batch", "16", "--producers", "2", "--seed", "0"]
+    log("serve: " + " ".join(cmd[3:]))
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=900,
+                       cwd=os.path.dirname(os.path.abspath(__file__)))
+    if r.returncode != 0:
+        raise RuntimeError(f"pd_one_gpu exited with {r.returncode}")
+    summary = json.loads([ln for ln in r.stdout.splitlines() if ln.startswith("{")][-1])
+    out["extra"]["pd_one_gpu"] = summary
+    log(f"serve: {summary}")
+
+
 def bench_long(args, torch, dev, out, n_req=16, T=2048, hidden=4096):
     """Long-context layer-pipelined save: n_req requests of T tokens (Llama-3.1-8B
     KV), 32 layers. Per layer the "prefill" runs a bf16 GEMM [n_req*T, hidden] x
@@ -650,6 +672,8 @@ def main():
         bench_step(args, torch, dev, out)
     if args.only in ("all", "long"):
         bench_long(args, torch, dev, out)
+    if args.only in ("all", "serve"):
+        bench_serve(args, out)
     if args.only == "all" and args.cpu_seconds > 0:
         bench_cpu(args, out)
     if args.only == "step":

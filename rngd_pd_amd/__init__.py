@@ -7,6 +7,9 @@ Layers, in dependency order (each only imports the ones above it):
   connector   bf16 wire, Transport ABC + /dev/shm transport, frame codec,
               RngdKVConnector (the vLLM KVConnector surface)
   airm        the rm-core ``airm.kv_transports`` ``shm`` adapter
-  engines     paged KV cache + block allocator, batched decode attention
+  engines     paged KV cache + block allocator, batched decode attention, the
+              Llama decode step (LlamaDecoder) and prefill (LlamaPrefill)
+  serving     continuous scheduling of decode streams onto the paged cache,
+              prefetch, and the one-GPU prefill/decode run (pd_one_gpu)
 """
 __version__ = "0.1.0"

@@ -117,7 +117,7 @@ class LlamaDecoder:
                                                                   cfg.head_dim):
             raise ValueError("cache shape does not match the model")
         self.w, self.cache = weights, cache
-        dev = self.device = cache.device
+        dev = self.device = cache.k.device          # the real device (cuda:N)
         B, H = max_batch, cfg.hidden
         self.max_batch = B
         e = lambda *s: torch.empty(s, dtype=BF16, device=dev)   # noqa: E731
@@ -139,6 +139,11 @@ class LlamaDecoder:
         self._layers = [tuple(t.data_ptr() for t in (w.norm1[i], w.wqkv[i], w.wo[i], w.norm2[i],
                                                      w.wgu[i], w.wd[i], cache.k[i], cache.v[i]))
                         for i in range(cfg.n_layers)]
+
+    def reserve(self, max_ctx):
+        """Allocate the attention workspace for max_batch streams at ``max_ctx``
+        now, so that no later step (or graph capture) allocates it."""
+        self._workspace(self.max_batch, max_ctx)
 
     def _workspace(self, B, max_ctx):
         need = _attn.workspace_bytes(B, self.cfg.n_heads, max_ctx, self.cfg.head_dim)
@@ -212,6 +217,8 @@ class LlamaDecoder:
             self.step(tokens, ctx_lens, tables, max_ctx)
         torch.cuda.current_stream(self.device).wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        # Thread-local capture: other threads of the process (cache loaders)
+        # may synchronise on their own streams while this one captures.
+        with torch.cuda.graph(graph, capture_error_mode="thread_local"):
             self.step(tokens, ctx_lens, tables, max_ctx)
         return graph

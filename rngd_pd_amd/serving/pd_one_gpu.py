@@ -1,0 +1,369 @@
+"""Prefill/decode disaggregation on one GPU: N prefill producers, one decode consumer.
+
+The reference runs prefill and decode as separate workers behind a gateway
+(serving/cluster.py: PrefillWorker, DecodeWorkerBase, _ContinuousScheduler)
+and hands KV over /dev/shm. Here all of them share one MI355X:
+
+  orchestrator (no GPU)  seeded Poisson arrivals, prompts routed round-robin
+       |  JSON lines over pipes
+  producer x N           LlamaPrefill -> RngdKVConnector.save_kv_layer per layer
+       |                 on the ipc transport (frames stay in the producer's HBM)
+  consumer               ContinuousScheduler: loader threads scatter each frame
+                         from the producer's memory into the paged cache; the
+                         decode step (LlamaDecoder, HIP graphs) runs the batch
+
+Every process builds the same random-init weights from one seed (no
+checkpoint). The orchestrator reports time to first token (arrival to the
+producer's first token), per-request end-to-end latency, decode TPOT and the
+output-token throughput of the run.
+
+  python -m rngd_pd_amd.serving.pd_one_gpu run [--requests 64 --rate 20 ...]
+  python -m rngd_pd_amd.serving.pd_one_gpu control ...   (one process, B=1, for tests)
+"""
+import argparse
+import json
+import math
+import os
+import queue
+import shutil
+import subprocess
+import sys
+import tempfile
+import threading
+import time
+
+_LOCK = threading.Lock()
+
+
+def _say(obj):
+    with _LOCK:
+        sys.stdout.write(json.dumps(obj) + "\n")
+        sys.stdout.flush()
+
+
+def _log(msg):
+    print(f"[pd] {msg}", file=sys.stderr, flush=True)
+
+
+def model_config(args):
+    from ..engines.llama_decode import LlamaConfig
+    if args.small:
+        return LlamaConfig(hidden=512, n_heads=8, n_kv_heads=2, head_dim=128, inter=1024,
+                           vocab=1000, n_layers=args.layers or 2)
+    return LlamaConfig(n_layers=args.layers or 32)
+
+
+def frame_tokens(args):
+    return (args.max_len + 15) // 16 * 16
+
+
+def workload(args):
+    """Seeded arrivals (exponential gaps at ``rate``/s), prompt lengths
+    U[min_len, max_len] and prompt token ids U[0, vocab)."""
+    import numpy as np
+    rng = np.random.default_rng(args.seed)
+    vocab = model_config(args).vocab
+    t, out = 0.0, []
+    for i in range(args.requests):
+        t += float(rng.exponential(1.0 / args.rate))
+        n = int(rng.integers(args.min_len, args.max_len + 1))
+        out.append({"req": f"q{i}", "arrival": t, "tokens": rng.integers(0, vocab, n).tolist()})
+    return out
+
+
+# ---------------------------------------------------------------------------
+# producer
+# ---------------------------------------------------------------------------
+def producer(args):
+    import torch
+    from ..connector.ipc import IpcTransport
+    from ..connector.rngd_kv import KVConnectorRole, RngdKVConnector
+    from ..engines.llama_decode import LlamaWeights
+    from ..engines.llama_prefill import LlamaPrefill
+    cfg = model_config(args)
+    w = LlamaWeights.random(cfg, seed=args.seed, device="cuda")
+    pre = LlamaPrefill(w, max_tokens=frame_tokens(args))
+    t = IpcTransport(args.root, n_slots=args.ipc_slots)
+    S = frame_tokens(args)
+    pre.forward([1] * 16)                                    # warm the library paths
+    torch.cuda.synchronize()
+    _say({"ev": "ready", "role": "producer", "pid": os.getpid()})
+    for line in sys.stdin:
+        msg = json.loads(line)
+        if msg.get("cmd") == "stop":
+            break
+        req, tokens = msg["req"], msg["tokens"]
+        t0 = time.monotonic()
+        conn = RngdKVConnector(KVConnectorRole.WORKER, req_id=req, transport=t,
+                               n_layers=cfg.n_layers, frame_tokens=S)
+        T = len(tokens)
+        first, _k, _v = pre.forward(
+            tokens, on_layer=lambda li, k, v: conn.save_kv_layer(f"layer.{li}", (k, v),
+                                                                 num_tokens=T))
+        conn.wait_for_save()
+        conn.close()
+        _say({"ev": "prefilled", "req": req, "first": first, "P": T, "t": time.monotonic(),
+              "prefill_ms": round((time.monotonic() - t0) * 1e3, 2)})
+    t.close()
+    _say({"ev": "exit", "role": "producer"})
+
+
+# ---------------------------------------------------------------------------
+# consumer
+# ---------------------------------------------------------------------------
+def consumer(args):
+    import torch
+    from ..connector.ipc import IpcTransport, close_opened
+    from ..connector.rngd_kv import KVConnectorRole, RngdKVConnector
+    from ..engines.llama_decode import LlamaDecoder, LlamaWeights
+    from ..engines.paged_cache import PagedKVCache
+    from .scheduler import ContinuousScheduler
+    cfg = model_config(args)
+    w = LlamaWeights.random(cfg, seed=args.seed, device="cuda")
+    per = math.ceil((args.max_len + args.max_new) / 16)
+    cache = PagedKVCache(cfg.n_layers, per * (args.requests + args.batch), cfg.n_kv_heads,
+                         cfg.head_dim, device="cuda")
+    dec = LlamaDecoder(w, cache, max_batch=args.batch)
+    t = IpcTransport(args.root)
+    S = frame_tokens(args)
+
+    def produce(item):
+        t0 = time.monotonic()
+        view = cache.view(item["req_id"], item["P"], S)
+        conn = RngdKVConnector(KVConnectorRole.WORKER, req_id=item["req_id"], transport=t,
+                               n_layers=cfg.n_layers)
+        conn.register_kv_caches(view)
+        conn.start_load_kv()
+        for i in range(cfg.n_layers):
+            conn.wait_for_layer_load(f"layer.{i}")
+        conn.close()
+        return item["first"], item["P"], (time.monotonic() - t0) * 1e3
+
+    sched = ContinuousScheduler(args.batch, dec, cache, produce, max_blocks=per,
+                                use_graphs=not args.eager)
+    sched.warmup()
+    _say({"ev": "ready", "role": "consumer", "pid": os.getpid()})
+
+    def watch(item):
+        item["ev"].wait()
+        if item["err"] is not None:
+            _say({"ev": "failed", "req": item["req_id"], "error": repr(item["err"])})
+        else:
+            _say({"ev": "done", "req": item["req_id"], "t": time.monotonic(), **item["out"]})
+
+    watchers = []
+    for line in sys.stdin:
+        msg = json.loads(line)
+        if msg.get("cmd") == "stop":
+            break
+        item = sched.submit_async({"req_id": msg["req"], "first": msg["first"], "P": msg["P"],
+                                   "max_new": msg["max_new"]})
+        th = threading.Thread(target=watch, args=(item,), daemon=True)
+        th.start()
+        watchers.append(th)
+    for th in watchers:
+        th.join()
+    sched.close()
+    torch.cuda.synchronize()
+    close_opened()
+    _say({"ev": "exit", "role": "consumer", "steps": sched.steps,
+          "occupancy": round(sched.lane_steps / max(sched.steps, 1), 2)})
+
+
+# ---------------------------------------------------------------------------
+# one-process control (B = 1, no handoff between processes)
+# ---------------------------------------------------------------------------
+def control(args):
+    """Prefill and decode each request in one process, one at a time: the
+    tokens a correct disaggregated run with --batch 1 must reproduce."""
+    import torch
+    from ..engines.llama_decode import LlamaDecoder, LlamaWeights
+    from ..engines.llama_prefill import LlamaPrefill
+    from ..engines.paged_cache import PagedKVCache
+    from ..kernels import handoff as K
+    cfg = model_config(args)
+    w = LlamaWeights.random(cfg, seed=args.seed, device="cuda")
+    pre = LlamaPrefill(w, max_tokens=frame_tokens(args))
+    per = math.ceil((args.max_len + args.max_new) / 16)
+    cache = PagedKVCache(cfg.n_layers, per + 1, cfg.n_kv_heads, cfg.head_dim, device="cuda")
+    dec = LlamaDecoder(w, cache, max_batch=1)
+    S = frame_tokens(args)
+    for r in workload(args):
+        first, k, v = pre.forward(r["tokens"])
+        P = len(r["tokens"])
+        cache.allocate(r["req"], P)
+        frame = K.pack_kv(k, v, P, S)
+        K.scatter_paged(frame, cache.table(r["req"]), P, S, cache.k, cache.v)
+        outs, cur = [first], first
+        for pos in range(P, P + args.max_new - 1):
+            cache.ensure(r["req"], pos + 1)
+            blocks = cache.blocks(r["req"]) + [-1] * (per - len(cache.blocks(r["req"])))
+            tab = torch.tensor([blocks], dtype=torch.int32, device="cuda")
+            tok = dec.step(torch.tensor([cur], device="cuda"),
+                           torch.tensor([pos + 1], dtype=torch.int32, device="cuda"), tab,
+                           per * 16)
+            cur = int(tok[0].item())
+            outs.append(cur)
+        cache.free(r["req"])
+        _say({"ev": "done", "req": r["req"], "tokens": outs, "P": P})
+
+
+# ---------------------------------------------------------------------------
+# orchestrator
+# ---------------------------------------------------------------------------
+def _child(role, args, root, env):
+    cmd = [sys.executable, "-u", "-m", "rngd_pd_amd.serving.pd_one_gpu", role, "--root", root,
+           "--seed", str(args.seed), "--requests", str(args.requests),
+           "--min-len", str(args.min_len), "--max-len", str(args.max_len),
+           "--max-new", str(args.max_new), "--batch", str(args.batch),
+           "--ipc-slots", str(args.ipc_slots), "--layers", str(args.layers or 0)]
+    if args.small:
+        cmd.append("--small")
+    if args.eager:
+        cmd.append("--eager")
+    return subprocess.Popen(cmd, stdin=subprocess.PIPE, stdout=subprocess.PIPE, env=env,
+                            text=True, bufsize=1)
+
+
+def _pump(name, proc, events):
+    for line in proc.stdout:
+        line = line.strip()
+        if line.startswith("{"):
+            events.put((name, json.loads(line)))
+    events.put((name, {"ev": "eof"}))
+
+
+def run(args):
+    """Start the children, feed the workload at its arrival times, collect results."""
+    root = tempfile.mkdtemp(prefix="pd1gpu-", dir="/dev/shm" if os.path.isdir("/dev/shm") else None)
+    env = dict(os.environ, PD_SHM_ROOT=root, PD_KV_PULL_TIMEOUT=str(args.timeout),
+               PYTHONPATH=os.path.dirname(os.path.dirname(os.path.dirname(
+                   os.path.abspath(__file__)))))
+    events = queue.Queue()
+    names = ["consumer"] + [f"producer{i}" for i in range(args.producers)]
+    procs = {n: _child("consumer" if n == "consumer" else "producer", args, root, env)
+             for n in names}
+    for n, p in procs.items():
+        threading.Thread(target=_pump, args=(n, p, events), daemon=True).start()
+    results, firsts, failed = {}, {}, []
+    try:
+        ready = set()
+        deadline = time.monotonic() + args.timeout * 4
+        while len(ready) < len(procs):
+            n, ev = events.get(timeout=max(1.0, deadline - time.monotonic()))
+            if ev["ev"] == "ready":
+                ready.add(n)
+                _log(f"{n} ready")
+            elif ev["ev"] == "eof":
+                raise RuntimeError(f"{n} exited before it was ready")
+        work = workload(args)
+        t0 = time.monotonic()
+        arrivals = {r["req"]: t0 + r["arrival"] for r in work}
+        nxt = 0
+        while len(results) + len(failed) < len(work):
+            now = time.monotonic()
+            while nxt < len(work) and arrivals[work[nxt]["req"]] <= now:
+                r = work[nxt]
+                p = procs[names[1 + nxt % args.producers]]
+                p.stdin.write(json.dumps({"cmd": "prefill", "req": r["req"],
+                                          "tokens": r["tokens"]}) + "\n")
+                p.stdin.flush()
+                nxt += 1
+            wait = (arrivals[work[nxt]["req"]] - time.monotonic()) if nxt < len(work) else 1.0
+            try:
+                n, ev = events.get(timeout=max(0.0005, min(wait, 1.0)))
+            except queue.Empty:
+                continue
+            if ev["ev"] == "prefilled":
+                firsts[ev["req"]] = ev
+                procs["consumer"].stdin.write(json.dumps({
+                    "cmd": "decode", "req": ev["req"], "first": ev["first"], "P": ev["P"],
+                    "max_new": args.max_new}) + "\n")
+                procs["consumer"].stdin.flush()
+            elif ev["ev"] == "done":
+                results[ev["req"]] = ev
+            elif ev["ev"] == "failed":
+                failed.append(ev)
+                _log(f"failed: {ev}")
+            elif ev["ev"] == "eof":
+                raise RuntimeError(f"{n} exited during the run")
+        t_end = time.monotonic()
+    finally:
+        for p in procs.values():
+            try:
+                p.stdin.write(json.dumps({"cmd": "stop"}) + "\n")
+                p.stdin.flush()
+            except (BrokenPipeError, ValueError):
+                pass
+        for n, p in procs.items():
+            try:
+                p.wait(timeout=args.timeout)
+            except subprocess.TimeoutExpired:
+                p.kill()
+                p.wait()
+        shutil.rmtree(root, ignore_errors=True)
+    bad = [n for n, p in procs.items() if p.returncode != 0]
+    if bad:
+        raise RuntimeError(f"children exited with errors: {bad}")
+    ttft = sorted((firsts[r]["t"] - arrivals[r]) * 1e3 for r in results)
+    e2e = sorted((results[r]["t"] - arrivals[r]) * 1e3 for r in results)
+    tpot = sorted(results[r]["tpot_ms"] for r in results)
+    pct = lambda xs, q: xs[min(len(xs) - 1, int(q * len(xs)))] if xs else None   # noqa: E731
+    n_tok = sum(len(results[r]["tokens"]) for r in results)
+    summary = {
+        "requests": len(work), "completed": len(results), "failed": len(failed),
+        "output_tokens": n_tok, "makespan_s": round(t_end - t0, 3),
+        "output_tokens_per_s": round(n_tok / (t_end - t0), 1),
+        "ttft_ms": {"p50": round(pct(ttft, 0.5), 1), "p90": round(pct(ttft, 0.9), 1),
+                    "max": round(ttft[-1], 1)},
+        "e2e_ms": {"p50": round(pct(e2e, 0.5), 1), "p90": round(pct(e2e, 0.9), 1),
+                   "max": round(e2e[-1], 1)},
+        "tpot_ms": {"p50": round(pct(tpot, 0.5), 3), "p90": round(pct(tpot, 0.9), 3)},
+        "prefill_ms_p50": round(pct(sorted(f["prefill_ms"] for f in firsts.values()), 0.5), 1),
+        "load_ms_p50": round(pct(sorted(results[r]["load_ms"] for r in results), 0.5), 2),
+        "occupancy_p50": pct(sorted(results[r]["occupancy"] for r in results), 0.5),
+        "producers": args.producers, "batch_width": args.batch,
+    }
+    return summary, {r: results[r]["tokens"] for r in results}
+
+
+def parse(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("role", choices=["run", "producer", "consumer", "control"])
+    ap.add_argument("--root", default=None)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--requests", type=int, default=64)
+    ap.add_argument("--rate", type=float, default=20.0)
+    ap.add_argument("--min-len", type=int, default=128)
+    ap.add_argument("--max-len", type=int, default=1024)
+    ap.add_argument("--max-new", type=int, default=128)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--producers", type=int, default=2)
+    ap.add_argument("--ipc-slots", type=int, default=8)
+    ap.add_argument("--layers", type=int, default=0)
+    ap.add_argument("--small", action="store_true", help="a 2-layer test-size model")
+    ap.add_argument("--eager", action="store_true", help="decode without HIP graphs")
+    ap.add_argument("--timeout", type=float, default=120.0)
+    ap.add_argument("--tokens-out", default=None, help="write each request's tokens (JSON)")
+    return ap.parse_args(argv)
+
+
+def main(argv=None):
+    args = parse(argv)
+    if args.role == "producer":
+        producer(args)
+    elif args.role == "consumer":
+        consumer(args)
+    elif args.role == "control":
+        control(args)
+    else:
+        summary, tokens = run(args)
+        if args.tokens_out:
+            with open(args.tokens_out, "w") as f:
+                json.dump(tokens, f)
+        print(json.dumps(summary), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
