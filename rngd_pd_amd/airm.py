@@ -1,10 +1,13 @@
-"""rm-core ``airm.kv_transports`` adapter: the ``shm`` KV path (the reference's airm.py:57-221).
+"""rm-core ``airm.kv_transports`` adapters: the ``shm`` and ``tcp`` KV paths
+(the reference's airm.py:57-271).
 
-ShmTransport is both an rm-core KVTransport (plan / submit / wait / take /
-close / conformance_case) and the connector's push/pull Transport, so
-``select_transport("shm")`` hands the workers the same object the registry
-names. Entry point: ``airm.kv_transports: shm = rngd_pd_amd.airm:ShmTransport``.
-It is a host-staging path between two host-memory tiers on one machine.
+ShmTransport and TcpTransport are both rm-core KVTransports (plan / submit /
+wait / take / close / conformance_case) and the connector's push/pull
+Transports, so ``select_transport(name)`` hands the workers the same object the
+registry names. Entry points: ``airm.kv_transports: shm =
+rngd_pd_amd.airm:ShmTransport`` and ``tcp = rngd_pd_amd.airm:TcpTransport``.
+Both are host-staging paths between two host-memory tiers (shm on one
+machine, tcp between any two through a relay).
 """
 import collections
 import os
@@ -14,6 +17,7 @@ import uuid
 
 import numpy as np
 
+from .connector import tcp as _tcp
 from .connector import transport as _kv
 from .paths import SHM_ROOT
 from .rm_compat import (ContractError, KVLayout, Measurement, MemoryTier,  # noqa: F401
@@ -183,4 +187,54 @@ class ShmTransport(_KeyedKV, _kv.ShmTransport):
             raise NoHardware(f"shm root {self.root} is not writable: {e}") from e
         return (MemoryTier("shm-prefill", "host-dram", 1 << 30),
                 MemoryTier("shm-decode", "host-dram", 1 << 30),
+                KVLayout(num_layers=2, num_kv_heads=2, head_dim=8, dtype="bf16"))
+
+
+class TcpTransport(_KeyedKV, _tcp.TcpTransport):
+    """KV between two host-memory tiers on any two machines, through one relay
+    (the native librngdpd_net.so; airm.py:224-271 of the reference).
+
+    Keyword arguments: remote -- (host, port) of the relay both sides use
+    (default $AIRM_KV_TCP_ADDR), serve_port -- also run a relay in this process.
+    Every blob carries a CRC-32 checked by the relay and by the receiver, so
+    wait() is ok only for the bytes submit() sent. The relay hands a blob out
+    once, so wait() keeps it for take()."""
+
+    name = "tcp"
+    SCOPE = "only host-dram -> host-dram"
+
+    def __init__(self, remote=None, serve_port=None):
+        _tcp.TcpTransport.__init__(self, remote=remote, serve_port=serve_port)
+        self._held = {}
+        self._init_kv()
+
+    def supports(self, src, dst):
+        return src.kind == "host-dram" and dst.kind == "host-dram" and src.name != dst.name
+
+    def _detail(self):
+        return {"server": "%s:%d" % self.remote if self.remote else None}
+
+    def _fetch(self, key, timeout):
+        buf = self.pull(key, timeout=timeout)
+        with self._lock:
+            self._held[key] = buf
+        return buf
+
+    def _consume(self, key):
+        with self._lock:
+            return self._held.pop(key)
+
+    def close(self):
+        with self._lock:
+            self._pending.clear()
+            self._delivered.clear()
+            self._held.clear()
+        _tcp.TcpTransport.close(self)
+
+    def conformance_case(self):
+        """Two host tiers and a relay on a free loopback port in this process."""
+        if self.remote is None:
+            _tcp.TcpTransport.__init__(self, serve_port=0)
+        return (MemoryTier("tcp-prefill", "host-dram", 1 << 30),
+                MemoryTier("tcp-decode", "host-dram", 1 << 30),
                 KVLayout(num_layers=2, num_kv_heads=2, head_dim=8, dtype="bf16"))

@@ -1,4 +1,5 @@
-"""Compile librngdpd.so (HIP, gfx950) in place: ``python -m rngd_pd_amd.build``."""
+"""Compile librngdpd.so (HIP, gfx950) and librngdpd_net.so (host-only tcp
+transport) in place: ``python -m rngd_pd_amd.build``."""
 import os
 import subprocess
 import sys
@@ -8,6 +9,8 @@ _ROOT = os.path.dirname(_HERE)
 SOURCES = ["handoff.hip", "attention.hip", "decode_step.hip", "wgemm.hip", "staging.hip",
            "runtime.hip"]
 OUT = os.path.join(_HERE, "librngdpd.so")
+NET_SOURCES = ["net/tcpkv.cpp"]
+NET_OUT = os.path.join(_HERE, "librngdpd_net.so")
 
 
 def hipcc_command(out=OUT):
@@ -17,7 +20,27 @@ def hipcc_command(out=OUT):
             + [os.path.join(_HERE, "csrc", s) for s in SOURCES])
 
 
+def net_command(out=NET_OUT):
+    """librngdpd_net.so: host code only (g++), no GPU runtime."""
+    return (["g++", "-O3", "-std=c++17", "-fPIC", "-shared", "-pthread", "-Wall",
+             "-I", os.path.join(_ROOT, "include"), "-o", out]
+            + [os.path.join(_HERE, "csrc", s) for s in NET_SOURCES])
+
+
+def build_net(verbose=False):
+    tmp = NET_OUT + ".tmp"
+    r = subprocess.run(net_command(tmp), stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True)
+    if r.returncode != 0:
+        raise RuntimeError("g++ failed:\n" + r.stdout)
+    if verbose and r.stdout.strip():
+        print(r.stdout)
+    os.replace(tmp, NET_OUT)
+    return NET_OUT
+
+
 def build(verbose=False):
+    build_net(verbose)
     tmp = OUT + ".tmp"
     r = subprocess.run(hipcc_command(tmp), stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                        text=True)

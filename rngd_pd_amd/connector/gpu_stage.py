@@ -180,10 +180,20 @@ class FrameLoader:
         """Pull one blob into pinned memory at ``base``; returns the payload's pinned offset."""
         hlen, _ = self.env[which]
         pad = _align(hlen) - hlen
+        # A transport that can receive into a buffer (shm reads the file, tcp
+        # the socket) writes the blob straight into pinned memory. shm knows
+        # the size first; tcp finds out on arrival and keeps a blob that does
+        # not fit for the pull() below.
         size = self.t.pull_size(key, self.timeout) if hasattr(self.t, "pull_size") else None
-        if hasattr(self.t, "pull_into") and size is not None and pad + size <= self.blob_room:
-            n = self.t.pull_into(key, self.pinned.memoryview(base + pad, self.blob_room - pad),
-                                 timeout=self.timeout)
+        fits = size is None or pad + size <= self.blob_room
+        n = None
+        if hasattr(self.t, "pull_into") and fits:
+            try:
+                n = self.t.pull_into(key, self.pinned.memoryview(base + pad, self.blob_room - pad),
+                                     timeout=self.timeout)
+            except ValueError:
+                n = None
+        if n is not None:
             blob = self.pinned.memoryview(base + pad, n)
             rng = _wire.payload_range(blob, shape)
             if rng is not None:

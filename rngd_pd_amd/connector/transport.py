@@ -9,7 +9,10 @@
   FencedTransport   a tier-to-tier rm-core transport behind push/pull        (:238-289)
   select_transport  by name: $AIRM_KV_TRANSPORT, default "shm"; no fallback  (:330-350)
 
-The tcp / nixl-ucx / nixl transports of the reference are cross-node paths
+  tcp               the cross-node relay transport, native (connector/tcp.py)
+  ipc               same-GPU frames through hipIpc handles (connector/ipc.py)
+
+The nixl-ucx / nixl transports of the reference (vendor P2P paths) are
 outside this package; selecting them raises.
 """
 import os
@@ -238,8 +241,9 @@ class FencedTransport(Transport):
 
 # Our own adapters, used when the registry has no entry point of that name.
 _OWN = {"shm": "rngd_pd_amd.airm:ShmTransport",
+        "tcp": "rngd_pd_amd.airm:TcpTransport",            # native relay (librngdpd_net.so)
         "ipc": "rngd_pd_amd.connector.ipc:IpcTransport"}   # same-GPU frames in HBM
-_NOT_HERE = ("tcp", "nixl-ucx", "nixl")
+_NOT_HERE = ("nixl-ucx", "nixl")
 _CLASSES = {}          # name -> implementation class, resolved once per process
 _FENCED = {}           # name -> the process's one FencedTransport
 _SHARED = {}           # name -> the process's one instance of a connection-holding transport
@@ -291,7 +295,7 @@ def select_transport(name=None, **kw) -> Transport:
 
 
 def make_transport(backend="shm", **kw) -> Transport:
-    """Factory by backend name: inproc, shm, ipc, nixl (raises)."""
+    """Factory by backend name: inproc, shm, ipc, tcp, nixl (raises)."""
     b = backend.lower()
     if b == "inproc":
         return InProcTransport()
@@ -302,6 +306,9 @@ def make_transport(backend="shm", **kw) -> Transport:
         return IpcTransport(**kw)
     if b == "nixl":
         return NixlTransport(**kw)
-    if b in ("tcp", "nixl-ucx"):
+    if b == "tcp":
+        from .tcp import TcpTransport
+        return TcpTransport(**kw)
+    if b == "nixl-ucx":
         raise NotImplementedError(f"{backend} is a cross-node transport this package does not provide")
     raise ValueError(f"unknown transport backend: {backend}")

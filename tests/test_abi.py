@@ -91,3 +91,24 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(RuntimeError, match="not built"):
         _lib.lib()
+
+
+NET_HEADER = os.path.join(ROOT, "include", "rngdpd_net.h")
+
+
+def test_net_library_exports_its_header():
+    """librngdpd_net.so (host-only tcp transport): every function of
+    include/rngdpd_net.h is exported and bound; error codes agree."""
+    from rngd_pd_amd.connector import tcp
+    text = re.sub(r"/\*.*?\*/", "", open(NET_HEADER).read(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(pdk_[a-z0-9_]+)\s*\(", text)))
+    assert "pdk_tcp_push" in names and "pdk_crc32" in names
+    lib = tcp._net()
+    for name in names:
+        assert hasattr(lib, name), f"{name} is declared but not exported"
+        assert getattr(lib, name).argtypes is not None, f"{name} has no ctypes signature"
+    raw = open(NET_HEADER).read()
+    for name, value in (("PDK_NET_ENOSPC", tcp.ENOSPC), ("PDK_NET_ETIMEDOUT", tcp.ETIMEDOUT),
+                        ("PDK_NET_EIO", tcp.EIO)):
+        assert int(re.search(rf"#define {name}\s+\((-?\d+)\)", raw).group(1)) == value
+    assert lib.pdk_tcp_client_open(None, 1, 1.0, None) == -22

@@ -115,3 +115,56 @@ def test_device_to_device_through_selected_shm(cuda, monkeypatch):
         np.testing.assert_array_equal(to_host(back), orc.pack_kv(k, v, P, S))
         dc.close()
         kv._CLASSES.clear()
+
+
+def test_device_to_device_through_tcp_relay(cuda, monkeypatch):
+    """The device path over the native tcp relay: save packs into pinned
+    memory and pushes header + payload + trailer in one send (CRC-32 on);
+    load receives each blob straight into pinned memory and scatters it. The
+    relay's blobs are the reference protocol's files byte for byte, and the
+    paged cache holds the oracle's frame."""
+    from rngd_pd_amd.connector import transport as kv
+    from rngd_pd_amd.connector.rngd_kv import KVConnectorRole, RngdKVConnector
+    from rngd_pd_amd.connector.tcp import TcpKVServer, TcpTransport
+    from rngd_pd_amd.engines.paged_cache import PagedKVCache
+    S, P = 512, 301
+    rng = np.random.default_rng(78)
+    k, v = rand_bf16(rng, (L, S, H, D)), rand_bf16(rng, (L, S, H, D))
+    srv = TcpKVServer(0, "127.0.0.1").start()
+    port = srv.wait_ready()
+    try:
+        t_pre = TcpTransport(remote=("127.0.0.1", port))
+        pf = RngdKVConnector(KVConnectorRole.WORKER, req_id="g4", transport=t_pre, n_layers=L,
+                             frame_tokens=S)
+        dk, dv = to_dev(k), to_dev(v)
+        for i in range(L):
+            pf.save_kv_layer(f"layer.{i}", (dk[i], dv[i]), num_tokens=P)
+        pf.wait_for_save()
+        pf.close()
+        st = srv.stats
+        assert st["pushed"] == 2 * L and st["crc_errors"] == 0
+        # One layer's blobs against the reference protocol's files for the same KV.
+        Kf, Vf, frame = _frames_f32(k, v, P, S)
+        with _tmpdir() as ref:
+            owire.save_request(ref, "g4", Kf, Vf)
+            for name in ("layer.0/k", "layer.0/v"):
+                blob = bytes(t_pre.pull(f"g4/{name}", timeout=5))
+                with open(os.path.join(ref, "g4__" + name.replace("/", "__")), "rb") as f:
+                    assert blob == f.read(), name
+                t_pre.push(f"g4/{name}", blob)                   # put it back for the load
+        t_dec = TcpTransport(remote=("127.0.0.1", port))
+        cache = PagedKVCache(L, 64, H, D, device=cuda, seed=2)
+        dc = RngdKVConnector(KVConnectorRole.WORKER, req_id="g4", transport=t_dec, n_layers=L)
+        dc.register_kv_caches(cache.view("g4", P, S))
+        dc.start_load_kv()
+        for i in range(L):
+            dc.wait_for_layer_load(f"layer.{i}")
+        back = cache.read_frame("g4", P, S)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_host(back), frame)
+        dc.close()
+        assert srv.stats["keys"] == 0
+        t_pre.close()
+        t_dec.close()
+    finally:
+        srv.stop()

@@ -144,7 +144,7 @@ class SelectionTests(_Env, unittest.TestCase):
         with self.assertRaises(KeyError):
             kv.select_transport()
         with self.assertRaises(KeyError):
-            kv.select_transport("tcp")
+            kv.select_transport("nixl-ucx")           # a vendor P2P path this package lacks
 
     def test_shm_without_rm_core(self):
         with mock.patch.dict(sys.modules, {"rm_core": None}):
@@ -179,7 +179,9 @@ class SelectionTests(_Env, unittest.TestCase):
         with self.assertRaises(NotImplementedError):
             kv.make_transport("nixl")
         with self.assertRaises(NotImplementedError):
-            kv.make_transport("tcp")
+            kv.make_transport("nixl-ucx")
+        from rngd_pd_amd.connector.tcp import TcpTransport
+        self.assertIsInstance(kv.make_transport("tcp"), TcpTransport)
         with self.assertRaises(ValueError):
             kv.make_transport("carrier-pigeon")
 
