@@ -6,8 +6,8 @@ import sys
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _ROOT = os.path.dirname(_HERE)
-SOURCES = ["handoff.hip", "attention.hip", "decode_step.hip", "wgemm.hip", "staging.hip",
-           "runtime.hip"]
+SOURCES = ["handoff.hip", "attention.hip", "decode_step.hip", "wgemm.hip", "koni.hip",
+           "staging.hip", "runtime.hip"]
 OUT = os.path.join(_HERE, "librngdpd.so")
 NET_SOURCES = ["net/tcpkv.cpp"]
 NET_OUT = os.path.join(_HERE, "librngdpd_net.so")
