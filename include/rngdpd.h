@@ -206,6 +206,14 @@ int pdk_greedy_argmax(const uint16_t* logits, int B, int V, int64_t ld,
 int pdk_rmsnorm(uint16_t* x, const uint16_t* add, const uint16_t* weight, int B,
                 int H, float eps, uint16_t* out, uintptr_t stream);
 
+/* pdk_rmsnorm with the residual of a split-K projection (pdk_linear_splitk):
+ * x = bf16(x + sum over s < splits of partials[s] [B][H]) (fp32, summed in
+ * order s = 0, 1, ...), written back, then out = rmsnorm(x) * weight. The
+ * residual add of the down projection folded into the next layer's norm. */
+int pdk_rmsnorm_partials(uint16_t* x, const float* partials, int splits,
+                         const uint16_t* weight, int B, int H, float eps,
+                         uint16_t* out, uintptr_t stream);
+
 /* RoPE at position ctx[b]-1 and the new token's cache write, from one
  * projection row per stream: qkv [B][qkv_ld] holds q (n_q_heads heads), k and
  * v (n_kv_heads each) of head_dim. Rotate-half with angle pos*inv_freq[i]
@@ -237,6 +245,13 @@ int pdk_swiglu(const uint16_t* gate_up, int B, int M, uint16_t* out,
  * (zipadd_dsl, kernels/dsl_batch.py:43-53, fused); residual may alias y. */
 int pdk_linear(const uint16_t* x, const uint16_t* w, int B, int K, int N,
                const uint16_t* residual, uint16_t* y, uintptr_t stream);
+
+/* The same product split over K: partials [splits][B][N] fp32, partial s
+ * holding the sum over its share of K (no rounding). For a large K with a
+ * small N (the down projection, K = 14336, N = 4096) the split restores the
+ * workgroup count that wide column tiles take away. 1 <= splits <= 16, K/128. */
+int pdk_linear_splitk(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                      int splits, float* partials, uintptr_t stream);
 
 /* y [B][M] = silu(x . wg^T) * (x . wu^T), w_gate_up = [wg; wu] as [2M][K]
  * (the gate and up matmuls and swiglu_dsl, kernels/dsl_batch.py:55-71, in one

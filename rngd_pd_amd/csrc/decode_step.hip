@@ -23,15 +23,18 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // One workgroup per row of H (H % 8 == 0, H <= 8192), 256 threads, 8 bf16 per
-// 16-byte access, the row held in registers between the two passes. kAdd:
-// x <- bf16(x + add), written back (the residual add, zipadd_dsl of
-// kernels/dsl_batch.py), before the norm. Then
+// 16-byte access, the row held in registers between the two passes. Before
+// the norm, kAdd == 1: x <- bf16(x + add) (the residual add, zipadd_dsl of
+// kernels/dsl_batch.py), written back; kAdd == 2: x <- bf16(x + sum over
+// `splits` fp32 partial rows) (the residual add of a split-K projection,
+// summed in a fixed order), written back. Then
 // out = bf16(x * rsqrt(mean(x^2) + eps) * w) (rms_dsl: x * (sum x^2 + eps*H)^-1/2
 // * w*sqrt(H), the same value).
 constexpr int kNormThreads = 256, kNormChunks = 4;     // 8 elements per chunk
 
-template <bool kAdd>
-__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(uint16_t* x, const uint16_t* add,
+template <int kAdd>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(uint16_t* x, const void* add,
+                                                               int splits, int B,
                                                                const uint16_t* w, float eps,
                                                                int H, uint16_t* out) {
   __shared__ float part[kNormThreads / 64];
@@ -45,16 +48,33 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(uint16_t* x, cons
     keep[j] = pdk::zero8();
     if (c < n8) {
       v8 a = pdk::ld16(x + row + 8 * c);
-      if (kAdd) {
-        const v8 b = pdk::ld16(add + row + 8 * c);
+      if (kAdd == 1) {
+        const v8 b = pdk::ld16(static_cast<const uint16_t*>(add) + row + 8 * c);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const float lo = pdk::bf16_to_f32(a.w[k] & 0xffffu) + pdk::bf16_to_f32(b.w[k] & 0xffffu);
           const float hi = pdk::bf16_to_f32(a.w[k] >> 16) + pdk::bf16_to_f32(b.w[k] >> 16);
           a.w[k] = pdk::f32_to_bf16_rne(lo) | (pdk::f32_to_bf16_rne(hi) << 16);
         }
-        pdk::st16(x + row + 8 * c, a);
+      } else if (kAdd == 2) {
+        float acc[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] = 0.f;
+        const float* p = static_cast<const float*>(add) + row + 8 * c;
+        for (int s = 0; s < splits; ++s) {
+          const float4 u = *reinterpret_cast<const float4*>(p + (int64_t)s * B * H);
+          const float4 v = *reinterpret_cast<const float4*>(p + (int64_t)s * B * H + 4);
+          acc[0] += u.x; acc[1] += u.y; acc[2] += u.z; acc[3] += u.w;
+          acc[4] += v.x; acc[5] += v.y; acc[6] += v.z; acc[7] += v.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float lo = pdk::bf16_to_f32(a.w[k] & 0xffffu) + acc[2 * k];
+          const float hi = pdk::bf16_to_f32(a.w[k] >> 16) + acc[2 * k + 1];
+          a.w[k] = pdk::f32_to_bf16_rne(lo) | (pdk::f32_to_bf16_rne(hi) << 16);
+        }
       }
+      if (kAdd) pdk::st16(x + row + 8 * c, a);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float lo = pdk::bf16_to_f32(a.w[k] & 0xffffu), hi = pdk::bf16_to_f32(a.w[k] >> 16);
@@ -158,24 +178,42 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* gu, int M, 
 
 }  // namespace
 
-extern "C" int pdk_rmsnorm(uint16_t* x, const uint16_t* add, const uint16_t* weight, int B,
-                           int H, float eps, uint16_t* out, uintptr_t stream) {
-  pdk::clear_error();
+static int check_norm(const void* x, const void* weight, const void* out, int B, int H) {
   PDK_REQUIRE(x && weight && out, "null pointer argument");
   PDK_REQUIRE(B >= 1 && B <= 65535, "B must be in [1, 65535] (got %d)", B);
   PDK_REQUIRE(H >= 8 && H % 8 == 0 && H <= kNormThreads * kNormChunks * 8,
               "H must be a multiple of 8 in [8, %d] (got %d)", kNormThreads * kNormChunks * 8, H);
-  PDK_REQUIRE(pdk::aligned16(x) && pdk::aligned16(weight) && pdk::aligned16(out) &&
-                  (!add || pdk::aligned16(add)),
+  PDK_REQUIRE(pdk::aligned16(x) && pdk::aligned16(weight) && pdk::aligned16(out),
               "tensors must be 16-byte aligned");
+  return PDK_OK;
+}
+
+extern "C" int pdk_rmsnorm(uint16_t* x, const uint16_t* add, const uint16_t* weight, int B,
+                           int H, float eps, uint16_t* out, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_norm(x, weight, out, B, H)) return rc;
+  PDK_REQUIRE(!add || pdk::aligned16(add), "tensors must be 16-byte aligned");
   PDK_REQUIRE(eps >= 0.f, "eps must be >= 0");
   hipStream_t st = pdk::as_stream(stream);
   if (add)
-    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(B), dim3(kNormThreads), 0, st, x, add, weight, eps, H,
-                       out);
+    hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(B), dim3(kNormThreads), 0, st, x, add, 0, B,
+                       weight, eps, H, out);
   else
-    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(B), dim3(kNormThreads), 0, st, x, add, weight, eps, H,
-                       out);
+    hipLaunchKernelGGL(rmsnorm_kernel<0>, dim3(B), dim3(kNormThreads), 0, st, x, nullptr, 0, B,
+                       weight, eps, H, out);
+  return pdk::check_launch("rmsnorm_kernel");
+}
+
+extern "C" int pdk_rmsnorm_partials(uint16_t* x, const float* partials, int splits,
+                                    const uint16_t* weight, int B, int H, float eps,
+                                    uint16_t* out, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_norm(x, weight, out, B, H)) return rc;
+  PDK_REQUIRE(partials && pdk::aligned16(partials), "partials must be 16-byte aligned");
+  PDK_REQUIRE(splits >= 1 && splits <= 64, "splits must be in [1, 64] (got %d)", splits);
+  PDK_REQUIRE(eps >= 0.f, "eps must be >= 0");
+  hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(B), dim3(kNormThreads), 0, pdk::as_stream(stream),
+                     x, partials, splits, B, weight, eps, H, out);
   return pdk::check_launch("rmsnorm_kernel");
 }
 

@@ -40,7 +40,7 @@ __device__ __forceinline__ f32x4 mfma(const v8& a, const v8& b, f32x4 c) {
 constexpr int kStepK = 128;        // k per wave step: 4 MFMA of 32
 constexpr int kWaves = 8;
 
-enum Epilogue { kPlain = 0, kResidual = 1, kSwiGLU = 2, kArgmax = 3 };
+enum Epilogue { kPlain = 0, kResidual = 1, kSwiGLU = 2, kArgmax = 3, kPartial = 4 };
 
 // Greedy-token key of one bf16 logit: the value in an order-preserving code
 // above the complement of the column, so the unsigned maximum is the largest
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ w, int B,
                                                             int K, int N,
                                                             const uint16_t* r, uint16_t* y,
-                                                            uint64_t* keys) {
+                                                            uint64_t* keys, float* part) {
   constexpr int kPairs = kEpi == kSwiGLU ? 2 : 1;
   constexpr int kW = kPairs * kCols;                 // W tiles per step
   constexpr int kDepth = depth_for(kTiles + kW);
@@ -99,12 +99,16 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   // cycle through kDepth slots; a slot past the wave's last step loads that
   // last step again (a valid address) and its X operand is zeroed, so every
   // load is unconditional and the tail adds nothing.
-  const int steps = K / kStepK;
+  // Split-K over gridDim.y workgroups: this one takes steps [s_lo, s_hi).
+  const int steps_all = K / kStepK;
+  const int s_lo = (int)((int64_t)blockIdx.y * steps_all / gridDim.y);
+  const int s_hi = (int)((int64_t)(blockIdx.y + 1) * steps_all / gridDim.y);
+  const int steps = s_hi - s_lo;
   const int n_mine = steps > wave ? (steps - wave + kWaves - 1) / kWaves : 0;
   const int last = wave + (max(n_mine, 1) - 1) * kWaves;
   v8 wv[kDepth][kW][4], xv[kDepth][kTiles][4];
   auto load = [&](int slot, int j) {
-    const int k = min(wave + j * kWaves, last) * kStepK;
+    const int k = (s_lo + min(wave + j * kWaves, last)) * kStepK;
 #pragma unroll
     for (int q = 0; q < kW; ++q)
 #pragma unroll
@@ -158,6 +162,10 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
         v[p] = sum;
       }
       const int64_t at = (int64_t)m * N + n;
+      if (kEpi == kPartial) {
+        if (ok) part[((int64_t)blockIdx.y * B + m) * N + n] = v[0];
+        continue;
+      }
       float out = v[0];
       if (kEpi == kResidual && ok) out += pdk::bf16_to_f32(r[at]);
       if (kEpi == kSwiGLU) out = v[0] / (1.f + expf(-v[0])) * v[kPairs - 1];
@@ -194,13 +202,14 @@ __global__ void argmax_finish_kernel(uint64_t* keys, int B, int32_t* tokens) {
 
 template <int kCols, int kEpi>
 int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
-                uint16_t* y, uint64_t* keys, hipStream_t st) {
-  const dim3 grid((N + 16 * kCols - 1) / (16 * kCols)), block(kWaves * 64);
+                uint16_t* y, uint64_t* keys, hipStream_t st, float* part = nullptr,
+                int splits = 1) {
+  const dim3 grid((N + 16 * kCols - 1) / (16 * kCols), splits), block(kWaves * 64);
   switch ((B + 15) / 16) {
-    case 1: hipLaunchKernelGGL((wgemm_kernel<1, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys); break;
-    case 2: hipLaunchKernelGGL((wgemm_kernel<2, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys); break;
-    case 3: hipLaunchKernelGGL((wgemm_kernel<3, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys); break;
-    default: hipLaunchKernelGGL((wgemm_kernel<4, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys); break;
+    case 1: hipLaunchKernelGGL((wgemm_kernel<1, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part); break;
+    case 2: hipLaunchKernelGGL((wgemm_kernel<2, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part); break;
+    case 3: hipLaunchKernelGGL((wgemm_kernel<3, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part); break;
+    default: hipLaunchKernelGGL((wgemm_kernel<4, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part); break;
   }
   return pdk::check_launch("wgemm_kernel");
 }
@@ -259,4 +268,19 @@ extern "C" int pdk_linear_argmax(const uint16_t* x, const uint16_t* w, int B, in
   if (int rc = launch<kArgmax>(x, w, B, K, N, nullptr, logits, keys, st)) return rc;
   hipLaunchKernelGGL(argmax_finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, keys, B, tokens);
   return pdk::check_launch("argmax_finish_kernel");
+}
+
+extern "C" int pdk_linear_splitk(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                                 int splits, float* partials, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_shape(x, w, partials, B, K, N)) return rc;
+  PDK_REQUIRE(splits >= 1 && splits <= 16 && splits <= K / kStepK,
+              "splits must be in [1, min(16, K/%d)] (got %d)", kStepK, splits);
+  // Wide column tiles (fewer re-reads of x) with the K split restoring the
+  // workgroup count.
+  hipStream_t st = pdk::as_stream(stream);
+  if (N >= 1024)
+    return launch_cols<4, kPartial>(x, w, B, K, N, nullptr, nullptr, nullptr, st, partials,
+                                    splits);
+  return launch_cols<1, kPartial>(x, w, B, K, N, nullptr, nullptr, nullptr, st, partials, splits);
 }

@@ -5,19 +5,19 @@ Replaces the reference's BatchDecodeEngine.step / step_logits
 (kernels/decode_batch.py:56-91) plus the batched lm_head and greedy argmax
 (engines/decode_batch.py:162-171). Per layer, one launch per line:
 
-  h = rmsnorm(x)                                   pdk_rmsnorm
+  x = x + sum(partials); h = rmsnorm(x)           pdk_rmsnorm_partials (pdk_rmsnorm at layer 0)
   qkv = h . Wqkv^T                                 pdk_linear
   RoPE(q, k); new k, v into the paged cache         pdk_rope_cache_append
   ao = attention over slots 0..pos                 pdk_decode_attn (+ its merge)
   x = x + ao . Wo^T                                pdk_linear, residual fused
   h = rmsnorm(x)                                   pdk_rmsnorm
   a = silu(h . Wg^T) * (h . Wu^T)                  pdk_linear_swiglu
-  x = x + a . Wd^T                                 pdk_linear, residual fused
+  partials = a . Wd^T split over K                 pdk_linear_splitk (fp32, joins x in the next norm)
 
-then the final norm and the lm_head GEMM with the first-maximum argmax in its
-epilogue (pdk_linear_argmax). Weights are [out, in] contiguous (torch Linear
-layout) with q|k|v and gate|up stacked, so each projection is one pass over
-its weights. Activations are bf16 at every tensor boundary, as the
+then the final norm (which adds the last layer's partials) and the lm_head
+GEMM with the first-maximum argmax in its epilogue (pdk_linear_argmax).
+Weights are [out, in] contiguous (torch Linear layout) with q|k|v and gate|up
+stacked, so each projection is one pass over its weights. Activations are bf16 at every tensor boundary, as the
 reference's are; the kernels accumulate in fp32 and round once.
 """
 import contextlib
@@ -129,6 +129,11 @@ class LlamaDecoder:
         self.logits = e(B, cfg.vocab)
         self.tokens = torch.empty(B, dtype=torch.int32, device=dev)
         self.keys = torch.zeros(B, dtype=torch.int64, device=dev)    # argmax scratch, kept zero
+        # The down projection runs split over K (its 14336-long rows) into fp32
+        # partial sums, which the next norm adds to the residual.
+        groups = (H + 63) // 64 if H >= 1024 else (H + 15) // 16
+        self.down_splits = max(1, min(8, cfg.inter // 128, -(-256 // groups)))
+        self.part = torch.empty((self.down_splits, B, H), dtype=torch.float32, device=dev)
         self.inv = cfg.inv_freq().to(dev)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
         self._ws = None
@@ -187,8 +192,12 @@ class LlamaDecoder:
         call = _lib.call
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
             torch.index_select(w.embed, 0, tokens.long(), out=x)
-            for n1, wqkv, wo, n2, wgu, wd, ck, cv in self._layers:
-                call("pdk_rmsnorm", xp, None, n1, B, H, eps, hp, st)
+            partp, sp = self.part.data_ptr(), self.down_splits
+            for li, (n1, wqkv, wo, n2, wgu, wd, ck, cv) in enumerate(self._layers):
+                if li:      # the previous layer's down projection joins the residual here
+                    call("pdk_rmsnorm_partials", xp, partp, sp, n1, B, H, eps, hp, st)
+                else:
+                    call("pdk_rmsnorm", xp, None, n1, B, H, eps, hp, st)
                 call("pdk_linear", hp, wqkv, B, H, QKV, None, qkvp, st)
                 call("pdk_rope_cache_append", qkvp, QKV, qp, inv, cp, tp, mb, ck, cv, nb, B, NH,
                      NKV, HD, st)
@@ -197,8 +206,8 @@ class LlamaDecoder:
                 call("pdk_linear", aop, wo, B, NH * HD, H, xp, xp, st)
                 call("pdk_rmsnorm", xp, None, n2, B, H, eps, hp, st)
                 call("pdk_linear_swiglu", hp, wgu, B, H, M, actp, st)
-                call("pdk_linear", actp, wd, B, M, H, xp, xp, st)
-            call("pdk_rmsnorm", xp, None, w.norm_f.data_ptr(), B, H, eps, hp, st)
+                call("pdk_linear_splitk", actp, wd, B, M, H, sp, partp, st)
+            call("pdk_rmsnorm_partials", xp, partp, sp, w.norm_f.data_ptr(), B, H, eps, hp, st)
             call("pdk_linear_argmax", hp, w.lm_head.data_ptr(), B, H, cfg.vocab,
                  self.logits.data_ptr(), self.keys.data_ptr(), self.tokens.data_ptr(), st)
         return self.tokens[:B]

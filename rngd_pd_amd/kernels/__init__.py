@@ -3,9 +3,10 @@ from .handoff import (pack_kv, pack_kv_batch, scatter_paged, scatter_paged_batch
                       frame_shape, frame_views, stream_handle, validate_table, copy_kernel)
 from .attention import decode_attention, cache_append, greedy_argmax, workspace_bytes, get_workspace
 from .decode_step import (rmsnorm, rope_cache_append, swiglu, linear, linear_swiglu,
-                          linear_argmax)
+                          linear_argmax, linear_splitk, rmsnorm_partials)
 
 __all__ = ["pack_kv", "pack_kv_batch", "scatter_paged", "scatter_paged_batch", "gather_paged",
            "frame_shape", "frame_views", "stream_handle", "validate_table", "copy_kernel",
            "decode_attention", "cache_append", "greedy_argmax", "workspace_bytes", "get_workspace",
-           "rmsnorm", "rope_cache_append", "swiglu", "linear", "linear_swiglu", "linear_argmax"]
+           "rmsnorm", "rope_cache_append", "swiglu", "linear", "linear_swiglu", "linear_argmax",
+           "linear_splitk", "rmsnorm_partials"]

@@ -138,3 +138,33 @@ def linear_argmax(x, w, keys, tokens=None, logits=None, stream=None):
               logits.data_ptr() if logits is not None else None, keys.data_ptr(),
               tokens.data_ptr(), stream_handle(stream))
     return tokens
+
+
+def linear_splitk(x, w, splits, partials=None, stream=None):
+    """x . w^T split over K into fp32 partial sums [splits, B, N] (summed
+    later, e.g. by rmsnorm_partials)."""
+    B, K, N = _check_linear(x, w)
+    if partials is None:
+        partials = torch.empty((splits, B, N), dtype=torch.float32, device=x.device)
+    elif partials.dtype != torch.float32 or partials.numel() < splits * B * N or \
+            not partials.is_contiguous():
+        raise ValueError(f"partials must be contiguous float32 holding {splits}x{B}x{N}")
+    _lib.call("pdk_linear_splitk", x.data_ptr(), w.data_ptr(), B, K, N, int(splits),
+              partials.data_ptr(), stream_handle(stream))
+    return partials
+
+
+def rmsnorm_partials(x, partials, splits, weight, eps, out=None, stream=None):
+    """x <- bf16(x + sum of partials[:splits]) in place, then rmsnorm(x) * weight."""
+    _need(x, "x")
+    _need(weight, "weight")
+    if x.dim() != 2 or not x.is_contiguous():
+        raise ValueError("x must be contiguous [B, H]")
+    B, H = x.shape
+    if partials.dtype != torch.float32 or partials.numel() < splits * B * H:
+        raise ValueError(f"partials must be float32 holding {splits}x{B}x{H}")
+    if out is None:
+        out = torch.empty_like(x)
+    _lib.call("pdk_rmsnorm_partials", x.data_ptr(), partials.data_ptr(), int(splits),
+              weight.data_ptr(), B, H, float(eps), out.data_ptr(), stream_handle(stream))
+    return out

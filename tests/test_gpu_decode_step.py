@@ -134,6 +134,39 @@ def test_linear(cuda, B, K, N):
     np.testing.assert_allclose(_f32(to_host(rd)), want + _f32(r), rtol=HALF_ULP, atol=tol)
 
 
+@pytest.mark.parametrize("B,K,N,splits", [(16, 14336, 4096, 4), (4, 14336, 4096, 4),
+                                          (3, 1024, 512, 8), (33, 384, 48, 3), (1, 128, 16, 1)])
+def test_linear_splitk_and_rmsnorm_partials(cuda, B, K, N, splits):
+    """Partial sums over the K split add up to x . w^T (fp32); the norm adds
+    them to the residual in order, rounds once, and normalises."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B * 7 + K + splits)
+    x, w = rand_bf16(rng, (B, K)), rand_bf16(rng, (N, K), 0.05)
+    r, g = rand_bf16(rng, (B, N), 4.0), rand_bf16(rng, (N,))
+    print(f"linear_splitk B={B} K={K} N={N} splits={splits}", flush=True)
+    part = K_.linear_splitk(to_dev(x), to_dev(w), splits)
+    torch.cuda.synchronize()
+    want = _f32(x).astype(np.float64) @ _f32(w).astype(np.float64).T
+    got = part.cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(got.sum(0), want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+    steps = K // 128
+    for s in range(splits):                                   # each split holds its own K range
+        lo, hi = s * steps // splits * 128, (s + 1) * steps // splits * 128
+        ws = _f32(x)[:, lo:hi].astype(np.float64) @ _f32(w)[:, lo:hi].astype(np.float64).T
+        np.testing.assert_allclose(got[s], ws, rtol=1e-5, atol=1e-5 * np.abs(want).max() + 1e-6)
+    if N % 8 == 0 and N >= 8:
+        xd = to_dev(r)
+        out = K_.rmsnorm_partials(xd, part, splits, to_dev(g), 1e-5)
+        torch.cuda.synchronize()
+        acc = np.zeros((B, N), np.float32)
+        for s in range(splits):
+            acc = acc + part[s].cpu().numpy()
+        summed = _bf16_bits_rne(_f32(r) + acc)
+        np.testing.assert_array_equal(to_host(xd), summed)
+        np.testing.assert_allclose(_f32(to_host(out)), od.rmsnorm(_f32(summed), _f32(g), 1e-5),
+                                   rtol=HALF_ULP, atol=1e-6)
+
+
 @pytest.mark.parametrize("B,K,M", [(4, 4096, 14336), (16, 128, 16), (40, 512, 64), (3, 256, 24)])
 def test_linear_swiglu(cuda, B, K, M):
     from rngd_pd_amd import kernels as K_
