@@ -40,8 +40,15 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(uint16_t* x, cons
   __shared__ float part[kNormThreads / 64];
   const int64_t row = (int64_t)blockIdx.x * H;
   const int n8 = H >> 3;
-  v8 keep[kNormChunks];
+  v8 keep[kNormChunks], gain[kNormChunks];
   float ss = 0.f;
+  // The weights are loaded with the row, before the reduction, so the second
+  // pass waits on no memory.
+#pragma unroll
+  for (int j = 0; j < kNormChunks; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    gain[j] = c < n8 ? pdk::ld16(w + 8 * c) : pdk::zero8();
+  }
 #pragma unroll
   for (int j = 0; j < kNormChunks; ++j) {
     const int c = threadIdx.x + j * kNormThreads;
@@ -95,7 +102,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(uint16_t* x, cons
     const int c = threadIdx.x + j * kNormThreads;
     if (c < n8) {
       const v8 a = keep[j];
-      const v8 g = pdk::ld16(w + 8 * c);
+      const v8 g = gain[j];
       v8 o;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
