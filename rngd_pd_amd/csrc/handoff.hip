@@ -25,6 +25,8 @@
 // in the cache when its consumer (a copy or the scatter) reads it: one
 // 512-token request packs in 22 us that way and in 28 us streaming.
 
+#include <algorithm>
+
 #include "pdk_common.h"
 
 namespace {
@@ -42,9 +44,50 @@ constexpr int64_t kStreamBytes = 256ll << 20;   // the MI355X last-level (Infini
 struct PackArgs {
   pdk_pack_req req[PDK_MAX_BATCH];
   int64_t off[PDK_MAX_BATCH + 1];
-  int32_t nT[PDK_MAX_BATCH];     // 64-token tiles of request r
+  int32_t nT[PDK_MAX_BATCH];     // 64-token tiles of request r holding valid tokens
+  int32_t nvalid[PDK_MAX_BATCH]; // its units that move tokens (the rest fill zeros)
+  int32_t Pz[PDK_MAX_BATCH];     // first column of its all-zero tail: min(64 nT, S)
+  int32_t nZ[PDK_MAX_BATCH];     // zero-fill chunks per (layer, head)
+  uint32_t magic[PDK_MAX_BATCH]; // ceil(2^32 / ((S - Pz) / 8)): row of a K tail group
   int n_req, S, Hkv, D, nD;
 };
+
+constexpr int kZeroInstr = 16;                    // 16-byte stores per lane per zero chunk
+constexpr int kZeroElems = kZeroInstr * 64 * 8;   // 8192 bf16 = 16 KiB per chunk
+
+// The all-zero tail of one (layer, head) of a frame: K rows (h, d) columns
+// [Pz, S) and the V block rows t in [Pz, S), flattened into 2 * D * (S - Pz)
+// elements (the K tails first, row by row, then the contiguous V tail). Each
+// store instruction of a chunk writes 1 KiB of consecutive elements of that
+// space: whole K-row runs and the V tail linearly, instead of the 128-byte
+// pieces a transposed tile would write.
+template <bool kStream>
+__device__ __forceinline__ void pack_zero_chunk(const PackArgs& a, int r, uint32_t z, int lane) {
+  const pdk_pack_req& R = a.req[r];
+  const int nZ = a.nZ[r];
+  const int zc = (int)(z % (uint32_t)nZ);
+  z /= (uint32_t)nZ;
+  const int h = (int)(z % (uint32_t)a.Hkv);
+  const int l = (int)(z / (uint32_t)a.Hkv);
+  const int S = a.S, D = a.D, Pz = a.Pz[r];
+  const uint32_t g_row = (uint32_t)(S - Pz) >> 3;   // 8-element groups per K tail row
+  const uint32_t gK = (uint32_t)D * g_row;         // groups of the K tails (= of the V tail)
+  const int64_t F = (int64_t)a.Hkv * D * S;
+  uint16_t* fk = R.frame + (int64_t)(2 * l) * F;
+  uint16_t* fv = fk + F + ((int64_t)h * S + Pz) * D;
+  const v8 zero = pdk::zero8();
+#pragma unroll
+  for (int i = 0; i < kZeroInstr; ++i) {
+    const uint32_t g = (uint32_t)zc * (kZeroElems / 8) + i * 64 + lane;
+    if (g < gK) {
+      const uint32_t row = __umulhi(g, a.magic[r]);
+      const uint32_t col = Pz + (g - row * g_row) * 8;
+      pdk::st16_as<kStream>(fk + ((int64_t)h * D + row) * S + col, zero);
+    } else if (g < 2 * gK) {
+      pdk::st16_as<kStream>(fv + (int64_t)(g - gK) * 8, zero);
+    }
+  }
+}
 
 // Request of wavefront tile `unit` (uniform across the wavefront).
 __device__ __forceinline__ int request_of(const int64_t* off, int n_req, int64_t unit) {
@@ -66,7 +109,11 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
   const int r = request_of(a.off, a.n_req, unit);
   const pdk_pack_req& R = a.req[r];
   const int lane = threadIdx.x & 63;
-  uint32_t u = (uint32_t)(unit - a.off[r]);   // tiles of one request fit 32 bits
+  uint32_t u = (uint32_t)(unit - a.off[r]);   // units of one request fit 32 bits
+  if (u >= (uint32_t)a.nvalid[r]) {           // uniform across the wavefront
+    pack_zero_chunk<kStream>(a, r, u - (uint32_t)a.nvalid[r], lane);
+    return;
+  }
   const int dt = (int)(u % (uint32_t)a.nD); u /= (uint32_t)a.nD;
   const int tt = (int)(u % (uint32_t)a.nT[r]); u /= (uint32_t)a.nT[r];
   const int h = (int)(u % (uint32_t)a.Hkv); u /= (uint32_t)a.Hkv;
@@ -315,6 +362,9 @@ extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_lay
   PDK_REQUIRE(reqs != nullptr, "reqs is null");
   PDK_REQUIRE(n_reqs >= 1 && n_reqs <= PDK_MAX_BATCH, "n_reqs must be in [1, %d] (got %d)",
               PDK_MAX_BATCH, n_reqs);
+  // The zero-fill chunks find a K row by a multiply-high by ceil(2^32 / g),
+  // exact while (row groups) * g^2 < 2^32: S <= 32768 keeps it so.
+  PDK_REQUIRE(S <= 32768, "S must be <= 32768 (got %d)", S);
   PackArgs a{};
   for (int i = 0; i < n_reqs; ++i) {
     const pdk_pack_req& r = reqs[i];
@@ -340,19 +390,29 @@ extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_lay
   a.nD = head_dim / kTileD;
   a.off[0] = 0;
   for (int i = 0; i < n_reqs; ++i) {
-    // A narrow frame needs only the tiles that hold valid columns.
-    const int cols = (a.req[i].flags & PDK_PACK_NARROW) ? a.req[i].P : S;
-    a.nT[i] = (cols + kTileT - 1) / kTileT;
-    a.off[i + 1] = a.off[i] + (int64_t)n_layers * n_kv_heads * a.nT[i] * a.nD;
+    // Tiles that hold valid tokens move them (and zero their own columns >= P);
+    // a full-width frame's tail past them is zero-filled by separate chunks.
+    const int P = a.req[i].P;
+    a.nT[i] = (P + kTileT - 1) / kTileT;
+    a.nvalid[i] = n_layers * n_kv_heads * a.nT[i] * a.nD;
+    a.Pz[i] = std::min(a.nT[i] * kTileT, S);
+    const bool narrow = (a.req[i].flags & PDK_PACK_NARROW) != 0;
+    const int64_t tail = (int64_t)2 * head_dim * (S - a.Pz[i]);
+    a.nZ[i] = narrow ? 0 : (int)((tail + kZeroElems - 1) / kZeroElems);
+    const uint32_t g_row = (uint32_t)(S - a.Pz[i]) / 8;
+    a.magic[i] = g_row ? (uint32_t)((((uint64_t)1 << 32) + g_row - 1) / g_row) : 0;
+    a.off[i + 1] = a.off[i] + a.nvalid[i] + (int64_t)n_layers * n_kv_heads * a.nZ[i];
   }
   if (a.off[n_reqs] == 0) return PDK_OK;
   const int64_t gx = grid_x(a.off[n_reqs]);
   PDK_REQUIRE(gx < (1ll << 31), "launch too large");
   // Bytes the launch moves: valid tokens read, frame columns written.
   int64_t moved = 0;
-  for (int i = 0; i < n_reqs; ++i)
+  for (int i = 0; i < n_reqs; ++i) {
+    const bool narrow = (a.req[i].flags & PDK_PACK_NARROW) != 0;
     moved += (int64_t)n_layers * 2 * n_kv_heads * head_dim * 2 *
-             (a.req[i].P + (int64_t)a.nT[i] * kTileT);
+             (a.req[i].P + (int64_t)(narrow ? a.req[i].P : S));
+  }
   if (moved > kStreamBytes)
     hipLaunchKernelGGL(pack_kernel<true>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
   else
