@@ -51,12 +51,17 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU baseline sample (0 skips it)")
-    ap.add_argument("--only", choices=["all", "handoff", "decode", "step", "long", "serve", "copy"],
-                    default="all",
-                    help="restrict the run (for profiler passes)")
+    ap.add_argument("--only", default="all",
+                    help="restrict the run (for profiler passes): all, or a comma-separated "
+                         "subset of handoff, decode, step, long, serve, copy")
     ap.add_argument("--copy-mib", type=int, default=1024,
                     help="bytes moved by --only copy (traffic-counter calibration)")
-    return ap.parse_args()
+    args = ap.parse_args()
+    legs = {"all", "handoff", "decode", "step", "long", "serve", "copy"}
+    args.legs = set(args.only.split(","))
+    if not args.legs <= legs:
+        ap.error(f"--only: unknown legs {sorted(args.legs - legs)}")
+    return args
 
 
 def log(msg):
@@ -682,26 +687,26 @@ def main():
                       "layers": L, "kv_heads": H, "head_dim": D, "frame_tokens": S,
                       "block_size": BS},
            "extra": {}}
-    if args.only == "copy":
+    if args.legs == {"copy"}:
         bench_copy(args, torch, K, dev)
         return 0
-    if args.only in ("all", "handoff"):
+    if args.legs & {"all", "handoff"}:
         bench_handoff(args, torch, K, lib, dev, out)
-    if args.only in ("all", "decode"):
+    if args.legs & {"all", "decode"}:
         bench_decode(args, torch, K, lib, dev, out)
-    if args.only in ("all", "step"):
+    if args.legs & {"all", "step"}:
         bench_step(args, torch, dev, out)
-    if args.only in ("all", "long"):
+    if args.legs & {"all", "long"}:
         bench_long(args, torch, dev, out)
-    if args.only in ("all", "serve"):
+    if args.legs & {"all", "serve"}:
         bench_serve(args, out)
-    if args.only == "all" and args.cpu_seconds > 0:
+    if "all" in args.legs and args.cpu_seconds > 0:
         bench_cpu(args, out)
-    if args.only == "step":
+    if args.legs == {"step"}:
         b = out["extra"]["decode_step_llama8b"]["B16"]
         out.update(value=b["tokens_per_s_graph"], unit="tokens/s",
                    ms_per_step=b["ms_per_step_graph"])
-    if args.only == "decode":
+    if args.legs == {"decode"}:
         b = out["extra"]["decode_batch"]["B16"]
         out.update(value=b["tokens_per_s_graph"], unit="tokens/s",
                    ms_per_step=b["step_us_graph"] / 1e3, roofline=b["roofline"])
