@@ -229,6 +229,20 @@ int pdk_rope_cache_append(const uint16_t* qkv, int64_t qkv_ld, uint16_t* q_out,
                           int B, int n_q_heads, int n_kv_heads, int head_dim,
                           uintptr_t stream);
 
+/* The same from the split-K q|k|v projection: partials [splits][B][N] fp32
+ * (pdk_linear_splitk's output, N = (n_q_heads + 2 n_kv_heads) head_dim) are
+ * added in split order and rounded to bf16 once per element, the value the
+ * unsplit projection writes, then RoPE and the cache write as above.
+ * splits in {1, 2, 4}. */
+int pdk_rope_cache_append_partials(const float* partials, int splits, int N,
+                                   uint16_t* q_out, const float* inv_freq,
+                                   const int32_t* ctx_lens,
+                                   const int32_t* block_tables, int max_blocks,
+                                   uint16_t* cache_k, uint16_t* cache_v,
+                                   int num_blocks, int B, int n_q_heads,
+                                   int n_kv_heads, int head_dim,
+                                   uintptr_t stream);
+
 /* out [B][M] = silu(g) * u for gate_up [B][2M] = [g | u] (swiglu_dsl,
  * kernels/dsl_batch.py:55-71). M % 8 == 0. */
 int pdk_swiglu(const uint16_t* gate_up, int B, int M, uint16_t* out,

@@ -77,6 +77,8 @@ SIGNATURES = {
     "pdk_rmsnorm": (_I, [_P, _P, _P, _I, _I, ctypes.c_float, _P, _U]),
     "pdk_rope_cache_append": (_I, [_P, _I64, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
                                    _U]),
+    "pdk_rope_cache_append_partials": (_I, [_P, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I,
+                                            _I, _I, _U]),
     "pdk_swiglu": (_I, [_P, _I, _I, _P, _U]),
     "pdk_linear": (_I, [_P, _P, _I, _I, _I, _P, _P, _U]),
     "pdk_linear_swiglu": (_I, [_P, _P, _I, _I, _I, _P, _U]),

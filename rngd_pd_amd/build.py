@@ -16,7 +16,10 @@ NET_OUT = os.path.join(_HERE, "librngdpd_net.so")
 def hipcc_command(out=OUT):
     return (["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
              "-shared", "-I", os.path.join(_ROOT, "include"),
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-o", out]
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             # Leading scalar kernel arguments arrive preloaded in SGPRs, so a
+             # kernel's first loads need not wait for a kernarg read.
+             "-mllvm", "-amdgpu-kernarg-preload-count=16", "-o", out]
             + [os.path.join(_HERE, "csrc", s) for s in SOURCES])
 
 

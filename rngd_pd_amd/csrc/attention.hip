@@ -210,19 +210,32 @@ __device__ __forceinline__ void attend_pair(const AttnArgs& a, Span& ra, Span& r
   if (has_b) span_pv(rb, p + 8, pmask, sb + 8 * g, lim, o);
 }
 
-__global__ __launch_bounds__(512) void decode_attn_kernel(const AttnArgs a) {
+// Scalar arguments, those the first loads need first: the compiler preloads
+// the leading ones into SGPRs (-amdgpu-kernarg-preload-count), so the query,
+// context-length and block-id loads issue without waiting for a kernarg read.
+// hgw packs Hkv (16 bits), G (8) and the wavefront count W (8).
+__global__ __launch_bounds__(512) void decode_attn_kernel(
+    const uint16_t* q, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
+    const int32_t* ctx_lens, uint32_t hgw, int max_blocks, int num_blocks, int split_tokens,
+    int nsplit, float scale_log2, uint16_t* out, float* ws_ml, float* ws_o) {
   __shared__ float sm_m[kMaxWaves][kMaxG];
   __shared__ float sm_l[kMaxWaves][kMaxG];
   extern __shared__ float sm_o[];                // [W][min(G, kMergeRows)][kOStride]
 
+  AttnArgs a;
+  a.Hkv = hgw & 0xffff;
+  a.G = (hgw >> 16) & 0xff;
+  a.Hq = a.Hkv * a.G;
+  a.q = q; a.ck = ck; a.cv = cv; a.tables = tables; a.ctx = ctx_lens; a.out = out;
+  a.ws_ml = ws_ml; a.ws_o = ws_o; a.num_blocks = num_blocks; a.max_blocks = max_blocks;
+  a.nsplit = nsplit; a.split_tokens = split_tokens; a.scale_log2 = scale_log2;
+  const int W = hgw >> 24;
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int W = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 4, j = lane & 15;
   const int G = a.G;
-  const int ctx = min(a.ctx[b], a.max_blocks * 16);
+  int ctx_raw = a.ctx[b];
   const int s_begin = split * a.split_tokens;
-  const int s_end = (split == a.nsplit - 1) ? ctx : min(ctx, s_begin + a.split_tokens);
   const int32_t* table = a.tables + (int64_t)b * a.max_blocks;
 
   const uint16_t* qp = a.q + ((int64_t)b * a.Hq + h * G + min(j, G - 1)) * kD + g * 8;
@@ -240,29 +253,45 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(const AttnArgs a) {
   // The wavefront index is uniform: spans and their block ids live in SGPRs,
   // so the block ids of both spans come in as scalar loads before any data
   // load is issued (a vector load here would make the second span's data
-  // wait, in-order, behind the first span's).
+  // wait, in-order, behind the first span's). Those of the first pair do not
+  // depend on the context length: they are read (at indices clamped into the
+  // table) together with it, and the asm statement keeps the compiler from
+  // waiting for the length first. An id read past the context is harmless:
+  // load_span maps an invalid id to block 0, and tokens >= s_end are masked.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int stride = W * kSpan;
-  const int last_blk = (s_end - 1) >> 4;
-  auto two_spans = [&](int sa, bool first) {
+  const int mb = a.max_blocks - 1;
+  auto ids = [&](int sa, int* id) {
+    const int sb = sa + stride;
+    id[0] = table[min(sa >> 4, mb)];
+    id[1] = table[min((sa >> 4) + 1, mb)];
+    id[2] = table[min(sb >> 4, mb)];
+    id[3] = table[min((sb >> 4) + 1, mb)];
+  };
+  const int sa0 = s_begin + wv * kSpan;
+  int id0[4];
+  ids(sa0, id0);
+  asm volatile("" : "+s"(ctx_raw) : "s"(id0[0]), "s"(id0[1]), "s"(id0[2]), "s"(id0[3]));
+  const int ctx = min(ctx_raw, a.max_blocks * 16);
+  const int s_end = (split == a.nsplit - 1) ? ctx : min(ctx, s_begin + a.split_tokens);
+  auto two_spans = [&](int sa, bool first, const int* id) {
     const int sb = sa + stride;
     const bool has_b = sb < s_end;
-    const int a_lo = table[sa >> 4];
-    const int a_hi = table[min((sa >> 4) + 1, last_blk)];
-    const int b_lo = has_b ? table[sb >> 4] : 0;
-    const int b_hi = has_b ? table[min((sb >> 4) + 1, last_blk)] : 0;
     Span ra, rb;
-    load_span(a, h, sa, g, j, a_lo, a_hi, ra);
-    if (has_b) load_span(a, h, sb, g, j, b_lo, b_hi, rb);
+    load_span(a, h, sa, g, j, id[0], id[1], ra);
+    if (has_b) load_span(a, h, sb, g, j, id[2], id[3], rb);
     attend_pair(a, ra, rb, has_b, qv, sa, sb, s_end, g, j, first, m, lsum, o);
   };
   // The first pair is peeled out of the loop: a split of up to 2*stride tokens
   // (512 with 8 wavefronts) then runs straight-line, with its loads issued
   // right behind the query loads instead of after a loop-header wait.
-  const int sa0 = s_begin + wv * kSpan;
   if (sa0 < s_end) {
-    two_spans(sa0, true);
-    for (int sa = sa0 + 2 * stride; sa < s_end; sa += 2 * stride) two_spans(sa, false);
+    two_spans(sa0, true, id0);
+    for (int sa = sa0 + 2 * stride; sa < s_end; sa += 2 * stride) {
+      int id[4];
+      ids(sa, id);
+      two_spans(sa, false, id);
+    }
   }
 
   // Merge the W wavefronts through LDS, one barrier per 8 query rows. Lane (g, j) holds
@@ -287,7 +316,7 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(const AttnArgs a) {
       }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < R * kD; idx += blockDim.x) {
+    for (int idx = threadIdx.x; idx < R * kD; idx += 64 * W) {
       const int row = idx / kD, d = idx - row * kD;
       float mw[kMaxWaves], M = -INFINITY;
 #pragma unroll
@@ -469,8 +498,10 @@ extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const
   }
   hipStream_t st = pdk::as_stream(stream);
   const size_t lds = (size_t)p.waves * min(G, kMergeRows) * kOStride * sizeof(float);
+  const uint32_t hgw = (uint32_t)n_kv_heads | ((uint32_t)G << 16) | ((uint32_t)p.waves << 24);
   hipLaunchKernelGGL(decode_attn_kernel, dim3(p.nsplit, n_kv_heads, B), dim3(64 * p.waves), lds, st,
-                     a);
+                     a.q, a.ck, a.cv, a.tables, a.ctx, hgw, a.max_blocks, a.num_blocks,
+                     a.split_tokens, a.nsplit, a.scale_log2, a.out, a.ws_ml, a.ws_o);
   int rc = pdk::check_launch("decode_attn_kernel");
   if (rc || p.nsplit == 1) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3(B * n_q_heads), dim3(kD), 0, st, a.ws_ml, a.ws_o,

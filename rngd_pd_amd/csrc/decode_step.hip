@@ -125,13 +125,29 @@ __device__ __forceinline__ uint16_t to_bf(float f) { return (uint16_t)pdk::f32_t
 // [B][NH][HD]; the rotated k and the v of the new token go to slot pos of the
 // paged cache (the one-hot injection of kernels/decode_batch.py:81-82 as a
 // store), K in the tiled block order of pdk::k_unit.
-__global__ void rope_append_kernel(const uint16_t* qkv, int64_t ld, uint16_t* q_out,
-                                   const float* inv_freq, const int32_t* ctx,
+//
+// With kSplits > 0 the row comes as kSplits fp32 partial sums of the q|k|v
+// projection (split-K, [split][B][ld]): they are added in split order and
+// rounded to bf16 once, the value the unsplit projection would have written.
+template <int kSplits>
+__global__ void rope_append_kernel(const void* src_, int64_t ld, int64_t split_stride,
+                                   uint16_t* q_out, const float* inv_freq, const int32_t* ctx,
                                    const int32_t* tables, int max_blocks, uint16_t* ck,
                                    uint16_t* cv, int num_blocks, int NH, int NKV, int HD) {
   const int head = blockIdx.x, b = blockIdx.y, i = threadIdx.x, half = HD >> 1;
   const int pos = ctx[b] - 1;
-  const uint16_t* row = qkv + (int64_t)b * ld;
+  // Element c of row b, already rounded to bf16.
+  auto val = [&](int64_t c) -> uint16_t {
+    if constexpr (kSplits == 0) {
+      return static_cast<const uint16_t*>(src_)[(int64_t)b * ld + c];
+    } else {
+      const float* p = static_cast<const float*>(src_) + (int64_t)b * ld + c;
+      float sum = p[0];
+#pragma unroll
+      for (int s = 1; s < kSplits; ++s) sum += p[s * split_stride];
+      return to_bf(sum);
+    }
+  };
   int blk = -1;
   if (pos >= 0 && pos < max_blocks * 16) {
     const int id = tables[(int64_t)b * max_blocks + (pos >> 4)];
@@ -139,8 +155,8 @@ __global__ void rope_append_kernel(const uint16_t* qkv, int64_t ld, uint16_t* q_
   }
   const int slot = pos & 15;
   if (head < NH + NKV) {
-    const uint16_t* src = row + (int64_t)head * HD;
-    const float a = bf(src[i]), c = bf(src[i + half]);
+    const int64_t c0 = (int64_t)head * HD;
+    const float a = bf(val(c0 + i)), c = bf(val(c0 + i + half));
     float s, co;
     sincosf((float)max(pos, 0) * inv_freq[i], &s, &co);
     const uint16_t o0 = to_bf(a * co - c * s), o1 = to_bf(c * co + a * s);
@@ -155,10 +171,10 @@ __global__ void rope_append_kernel(const uint16_t* qkv, int64_t ld, uint16_t* q_
     }
   } else if (blk >= 0) {
     const int vh = head - NH - NKV;
-    const uint16_t* src = row + (int64_t)(NH + NKV + vh) * HD;
+    const int64_t c0 = (int64_t)(NH + NKV + vh) * HD;
     uint16_t* vb = cv + ((int64_t)blk * NKV + vh) * HD * 16;
-    vb[(int64_t)i * 16 + slot] = src[i];
-    vb[(int64_t)(i + half) * 16 + slot] = src[i + half];
+    vb[(int64_t)i * 16 + slot] = val(c0 + i);
+    vb[(int64_t)(i + half) * 16 + slot] = val(c0 + i + half);
   }
 }
 
@@ -224,6 +240,23 @@ extern "C" int pdk_rmsnorm_partials(uint16_t* x, const float* partials, int spli
   return pdk::check_launch("rmsnorm_kernel");
 }
 
+static int check_rope(const void* src, const uint16_t* q_out, const float* inv_freq,
+                      const int32_t* ctx_lens, const int32_t* block_tables, int max_blocks,
+                      const uint16_t* cache_k, const uint16_t* cache_v, int num_blocks, int B,
+                      int n_q_heads, int n_kv_heads, int head_dim, int64_t ld) {
+  PDK_REQUIRE(src && q_out && inv_freq && ctx_lens && block_tables && cache_k && cache_v,
+              "null pointer argument");
+  PDK_REQUIRE(B >= 1 && B <= 65535, "B must be in [1, 65535] (got %d)", B);
+  PDK_REQUIRE(n_q_heads >= 1 && n_kv_heads >= 1 && n_q_heads + 2 * n_kv_heads <= 65535,
+              "head counts out of range");
+  PDK_REQUIRE(head_dim >= 32 && head_dim % 32 == 0 && head_dim <= 2048,
+              "head_dim must be a multiple of 32 in [32, 2048] (got %d)", head_dim);
+  PDK_REQUIRE(ld >= (int64_t)(n_q_heads + 2 * n_kv_heads) * head_dim,
+              "row stride %lld shorter than a (q, k, v) row", (long long)ld);
+  PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1, "num_blocks and max_blocks must be >= 1");
+  return PDK_OK;
+}
+
 extern "C" int pdk_rope_cache_append(const uint16_t* qkv, int64_t qkv_ld, uint16_t* q_out,
                                      const float* inv_freq, const int32_t* ctx_lens,
                                      const int32_t* block_tables, int max_blocks,
@@ -231,20 +264,38 @@ extern "C" int pdk_rope_cache_append(const uint16_t* qkv, int64_t qkv_ld, uint16
                                      int n_q_heads, int n_kv_heads, int head_dim,
                                      uintptr_t stream) {
   pdk::clear_error();
-  PDK_REQUIRE(qkv && q_out && inv_freq && ctx_lens && block_tables && cache_k && cache_v,
-              "null pointer argument");
-  PDK_REQUIRE(B >= 1 && B <= 65535, "B must be in [1, 65535] (got %d)", B);
-  PDK_REQUIRE(n_q_heads >= 1 && n_kv_heads >= 1 && n_q_heads + 2 * n_kv_heads <= 65535,
-              "head counts out of range");
-  PDK_REQUIRE(head_dim >= 32 && head_dim % 32 == 0 && head_dim <= 2048,
-              "head_dim must be a multiple of 32 in [32, 2048] (got %d)", head_dim);
-  PDK_REQUIRE(qkv_ld >= (int64_t)(n_q_heads + 2 * n_kv_heads) * head_dim,
-              "qkv_ld=%lld shorter than a (q, k, v) row", (long long)qkv_ld);
-  PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1, "num_blocks and max_blocks must be >= 1");
-  hipLaunchKernelGGL(rope_append_kernel, dim3(n_q_heads + 2 * n_kv_heads, B),
-                     dim3(head_dim / 2), 0, pdk::as_stream(stream), qkv, qkv_ld, q_out, inv_freq,
-                     ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads,
-                     n_kv_heads, head_dim);
+  if (int rc = check_rope(qkv, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k,
+                          cache_v, num_blocks, B, n_q_heads, n_kv_heads, head_dim, qkv_ld))
+    return rc;
+  hipLaunchKernelGGL(rope_append_kernel<0>, dim3(n_q_heads + 2 * n_kv_heads, B),
+                     dim3(head_dim / 2), 0, pdk::as_stream(stream), qkv, qkv_ld, (int64_t)0,
+                     q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v,
+                     num_blocks, n_q_heads, n_kv_heads, head_dim);
+  return pdk::check_launch("rope_append_kernel");
+}
+
+extern "C" int pdk_rope_cache_append_partials(const float* partials, int splits, int N,
+                                              uint16_t* q_out, const float* inv_freq,
+                                              const int32_t* ctx_lens,
+                                              const int32_t* block_tables, int max_blocks,
+                                              uint16_t* cache_k, uint16_t* cache_v,
+                                              int num_blocks, int B, int n_q_heads,
+                                              int n_kv_heads, int head_dim, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_rope(partials, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k,
+                          cache_v, num_blocks, B, n_q_heads, n_kv_heads, head_dim, N))
+    return rc;
+  const dim3 grid(n_q_heads + 2 * n_kv_heads, B), block(head_dim / 2);
+  const int64_t stride = (int64_t)B * N;
+  hipStream_t st = pdk::as_stream(stream);
+  switch (splits) {
+    case 1: hipLaunchKernelGGL(rope_append_kernel<1>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim); break;
+    case 2: hipLaunchKernelGGL(rope_append_kernel<2>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim); break;
+    case 4: hipLaunchKernelGGL(rope_append_kernel<4>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim); break;
+    default:
+      pdk::set_error("splits must be 1, 2 or 4 (got %d)", splits);
+      return PDK_EINVAL;
+  }
   return pdk::check_launch("rope_append_kernel");
 }
 

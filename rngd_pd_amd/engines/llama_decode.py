@@ -6,8 +6,8 @@ Replaces the reference's BatchDecodeEngine.step / step_logits
 (engines/decode_batch.py:162-171). Per layer, one launch per line:
 
   x = x + sum(partials); h = rmsnorm(x)           pdk_rmsnorm_partials (pdk_rmsnorm at layer 0)
-  qkv = h . Wqkv^T                                 pdk_linear
-  RoPE(q, k); new k, v into the paged cache         pdk_rope_cache_append
+  qkv = h . Wqkv^T                                 pdk_linear_splitk (2 fp32 halves of K; pdk_linear when K < 4096)
+  RoPE(q, k); new k, v into the paged cache         pdk_rope_cache_append_partials (adds the halves)
   ao = attention over slots 0..pos                 pdk_decode_attn (+ its merge)
   x = x + ao . Wo^T                                pdk_linear, residual fused
   h = rmsnorm(x)                                   pdk_rmsnorm
@@ -134,6 +134,13 @@ class LlamaDecoder:
         groups = (H + 63) // 64 if H >= 1024 else (H + 15) // 16
         self.down_splits = max(1, min(8, cfg.inter // 128, -(-256 // groups)))
         self.part = torch.empty((self.down_splits, B, H), dtype=torch.float32, device=dev)
+        # The q|k|v projection (N = 6144 at 8B) splits K in two when every wave
+        # of the GEMM still gets two 128-long steps of each half: 2 x 96 wide
+        # workgroups instead of 384 narrow ones, which re-read x per 16
+        # columns. The RoPE kernel adds the halves.
+        self.qkv_splits = 2 if H // 128 >= 32 else 1
+        self.part_qkv = torch.empty((self.qkv_splits, B, cfg.qkv_dim), dtype=torch.float32,
+                                    device=dev)
         self.inv = cfg.inv_freq().to(dev)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
         self._ws = None
@@ -193,14 +200,20 @@ class LlamaDecoder:
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
             torch.index_select(w.embed, 0, tokens.long(), out=x)
             partp, sp = self.part.data_ptr(), self.down_splits
+            pqp, qs = self.part_qkv.data_ptr(), self.qkv_splits
             for li, (n1, wqkv, wo, n2, wgu, wd, ck, cv) in enumerate(self._layers):
                 if li:      # the previous layer's down projection joins the residual here
                     call("pdk_rmsnorm_partials", xp, partp, sp, n1, B, H, eps, hp, st)
                 else:
                     call("pdk_rmsnorm", xp, None, n1, B, H, eps, hp, st)
-                call("pdk_linear", hp, wqkv, B, H, QKV, None, qkvp, st)
-                call("pdk_rope_cache_append", qkvp, QKV, qp, inv, cp, tp, mb, ck, cv, nb, B, NH,
-                     NKV, HD, st)
+                if qs > 1:
+                    call("pdk_linear_splitk", hp, wqkv, B, H, QKV, qs, pqp, st)
+                    call("pdk_rope_cache_append_partials", pqp, qs, QKV, qp, inv, cp, tp, mb, ck,
+                         cv, nb, B, NH, NKV, HD, st)
+                else:
+                    call("pdk_linear", hp, wqkv, B, H, QKV, None, qkvp, st)
+                    call("pdk_rope_cache_append", qkvp, QKV, qp, inv, cp, tp, mb, ck, cv, nb, B,
+                         NH, NKV, HD, st)
                 call("pdk_decode_attn", qp, ck, cv, nb, tp, mb, cp, int(max_ctx), B, NH, NKV, HD,
                      self.scale, ws_ptr, ws_bytes, aop, st)
                 call("pdk_linear", aop, wo, B, NH * HD, H, xp, xp, st)

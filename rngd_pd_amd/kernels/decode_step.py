@@ -67,6 +67,36 @@ def rope_cache_append(qkv, inv_freq, ctx_lens, block_tables, cache_k, cache_v, n
     return q_out
 
 
+def rope_cache_append_partials(partials, inv_freq, ctx_lens, block_tables, cache_k, cache_v,
+                               n_q_heads, q_out=None, stream=None):
+    """rope_cache_append from split-K partial sums of the q|k|v projection.
+
+    partials float32 [splits, B, N] (linear_splitk's output, N = (n_q + 2 n_kv)
+    * D), added in split order and rounded to bf16 per element first."""
+    _need(partials, "partials", torch.float32)
+    _need(inv_freq, "inv_freq", torch.float32)
+    _need(ctx_lens, "ctx_lens", torch.int32)
+    _need(block_tables, "block_tables", torch.int32)
+    nb, Hkv, D = _check_layer_cache(cache_k, cache_v)
+    if partials.dim() != 3 or not partials.is_contiguous():
+        raise ValueError("partials must be contiguous [splits, B, N]")
+    splits, B, N = partials.shape
+    if N != (n_q_heads + 2 * Hkv) * D:
+        raise ValueError(f"partials rows hold {N} values, need {(n_q_heads + 2 * Hkv) * D}")
+    if inv_freq.numel() != D // 2:
+        raise ValueError(f"inv_freq must hold head_dim/2 = {D // 2} values")
+    if ctx_lens.numel() != B or block_tables.dim() != 2 or block_tables.shape[0] != B \
+            or not block_tables.is_contiguous():
+        raise ValueError("ctx_lens [B] and contiguous block_tables [B, max_blocks] expected")
+    if q_out is None:
+        q_out = torch.empty((B, n_q_heads, D), dtype=cache_k.dtype, device=partials.device)
+    _lib.call("pdk_rope_cache_append_partials", partials.data_ptr(), splits, N, q_out.data_ptr(),
+              inv_freq.data_ptr(), ctx_lens.data_ptr(), block_tables.data_ptr(),
+              block_tables.shape[1], cache_k.data_ptr(), cache_v.data_ptr(), nb, B, n_q_heads,
+              Hkv, D, stream_handle(stream))
+    return q_out
+
+
 def swiglu(gate_up, out=None, stream=None):
     """gate_up [B, 2M] = [g | u] -> silu(g) * u [B, M]."""
     _need(gate_up, "gate_up")

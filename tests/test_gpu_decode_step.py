@@ -101,6 +101,49 @@ def test_rope_and_cache_write(cuda, D):
     np.testing.assert_array_equal(got_v, expect_v)
 
 
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_rope_from_partials_equals_rounded_sum(cuda, splits):
+    """Split-K partials of the q|k|v projection: the kernel adds them in split
+    order in fp32, rounds once to bf16, then does exactly what the bf16-row
+    kernel does on that row (bit-for-bit equal q, K and V cache contents)."""
+    from rngd_pd_amd import kernels as K
+    NH, NKV, D = 8, 2, 128
+    positions = [0, 17, 511, 4000]
+    B = len(positions)
+    rng = np.random.default_rng(100 + splits)
+    max_blocks = max(positions) // 16 + 1
+    nb = 2 * B + 1
+    tables = np.zeros((B, max_blocks), np.int32)
+    own = rng.permutation(np.arange(1, nb))[:B]
+    for b, p in enumerate(positions):
+        tables[b, p // 16] = own[b]
+    N = (NH + 2 * NKV) * D
+    part = (rng.standard_normal((splits, B, N)) * 3).astype(np.float32)
+    total = part[0].copy()
+    for s in range(1, splits):
+        total = total + part[s]                                    # float32, split order
+    rows = _bf16_bits_rne(total)
+    ck0, cv0 = rand_bf16(rng, (nb, NKV, 16, D)), rand_bf16(rng, (nb, NKV, D, 16))
+    inv = torch.from_numpy(od.inv_freq(D, 500000.0, LLAMA3)).to(cuda)
+    ctx = torch.tensor([p + 1 for p in positions], dtype=torch.int32, device=cuda)
+    tab = torch.from_numpy(tables).to(cuda)
+    print(f"rope_cache_append_partials splits={splits} positions={positions}", flush=True)
+    ck_a, cv_a = to_dev(ck0), to_dev(cv0)
+    q_a = K.rope_cache_append_partials(torch.from_numpy(part).to(cuda), inv, ctx, tab, ck_a, cv_a,
+                                       NH)
+    ck_b, cv_b = to_dev(ck0), to_dev(cv0)
+    q_b = K.rope_cache_append(to_dev(rows), inv, ctx, tab, ck_b, cv_b, NH)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(q_a), to_host(q_b))
+    np.testing.assert_array_equal(to_host(ck_a), to_host(ck_b))
+    np.testing.assert_array_equal(to_host(cv_a), to_host(cv_b))
+    # and the V slots hold the rounded sums themselves
+    got_v = to_host(cv_a)
+    for b, p in enumerate(positions):
+        np.testing.assert_array_equal(got_v[own[b], :, :, p % 16],
+                                      rows[b, (NH + NKV) * D:].reshape(NKV, D))
+
+
 @pytest.mark.parametrize("B,M", [(3, 14336), (1, 8), (16, 1024)])
 def test_swiglu(cuda, B, M):
     from rngd_pd_amd import kernels as K
