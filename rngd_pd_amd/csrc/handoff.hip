@@ -16,14 +16,14 @@
 // Cache policy. A launch that moves more bytes than the last-level cache holds
 // (kStreamBytes) uses streaming (non-temporal) accesses on its read-once side:
 // pack streams its prefill reads and whole-line frame writes, gather its frame
-// writes, scatter its frame reads. Scatter keeps ordinary stores: its V-block
-// stores are 32-byte pieces of a line that the L2 must combine before they
-// reach HBM (streaming them took the batch below from 104 to 177 us). Measured
-// on 8 Llama-3.1-8B requests (728 MiB packed, 452 MiB scattered; pack then
-// scatter): 283 us per pair with ordinary accesses, 258 us streaming. A
-// smaller launch keeps ordinary accesses, so a just-written frame can still be
-// in the cache when its consumer (a copy or the scatter) reads it: one
-// 512-token request packs in 22 us that way and in 28 us streaming.
+// writes, scatter its frame reads. Scatter's cache-block stores stay ordinary:
+// on 8 Llama-3.1-8B requests (452 MiB scattered right after their pack) they
+// take the scatter from 95 us with streaming stores to 78 us, and the pack
+// that follows is no slower for it; ordinary frame stores in pack instead cost
+// the scatter 8 us. A smaller launch keeps ordinary accesses, so a
+// just-written frame can still be in the cache when its consumer (a copy or
+// the scatter) reads it: one 512-token request packs in 22 us that way and in
+// 28 us streaming.
 
 #include <algorithm>
 
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
     const int b = blk[k >> 1];
     if (b >= 0) {
       uint16_t* ck = a.cache_k + (int64_t)l * a.cache_ls + ((int64_t)b * a.Hkv + h) * 16 * D;
-      pdk::st16_as<kStream>(ck + ((int64_t)((k & 1) * nS + 2 * dt) * 32 + lane) * 8,
+      pdk::st16(ck + ((int64_t)((k & 1) * nS + 2 * dt) * 32 + lane) * 8,
                             v8{{x.x, x.y, x.z, x.w}});
     }
   }
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
     const int b = blk[k >> 1];
     if (b >= 0) {
       uint16_t* cv = a.cache_v + (int64_t)l * a.cache_ls + ((int64_t)b * a.Hkv + h) * D * 16;
-      pdk::st16_as<kStream>(cv + ((int64_t)dt * 128 + (k & 1) * 64 + lane) * 8,
+      pdk::st16(cv + ((int64_t)dt * 128 + (k & 1) * 64 + lane) * 8,
                             v8{{x.x, x.y, x.z, x.w}});
     }
   }
