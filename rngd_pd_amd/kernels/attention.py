@@ -20,11 +20,12 @@ _WORKSPACES = {}
 
 
 def get_workspace(nbytes, device):
-    """A zero-initialised fp32 workspace of at least ``nbytes`` on ``device``.
+    """An fp32 workspace of at least ``nbytes`` on ``device``, kept per device.
 
-    The kernel's split counters must read zero before a call and every call
-    leaves them zero, so one buffer is reused across calls. It serves one
-    stream at a time: concurrent calls on different streams need their own."""
+    It holds the per-split partial maxima, sums and outputs of a split
+    context; every entry a call reads is written earlier in that call, so one
+    buffer is reused across calls without clearing. It serves one stream at a
+    time: concurrent calls on different streams need their own."""
     key = torch.device(device).index or 0
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
