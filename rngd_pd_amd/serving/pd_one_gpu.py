@@ -85,7 +85,11 @@ def producer(args):
     pre = LlamaPrefill(w, max_tokens=frame_tokens(args))
     t = IpcTransport(args.root, n_slots=args.ipc_slots)
     S = frame_tokens(args)
-    pre.forward([1] * 16)                                    # warm the library paths
+    # Warm the library paths at prompt lengths across the served range: the
+    # GEMM library picks (and loads on first use) a kernel per shape, which
+    # otherwise lands on the first requests' time to first token.
+    for n in sorted({16, args.min_len, args.max_len, *range(args.min_len, args.max_len, 128)}):
+        pre.forward([1] * max(1, min(n, S)))
     torch.cuda.synchronize()
     _say({"ev": "ready", "role": "producer", "pid": os.getpid()})
     for line in sys.stdin:
