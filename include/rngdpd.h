@@ -177,6 +177,27 @@ int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k,
                     void* workspace, size_t workspace_bytes, uint16_t* out,
                     uintptr_t stream);
 
+/* pdk_rope_cache_append_partials followed by pdk_decode_attn, in one launch:
+ * q, k and v of the new token come as split-K partial sums of the q|k|v
+ * projection (qkv_partials [splits][B][(n_q_heads + 2 n_kv_heads) head_dim]
+ * fp32, splits in {1, 2, 4}; inv_freq fp32 [head_dim/2]). Each workgroup adds
+ * the partials of its KV head's group in split order, rounds once to bf16,
+ * rotates q and k (RoPE at position ctx[b]-1), uses them for the new token in
+ * place of the cache's old contents, and the workgroup holding that position
+ * writes the new k and v into its cache slot. Outputs and cache contents are
+ * bit-identical to the two calls. Replaces the RoPE rotation, the one-hot
+ * cache injection and the attention of DecodeLayer.forward
+ * (kernels/decode_batch.py:69-85) as one step. Other arguments and limits as
+ * pdk_decode_attn (same workspace size). */
+int pdk_decode_attn_rope(const float* qkv_partials, int splits,
+                         const float* inv_freq, uint16_t* cache_k,
+                         uint16_t* cache_v, int num_blocks,
+                         const int32_t* block_tables, int max_blocks,
+                         const int32_t* ctx_lens, int max_ctx, int B,
+                         int n_q_heads, int n_kv_heads, int head_dim,
+                         float scale, void* workspace, size_t workspace_bytes,
+                         uint16_t* out, uintptr_t stream);
+
 /* Write one new token's k and v per stream at slot ctx[b]-1 of the paged
  * cache: the one-hot cache injection Kf = Kp + k*oh, Vf = Vp + v*oh
  * (kernels/decode_batch.py:81-82), done as a store.

@@ -72,6 +72,8 @@ SIGNATURES = {
     "pdk_decode_attn_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "pdk_decode_attn": (_I, [_P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, ctypes.c_float,
                              _P, _SZ, _P, _U]),
+    "pdk_decode_attn_rope": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I,
+                                  ctypes.c_float, _P, _SZ, _P, _U]),
     "pdk_cache_append": (_I, [_P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _U]),
     "pdk_greedy_argmax": (_I, [_P, _I, _I, _I64, _P, _U]),
     "pdk_rmsnorm": (_I, [_P, _P, _P, _I, _I, ctypes.c_float, _P, _U]),

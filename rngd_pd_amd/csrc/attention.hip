@@ -165,15 +165,95 @@ __device__ __forceinline__ void span_pv(Span& r, const float* p, uint32_t pmask,
   for (int n = 0; n < 8; ++n) o[n] = mfma(pv, r.vf[n], o[n]);
 }
 
+// The new token of the fused RoPE path: its position, its rotated k and its v
+// (bf16, in LDS), and where its cache slot lives.
+struct NewToken {
+  int pos, lane, Hkv, h;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* ck_w;
+  uint16_t* cv_w;
+};
+
+// Block of the new token in the span starting at `span` (its ids lo, hi), or
+// -1 when the span does not hold it or the id is invalid: only a valid block's
+// slot is written, by either path, and V of an invalid block is zeroed by
+// span_pv anyway.
+__device__ __forceinline__ int new_token_block(const NewToken& nt, int span, int lo, int hi,
+                                               int num_blocks) {
+  if (nt.pos < span || nt.pos >= span + kSpan) return -1;   // wavefront-uniform
+  const int blk = (nt.pos - span < 16) ? lo : hi;
+  return (blk >= 0 && blk < num_blocks) ? blk : -1;
+}
+
+// The span's K tiles take the new token's k in place of the cache's old
+// contents (lane (g, j): tile 0 row j is token span + 16 (j / 8) + 8 ((j % 8)
+// / 4) + j % 4, tile 1 the same + 4, pdk::k_unit's slot order), and the
+// wavefront writes k and v into the token's cache slot. Value selects, not a
+// branch choosing which register to store, keep the span in registers; they
+// sit right before the QK products, which wait for these loads anyway.
+__device__ __forceinline__ void patch_k(Span& r, int span, int blk, const NewToken& nt, int g,
+                                        int j) {
+  const int j8 = j & 7;
+  const int ta = span + ((j >> 3) << 4) + ((j8 >> 2) << 3) + (j8 & 3);
+  const bool in_a = ta == nt.pos, in_b = ta + 4 == nt.pos;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const v8 k = *reinterpret_cast<const v8*>(nt.k + 32 * s + 8 * g);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      r.ka[s].w[w] = in_a ? k.w[w] : r.ka[s].w[w];
+      r.kb[s].w[w] = in_b ? k.w[w] : r.kb[s].w[w];
+    }
+  }
+  const int slot = nt.pos & 15;
+  uint16_t* kb = nt.ck_w + ((int64_t)blk * nt.Hkv + nt.h) * 16 * kD;
+  uint16_t* vb = nt.cv_w + ((int64_t)blk * nt.Hkv + nt.h) * kD * 16;
+  if (nt.lane < kD / 8)
+    pdk::st16(kb + pdk::k_unit(slot, 8 * nt.lane, kD) * 8,
+              *reinterpret_cast<const v8*>(nt.k + 8 * nt.lane));
+#pragma unroll
+  for (int d = nt.lane; d < kD; d += 64) vb[(int64_t)d * 16 + slot] = nt.v[d];
+}
+
+// The span's V rows take the new token's v (lane (g, j) holds dims j + 16n of
+// tokens span + 8g .. + 7), right before the PV products.
+__device__ __forceinline__ void patch_v(Span& r, int span, const NewToken& nt, int g, int j) {
+  const int tv = span + 8 * g;
+  const bool in_v = nt.pos >= tv && nt.pos < tv + 8;
+  const int e = nt.pos - tv, word = e >> 1;
+  const uint32_t keep = (e & 1) ? 0x0000ffffu : 0xffff0000u;
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const uint32_t bits = (uint32_t)nt.v[(j + 16 * n) & (kD - 1)] << ((e & 1) * 16);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const bool hit = in_v && w == word;
+      r.vf[n].w[w] = hit ? ((r.vf[n].w[w] & keep) | bits) : r.vf[n].w[w];
+    }
+  }
+}
+
 // Fold spans A (and B, when has_b) into the running (m, lsum, o) of query
 // j = lane & 15 with one softmax over their 64 tokens. On the first pair the
 // running state is empty, so nothing is rescaled.
+// With kPatch (the fused RoPE path), ids are the spans' block ids (a lo, a
+// hi, b lo, b hi) and nt the new token, patched into whichever span holds it.
+template <bool kPatch>
 __device__ __forceinline__ void attend_pair(const AttnArgs& a, Span& ra, Span& rb, bool has_b,
                                             const v8 qv[4], int sa, int sb, int lim, int g, int j,
-                                            bool first, float& m, float& lsum, f32x4 o[8]) {
+                                            bool first, float& m, float& lsum, f32x4 o[8],
+                                            const NewToken& nt, const int* ids) {
+  int blk_a = -1, blk_b = -1;
+  if constexpr (kPatch) {
+    blk_a = new_token_block(nt, sa, ids[0], ids[1], a.num_blocks);
+    blk_b = has_b ? new_token_block(nt, sb, ids[2], ids[3], a.num_blocks) : -1;
+  }
   float sc[16];
+  if (kPatch && blk_a >= 0) patch_k(ra, sa, blk_a, nt, g, j);
   span_scores(ra, qv, a.scale_log2, sa + 8 * g, lim, sc);
   if (has_b) {
+    if (kPatch && blk_b >= 0) patch_k(rb, sb, blk_b, nt, g, j);
     span_scores(rb, qv, a.scale_log2, sb + 8 * g, lim, sc + 8);
   } else {
 #pragma unroll
@@ -206,20 +286,39 @@ __device__ __forceinline__ void attend_pair(const AttnArgs& a, Span& ra, Span& r
   }
   m = m_new;
   const uint32_t pmask = j < a.G ? 0xffffffffu : 0u;
+  if (kPatch && blk_a >= 0) patch_v(ra, sa, nt, g, j);
   span_pv(ra, p, pmask, sa + 8 * g, lim, o);
-  if (has_b) span_pv(rb, p + 8, pmask, sb + 8 * g, lim, o);
+  if (has_b) {
+    if (kPatch && blk_b >= 0) patch_v(rb, sb, nt, g, j);
+    span_pv(rb, p + 8, pmask, sb + 8 * g, lim, o);
+  }
 }
 
 // Scalar arguments, those the first loads need first: the compiler preloads
 // the leading ones into SGPRs (-amdgpu-kernarg-preload-count), so the query,
 // context-length and block-id loads issue without waiting for a kernarg read.
 // hgw packs Hkv (16 bits), G (8) and the wavefront count W (8).
-__global__ __launch_bounds__(512) void decode_attn_kernel(
+//
+// kRope = 0: q [B][Hq][D] bf16 as given. kRope = 1, 2 or 4: q, k and v of the
+// new token come as kRope fp32 split-K partial sums of the q|k|v projection
+// (part, [kRope][B][(Hq + 2 Hkv) D], split s at s * part_stride): the
+// workgroup adds them in split order, rounds to bf16, rotates q and k (RoPE at
+// position ctx-1, angle pos * inv_freq[i]) into LDS, writes the new k and v to
+// their cache slot (the workgroup whose split holds that position), and uses
+// them for the new token in place of the cache's contents. Every value is the
+// one pdk_rope_cache_append_partials computes, so the result is bit-identical
+// to that kernel followed by the kRope = 0 path.
+template <int kRope>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_attn_kernel(
     const uint16_t* q, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
     const int32_t* ctx_lens, uint32_t hgw, int max_blocks, int num_blocks, int split_tokens,
-    int nsplit, float scale_log2, uint16_t* out, float* ws_ml, float* ws_o) {
+    int nsplit, float scale_log2, uint16_t* out, float* ws_ml, float* ws_o,
+    const float* part, int64_t part_stride, const float* inv_freq, uint16_t* ck_w,
+    uint16_t* cv_w) {
   __shared__ float sm_m[kMaxWaves][kMaxG];
   __shared__ float sm_l[kMaxWaves][kMaxG];
+  __shared__ __align__(16) uint16_t q_rot[kRope ? kMaxG : 1][kD];   // rotated q of the group
+  __shared__ __align__(16) uint16_t kv_new[2][kD];                  // rotated k, v of the new token
   extern __shared__ float sm_o[];                // [W][min(G, kMergeRows)][kOStride]
 
   AttnArgs a;
@@ -238,12 +337,14 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(
   const int s_begin = split * a.split_tokens;
   const int32_t* table = a.tables + (int64_t)b * a.max_blocks;
 
-  const uint16_t* qp = a.q + ((int64_t)b * a.Hq + h * G + min(j, G - 1)) * kD + g * 8;
   v8 qv[4];
+  if constexpr (kRope == 0) {
+    const uint16_t* qp = a.q + ((int64_t)b * a.Hq + h * G + min(j, G - 1)) * kD + g * 8;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) qv[s] = pdk::ld16(qp + 32 * s);
-  // Columns j >= G repeat query G-1 (index clamped above); their P is zeroed
-  // before PV and their (m, lsum) are never read, so Q needs no mask.
+    for (int s = 0; s < 4; ++s) qv[s] = pdk::ld16(qp + 32 * s);
+  }
+  // Columns j >= G repeat query G-1 (index clamped); their P is zeroed before
+  // PV and their (m, lsum) are never read, so Q needs no mask.
 
   float m = -INFINITY, lsum = 0.f;
   f32x4 o[8];
@@ -261,6 +362,38 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int stride = W * kSpan;
   const int mb = a.max_blocks - 1;
+  // Fused RoPE, first phase: the partial sums of this wavefront's rows, loaded
+  // before its K/V loads so that using them does not wait for those (a
+  // wavefront's loads complete in order). Rows of 64 lanes: r < G the group's
+  // query heads (dims lane and lane + 64), r == G the new k, r == G+1, G+2 the
+  // new v (dims 64 (r - G - 1) + lane); row r belongs to wavefront r % W.
+  constexpr int kPre = 4;                        // rows per wavefront loaded early
+  constexpr int kParts = kRope > 0 ? kRope : 1;
+  const int n_rows = G + 3;
+  const int64_t n_qkv = (int64_t)(a.Hq + 2 * a.Hkv) * kD;
+  const float* prow = part + (int64_t)b * n_qkv;
+  auto row_col = [&](int r) -> int64_t {
+    return r < G ? (int64_t)(h * G + r) * kD
+         : r == G ? (int64_t)(a.Hq + h) * kD
+                  : (int64_t)(a.Hq + a.Hkv + h) * kD + (r - G - 1) * 64;
+  };
+  float raw[kPre][2][kParts];
+  float ifreq = 0.f;
+  if constexpr (kRope > 0) {
+    ifreq = inv_freq[lane];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+      const int r = wv + k * W;
+      if (r < n_rows) {
+        const int64_t c = row_col(r) + lane;
+#pragma unroll
+        for (int sp = 0; sp < kRope; ++sp) {
+          raw[k][0][sp] = prow[sp * part_stride + c];
+          raw[k][1][sp] = r <= G ? prow[sp * part_stride + c + 64] : 0.f;
+        }
+      }
+    }
+  }
   auto ids = [&](int sa, int* id) {
     const int sb = sa + stride;
     id[0] = table[min(sa >> 4, mb)];
@@ -274,23 +407,85 @@ __global__ __launch_bounds__(512) void decode_attn_kernel(
   asm volatile("" : "+s"(ctx_raw) : "s"(id0[0]), "s"(id0[1]), "s"(id0[2]), "s"(id0[3]));
   const int ctx = min(ctx_raw, a.max_blocks * 16);
   const int s_end = (split == a.nsplit - 1) ? ctx : min(ctx, s_begin + a.split_tokens);
-  auto two_spans = [&](int sa, bool first, const int* id) {
-    const int sb = sa + stride;
-    const bool has_b = sb < s_end;
-    Span ra, rb;
-    load_span(a, h, sa, g, j, id[0], id[1], ra);
-    if (has_b) load_span(a, h, sb, g, j, id[2], id[3], rb);
-    attend_pair(a, ra, rb, has_b, qv, sa, sb, s_end, g, j, first, m, lsum, o);
-  };
+  const int pos = ctx_raw - 1;                   // the new token (fused RoPE path)
   // The first pair is peeled out of the loop: a split of up to 2*stride tokens
   // (512 with 8 wavefronts) then runs straight-line, with its loads issued
   // right behind the query loads instead of after a loop-header wait.
-  if (sa0 < s_end) {
-    two_spans(sa0, true, id0);
+  const bool active = sa0 < s_end;
+  const int sb0 = sa0 + stride;
+  const bool has_b0 = sb0 < s_end;
+  // With the fused RoPE both spans' loads are issued unconditionally, those of
+  // a span without tokens from block 0 (cached after its first read): every
+  // path then has the same loads in flight, so the RoPE phase's wait counts
+  // only the partial sums' loads instead of draining all of them. Without it
+  // the loads stay under the branch (measured 0.5 us per layer faster).
+  Span ra0, rb0;
+  if constexpr (kRope > 0) {
+    load_span(a, h, sa0, g, j, active ? id0[0] : 0, active ? id0[1] : 0, ra0);
+    load_span(a, h, sb0, g, j, has_b0 ? id0[2] : 0, has_b0 ? id0[3] : 0, rb0);
+  } else if (active) {
+    load_span(a, h, sa0, g, j, id0[0], id0[1], ra0);
+    if (has_b0) load_span(a, h, sb0, g, j, id0[2], id0[3], rb0);
+  }
+  if constexpr (kRope > 0) {
+    // Second phase, while the first pair's K/V loads are in flight: add the
+    // partials in split order, round to bf16 (the projection's output), rotate
+    // q and k with the angle pos * inv_freq[lane], and put the group's q and
+    // the new k and v into LDS.
+    float sn, cs;
+    sincosf((float)max(pos, 0) * ifreq, &sn, &cs);
+    auto rnd = [](float x) { return pdk::bf16_to_f32(pdk::f32_to_bf16_rne(x)); };
+    auto put = [&](int r, float x0, float x1) {
+      if (r <= G) {
+        uint16_t* dst = r < G ? q_rot[r] : kv_new[0];
+        dst[lane] = (uint16_t)pdk::f32_to_bf16_rne(x0 * cs - x1 * sn);
+        dst[lane + 64] = (uint16_t)pdk::f32_to_bf16_rne(x1 * cs + x0 * sn);
+      } else {
+        kv_new[1][(r - G - 1) * 64 + lane] = (uint16_t)pdk::f32_to_bf16_rne(x0);
+      }
+    };
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+      const int r = wv + k * W;
+      if (r < n_rows) {
+        float x0 = raw[k][0][0], x1 = raw[k][1][0];
+#pragma unroll
+        for (int sp = 1; sp < kRope; ++sp) {
+          x0 += raw[k][0][sp];
+          x1 += raw[k][1][sp];
+        }
+        put(r, rnd(x0), rnd(x1));
+      }
+    }
+    for (int r = wv + kPre * W; r < n_rows; r += W) {      // one wavefront, G = 16: late rows
+      const int64_t c = row_col(r) + lane;
+      float x0 = prow[c], x1 = r <= G ? prow[c + 64] : 0.f;
+#pragma unroll
+      for (int sp = 1; sp < kRope; ++sp) {
+        x0 += prow[sp * part_stride + c];
+        x1 += r <= G ? prow[sp * part_stride + c + 64] : 0.f;
+      }
+      put(r, rnd(x0), rnd(x1));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qv[s] = *reinterpret_cast<const v8*>(&q_rot[min(j, G - 1)][32 * s + 8 * g]);
+  }
+  const NewToken nt{pos, lane, a.Hkv, h, kv_new[0], kv_new[1], ck_w, cv_w};
+  if (active) {
+    attend_pair<(kRope > 0)>(a, ra0, rb0, has_b0, qv, sa0, sb0, s_end, g, j, true, m, lsum, o, nt,
+                             id0);
     for (int sa = sa0 + 2 * stride; sa < s_end; sa += 2 * stride) {
       int id[4];
       ids(sa, id);
-      two_spans(sa, false, id);
+      const int sb = sa + stride;
+      const bool has_b = sb < s_end;
+      Span ra, rb;
+      load_span(a, h, sa, g, j, id[0], id[1], ra);
+      if (has_b) load_span(a, h, sb, g, j, id[2], id[3], rb);
+      attend_pair<(kRope > 0)>(a, ra, rb, has_b, qv, sa, sb, s_end, g, j, false, m, lsum, o, nt,
+                               id);
     }
   }
 
@@ -445,12 +640,22 @@ extern "C" size_t pdk_decode_attn_workspace_bytes(int B, int n_q_heads, int max_
   return ws_bytes(B, n_q_heads, min(kMaxSplits, max(1, (max_ctx + 127) / 128)));
 }
 
-extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
-                               int num_blocks, const int32_t* block_tables, int max_blocks,
-                               const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads,
-                               int n_kv_heads, int head_dim, float scale, void* workspace,
-                               size_t workspace_bytes, uint16_t* out, uintptr_t stream) {
-  pdk::clear_error();
+namespace {
+
+// Inputs of the fused RoPE path (null part: q given).
+struct RopeIn {
+  const float* part;
+  int splits;
+  const float* inv_freq;
+  uint16_t* ck_w;
+  uint16_t* cv_w;
+};
+
+int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
+                int num_blocks, const int32_t* block_tables, int max_blocks,
+                const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads, int n_kv_heads,
+                int head_dim, float scale, void* workspace, size_t workspace_bytes, uint16_t* out,
+                uintptr_t stream, const RopeIn& rope) {
   if (head_dim != kD) {
     pdk::set_error("decode attention implements head_dim %d only (got %d)", kD, head_dim);
     return PDK_ENOTSUP;
@@ -464,9 +669,9 @@ extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const
     pdk::set_error("GQA group %d not in {1,2,4,8,16}", G);
     return PDK_ENOTSUP;
   }
-  PDK_REQUIRE(q && cache_k && cache_v && out && block_tables && ctx_lens,
+  PDK_REQUIRE((q || rope.part) && cache_k && cache_v && out && block_tables && ctx_lens,
               "null pointer argument");
-  PDK_REQUIRE(pdk::aligned16(q) && pdk::aligned16(cache_k) && pdk::aligned16(cache_v),
+  PDK_REQUIRE((!q || pdk::aligned16(q)) && pdk::aligned16(cache_k) && pdk::aligned16(cache_v),
               "q/cache_k/cache_v must be 16-byte aligned");
   PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1, "num_blocks and max_blocks must be >= 1");
   PDK_REQUIRE(max_ctx >= 1 && max_ctx <= max_blocks * 16,
@@ -499,14 +704,58 @@ extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const
   hipStream_t st = pdk::as_stream(stream);
   const size_t lds = (size_t)p.waves * min(G, kMergeRows) * kOStride * sizeof(float);
   const uint32_t hgw = (uint32_t)n_kv_heads | ((uint32_t)G << 16) | ((uint32_t)p.waves << 24);
-  hipLaunchKernelGGL(decode_attn_kernel, dim3(p.nsplit, n_kv_heads, B), dim3(64 * p.waves), lds, st,
-                     a.q, a.ck, a.cv, a.tables, a.ctx, hgw, a.max_blocks, a.num_blocks,
-                     a.split_tokens, a.nsplit, a.scale_log2, a.out, a.ws_ml, a.ws_o);
+  const dim3 grid(p.nsplit, n_kv_heads, B), block(64 * p.waves);
+  const int64_t pstride = (int64_t)B * (n_q_heads + 2 * n_kv_heads) * kD;
+#define PDK_ATTN_LAUNCH(R)                                                                      \
+  hipLaunchKernelGGL(decode_attn_kernel<R>, grid, block, lds, st, a.q, a.ck, a.cv, a.tables,   \
+                     a.ctx, hgw, a.max_blocks, a.num_blocks, a.split_tokens, a.nsplit,         \
+                     a.scale_log2, a.out, a.ws_ml, a.ws_o, rope.part, pstride, rope.inv_freq,  \
+                     rope.ck_w, rope.cv_w)
+  switch (rope.part ? rope.splits : 0) {
+    case 0: PDK_ATTN_LAUNCH(0); break;
+    case 1: PDK_ATTN_LAUNCH(1); break;
+    case 2: PDK_ATTN_LAUNCH(2); break;
+    case 4: PDK_ATTN_LAUNCH(4); break;
+    default:
+      pdk::set_error("splits must be 1, 2 or 4 (got %d)", rope.splits);
+      return PDK_EINVAL;
+  }
+#undef PDK_ATTN_LAUNCH
   int rc = pdk::check_launch("decode_attn_kernel");
   if (rc || p.nsplit == 1) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3(B * n_q_heads), dim3(kD), 0, st, a.ws_ml, a.ws_o,
                      p.nsplit, out);
   return pdk::check_launch("merge_kernel");
+}
+
+}  // namespace
+
+extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
+                               int num_blocks, const int32_t* block_tables, int max_blocks,
+                               const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads,
+                               int n_kv_heads, int head_dim, float scale, void* workspace,
+                               size_t workspace_bytes, uint16_t* out, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(q, "null pointer argument");
+  return launch_attn(q, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens, max_ctx,
+                     B, n_q_heads, n_kv_heads, head_dim, scale, workspace, workspace_bytes, out,
+                     stream, RopeIn{nullptr, 0, nullptr, nullptr, nullptr});
+}
+
+extern "C" int pdk_decode_attn_rope(const float* qkv_partials, int splits, const float* inv_freq,
+                                    uint16_t* cache_k, uint16_t* cache_v, int num_blocks,
+                                    const int32_t* block_tables, int max_blocks,
+                                    const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads,
+                                    int n_kv_heads, int head_dim, float scale, void* workspace,
+                                    size_t workspace_bytes, uint16_t* out, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(qkv_partials && inv_freq, "null pointer argument");
+  PDK_REQUIRE(splits == 1 || splits == 2 || splits == 4, "splits must be 1, 2 or 4 (got %d)",
+              splits);
+  return launch_attn(nullptr, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens,
+                     max_ctx, B, n_q_heads, n_kv_heads, head_dim, scale, workspace,
+                     workspace_bytes, out, stream,
+                     RopeIn{qkv_partials, splits, inv_freq, cache_k, cache_v});
 }
 
 extern "C" int pdk_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* cache_k,

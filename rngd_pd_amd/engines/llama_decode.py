@@ -6,9 +6,9 @@ Replaces the reference's BatchDecodeEngine.step / step_logits
 (engines/decode_batch.py:162-171). Per layer, one launch per line:
 
   x = x + sum(partials); h = rmsnorm(x)           pdk_rmsnorm_partials (pdk_rmsnorm at layer 0)
-  qkv = h . Wqkv^T                                 pdk_linear_splitk (2 fp32 halves of K; pdk_linear when K < 4096)
-  RoPE(q, k); new k, v into the paged cache         pdk_rope_cache_append_partials (adds the halves)
-  ao = attention over slots 0..pos                 pdk_decode_attn (+ its merge)
+  qkv = h . Wqkv^T                                 pdk_linear_splitk (fp32 halves of K; one part when K < 4096)
+  RoPE(q, k); new k, v into the paged cache;
+  ao = attention over slots 0..pos                 pdk_decode_attn_rope (+ its merge when split)
   x = x + ao . Wo^T                                pdk_linear, residual fused
   h = rmsnorm(x)                                   pdk_rmsnorm
   a = silu(h . Wg^T) * (h . Wu^T)                  pdk_linear_swiglu
@@ -122,8 +122,6 @@ class LlamaDecoder:
         self.max_batch = B
         e = lambda *s: torch.empty(s, dtype=BF16, device=dev)   # noqa: E731
         self.x, self.h = e(B, H), e(B, H)
-        self.qkv = e(B, cfg.qkv_dim)
-        self.q = e(B, cfg.n_heads, cfg.head_dim)
         self.ao = e(B, cfg.n_heads, cfg.head_dim)
         self.act = e(B, cfg.inter)
         self.logits = e(B, cfg.vocab)
@@ -137,7 +135,7 @@ class LlamaDecoder:
         # The q|k|v projection (N = 6144 at 8B) splits K in two when every wave
         # of the GEMM still gets two 128-long steps of each half: 2 x 96 wide
         # workgroups instead of 384 narrow ones, which re-read x per 16
-        # columns. The RoPE kernel adds the halves.
+        # columns. The attention kernel adds the halves (and applies RoPE).
         self.qkv_splits = 2 if H // 128 >= 32 else 1
         self.part_qkv = torch.empty((self.qkv_splits, B, cfg.qkv_dim), dtype=torch.float32,
                                     device=dev)
@@ -194,7 +192,7 @@ class LlamaDecoder:
         ws_bytes = ws.numel() * 4 if ws is not None else 0
         mb, nb = tables.shape[1], cache.num_blocks
         tp, cp = tables.data_ptr(), ctx_lens.data_ptr()
-        xp, hp, qkvp, qp = x.data_ptr(), self.h.data_ptr(), self.qkv.data_ptr(), self.q.data_ptr()
+        xp, hp = x.data_ptr(), self.h.data_ptr()
         aop, actp, inv = self.ao.data_ptr(), self.act.data_ptr(), self.inv.data_ptr()
         call = _lib.call
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
@@ -206,16 +204,9 @@ class LlamaDecoder:
                     call("pdk_rmsnorm_partials", xp, partp, sp, n1, B, H, eps, hp, st)
                 else:
                     call("pdk_rmsnorm", xp, None, n1, B, H, eps, hp, st)
-                if qs > 1:
-                    call("pdk_linear_splitk", hp, wqkv, B, H, QKV, qs, pqp, st)
-                    call("pdk_rope_cache_append_partials", pqp, qs, QKV, qp, inv, cp, tp, mb, ck,
-                         cv, nb, B, NH, NKV, HD, st)
-                else:
-                    call("pdk_linear", hp, wqkv, B, H, QKV, None, qkvp, st)
-                    call("pdk_rope_cache_append", qkvp, QKV, qp, inv, cp, tp, mb, ck, cv, nb, B,
-                         NH, NKV, HD, st)
-                call("pdk_decode_attn", qp, ck, cv, nb, tp, mb, cp, int(max_ctx), B, NH, NKV, HD,
-                     self.scale, ws_ptr, ws_bytes, aop, st)
+                call("pdk_linear_splitk", hp, wqkv, B, H, QKV, qs, pqp, st)
+                call("pdk_decode_attn_rope", pqp, qs, inv, ck, cv, nb, tp, mb, cp, int(max_ctx),
+                     B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, st)
                 call("pdk_linear", aop, wo, B, NH * HD, H, xp, xp, st)
                 call("pdk_rmsnorm", xp, None, n2, B, H, eps, hp, st)
                 call("pdk_linear_swiglu", hp, wgu, B, H, M, actp, st)

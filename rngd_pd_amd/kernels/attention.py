@@ -84,6 +84,49 @@ def decode_attention(q, cache_k, cache_v, block_tables, ctx_lens, max_ctx, scale
     return out
 
 
+def decode_attention_rope(qkv_partials, inv_freq, cache_k, cache_v, block_tables, ctx_lens,
+                          max_ctx, n_q_heads, scale=1.0, out=None, workspace=None, stream=None):
+    """RoPE, the new token's cache write and attention for one layer in one launch.
+
+    qkv_partials float32 [splits, B, (n_q + 2 n_kv) D] (split-K partial sums of
+    the q|k|v projection, splits in {1, 2, 4}); inv_freq float32 [D/2]. Same
+    result, bit for bit, as rope_cache_append_partials then decode_attention."""
+    _need(qkv_partials, "qkv_partials", torch.float32)
+    _need(inv_freq, "inv_freq", torch.float32)
+    nb, H, D = _check_layer_cache(cache_k, cache_v)
+    if qkv_partials.dim() != 3 or not qkv_partials.is_contiguous():
+        raise ValueError("qkv_partials must be contiguous [splits, B, N]")
+    splits, B, N = qkv_partials.shape
+    if N != (n_q_heads + 2 * H) * D:
+        raise ValueError(f"qkv_partials rows hold {N} values, need {(n_q_heads + 2 * H) * D}")
+    if inv_freq.numel() != D // 2:
+        raise ValueError(f"inv_freq must hold head_dim/2 = {D // 2} values")
+    _need(block_tables, "block_tables", torch.int32)
+    _need(ctx_lens, "ctx_lens", torch.int32)
+    if block_tables.dim() != 2 or block_tables.shape[0] != B or not block_tables.is_contiguous():
+        raise ValueError("block_tables must be contiguous int32 [B, max_blocks]")
+    if ctx_lens.numel() != B:
+        raise ValueError("ctx_lens must hold B entries")
+    if out is None:
+        out = torch.empty((B, n_q_heads, D), dtype=cache_k.dtype, device=cache_k.device)
+    need = workspace_bytes(B, n_q_heads, max_ctx, D)
+    ws = None
+    if need:
+        if workspace is not None:
+            if workspace.numel() * workspace.element_size() < need:
+                raise ValueError(f"workspace holds fewer than the {need} bytes needed")
+            ws = workspace
+        else:
+            ws = get_workspace(need, cache_k.device)
+    _lib.call("pdk_decode_attn_rope", qkv_partials.data_ptr(), splits, inv_freq.data_ptr(),
+              cache_k.data_ptr(), cache_v.data_ptr(), nb, block_tables.data_ptr(),
+              block_tables.shape[1], ctx_lens.data_ptr(), int(max_ctx), B, n_q_heads, H, D,
+              float(scale), ws.data_ptr() if ws is not None else None,
+              ws.numel() * ws.element_size() if ws is not None else 0, out.data_ptr(),
+              stream_handle(stream))
+    return out
+
+
 def cache_append(k_new, v_new, cache_k, cache_v, block_tables, ctx_lens, stream=None):
     """Write each stream's new k/v [B, Hkv, D] at slot ctx_lens[b]-1
     (the one-hot injection of kernels/decode_batch.py:81-82)."""

@@ -144,6 +144,46 @@ def test_rope_from_partials_equals_rounded_sum(cuda, splits):
                                       rows[b, (NH + NKV) * D:].reshape(NKV, D))
 
 
+@pytest.mark.parametrize("B,splits", [(16, 2), (4, 2), (1, 1), (5, 4)])
+def test_fused_rope_attention_equals_two_calls(cuda, B, splits):
+    """pdk_decode_attn_rope against pdk_rope_cache_append_partials followed by
+    pdk_decode_attn on copies of the same cache: bit-identical outputs and
+    cache contents, over context lengths that put the new token at a block's
+    first, last and middle slot, past one workgroup's 512 tokens, in the
+    context splits of small batches, and in a block whose id is invalid (no
+    cache write on either path)."""
+    from rngd_pd_amd import kernels as K
+    NH, NKV, D = 32, 8, 128
+    ctx_pool = [1, 16, 17, 512, 511, 300, 1000, 33, 64, 129, 700, 2, 48, 250, 999, 15]
+    ctx = ctx_pool[:B]
+    rng = np.random.default_rng(300 + 7 * B + splits)
+    max_blocks = (max(ctx) + 15) // 16
+    nb = B * max_blocks + 3
+    tables = rng.permutation(nb)[:B * max_blocks].astype(np.int32).reshape(B, max_blocks)
+    if B >= 4:
+        b = 3                                           # the new token's block id is invalid
+        tables[b, (ctx[b] - 1) // 16] = -1
+    N = (NH + 2 * NKV) * D
+    part = (rng.standard_normal((splits, B, N)) * 2).astype(np.float32)
+    ck0, cv0 = rand_bf16(rng, (nb, NKV, 16, D)), rand_bf16(rng, (nb, NKV, D, 16))
+    inv = torch.from_numpy(od.inv_freq(D, 500000.0, LLAMA3)).to(cuda)
+    ctx_t = torch.tensor(ctx, dtype=torch.int32, device=cuda)
+    tab = torch.from_numpy(tables).to(cuda)
+    part_d = torch.from_numpy(part).to(cuda)
+    scale = 1.0 / math.sqrt(D)
+    print(f"fused rope+attention B={B} splits={splits} ctx={ctx}", flush=True)
+    ck_a, cv_a = to_dev(ck0), to_dev(cv0)
+    q = K.rope_cache_append_partials(part_d, inv, ctx_t, tab, ck_a, cv_a, NH)
+    out_a = K.decode_attention(q, ck_a, cv_a, tab, ctx_t, max(ctx), scale=scale)
+    ck_b, cv_b = to_dev(ck0), to_dev(cv0)
+    out_b = K.decode_attention_rope(part_d, inv, ck_b, cv_b, tab, ctx_t, max(ctx), NH,
+                                    scale=scale)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(out_b), to_host(out_a))
+    np.testing.assert_array_equal(to_host(ck_b), to_host(ck_a))
+    np.testing.assert_array_equal(to_host(cv_b), to_host(cv_a))
+
+
 @pytest.mark.parametrize("B,M", [(3, 14336), (1, 8), (16, 1024)])
 def test_swiglu(cuda, B, M):
     from rngd_pd_amd import kernels as K
