@@ -223,7 +223,9 @@ template <int kEpi>
 int launch(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
            uint16_t* y, uint64_t* keys, hipStream_t st) {
   const int64_t wide = (N + 63) / 64;                // workgroups with 4 tiles
-  const bool four = kEpi == kSwiGLU ? wide >= 192 : (B > 8 && wide >= 1024);
+  // Wide SwiGLU tiles hold 8 weight tiles per step in registers: beyond 32
+  // streams they would spill, and one tile is used instead.
+  const bool four = kEpi == kSwiGLU ? (wide >= 192 && B <= 32) : (B > 8 && wide >= 1024);
   if (four) return launch_cols<4, kEpi>(x, w, B, K, N, r, y, keys, st);
   return launch_cols<1, kEpi>(x, w, B, K, N, r, y, keys, st);
 }

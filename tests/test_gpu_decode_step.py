@@ -250,7 +250,8 @@ def test_linear_splitk_and_rmsnorm_partials(cuda, B, K, N, splits):
                                    rtol=HALF_ULP, atol=1e-6)
 
 
-@pytest.mark.parametrize("B,K,M", [(4, 4096, 14336), (16, 128, 16), (40, 512, 64), (3, 256, 24)])
+@pytest.mark.parametrize("B,K,M", [(4, 4096, 14336), (16, 128, 16), (40, 512, 64), (3, 256, 24),
+                                   (40, 256, 12288), (24, 256, 12288)])
 def test_linear_swiglu(cuda, B, K, M):
     from rngd_pd_amd import kernels as K_
     rng = np.random.default_rng(B + K + M)
