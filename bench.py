@@ -650,6 +650,36 @@ def bench_cpu(args, out):
     }
     log(f"cpu baseline: {out['cpu_baseline']['value']} GB/s, "
         f"{out['cpu_baseline']['ms_per_request_median']} ms/request")
+    bench_cpu_attention(args, out)
+
+
+def bench_cpu_attention(args, out, B=16, ctx=512):
+    """Decode attention's CPU baseline: the oracle's fp32 restatement of
+    cpu_layer's attention (numpy einsum, one thread), on a bounded sample of
+    the B=16, context 512 layers the GPU leg runs."""
+    from oracle import attention as oatt
+    rng = np.random.default_rng(3)
+    NKV, HQ_, HD = H, HQ, D
+    q = rng.standard_normal((B, HQ_, HD)).astype(np.float32)
+    Kd = rng.standard_normal((B, NKV, HD, ctx)).astype(np.float32)
+    Vd = rng.standard_normal((B, NKV, ctx, HD)).astype(np.float32)
+    pos = [ctx - 1] * B
+    oatt.cpu_attention(q, Kd, Vd, pos)                         # warm
+    times = []
+    t0 = time.perf_counter()
+    while not times or (time.perf_counter() - t0 < min(5.0, args.cpu_seconds / 2)
+                        and len(times) < 64):
+        t = time.perf_counter()
+        oatt.cpu_attention(q, Kd, Vd, pos)
+        times.append(time.perf_counter() - t)
+    per_layer = statistics.median(times)
+    out["extra"]["cpu_baseline_attention"] = {
+        "tokens_per_s": round(B / (per_layer * L), 2), "unit": "tokens/s (attention-only step)",
+        "ms_per_layer": round(per_layer * 1e3, 3), "threads": 1, "kind": "port",
+        "sample": f"{len(times)} layers of B={B}, context {ctx}, Hq {HQ_}, Hkv {NKV}, fp32 numpy "
+                  f"einsum (no BLAS), median per layer x {L} layers per step"}
+    log(f"cpu attention baseline: {per_layer * 1e3:.2f} ms/layer, "
+        f"{out['extra']['cpu_baseline_attention']['tokens_per_s']} tokens/s")
 
 
 def bench_copy(args, torch, K, dev):
