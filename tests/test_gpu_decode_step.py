@@ -144,19 +144,21 @@ def test_rope_from_partials_equals_rounded_sum(cuda, splits):
                                       rows[b, (NH + NKV) * D:].reshape(NKV, D))
 
 
-@pytest.mark.parametrize("B,splits", [(16, 2), (4, 2), (1, 1), (5, 4)])
-def test_fused_rope_attention_equals_two_calls(cuda, B, splits):
+@pytest.mark.parametrize("B,splits,NH,NKV", [(16, 2, 32, 8), (4, 2, 32, 8), (1, 1, 32, 8),
+                                             (5, 4, 32, 8), (4, 2, 8, 8), (3, 1, 16, 8),
+                                             (6, 2, 64, 8), (2, 4, 32, 2), (16, 1, 16, 1)])
+def test_fused_rope_attention_equals_two_calls(cuda, B, splits, NH, NKV):
     """pdk_decode_attn_rope against pdk_rope_cache_append_partials followed by
     pdk_decode_attn on copies of the same cache: bit-identical outputs and
     cache contents, over context lengths that put the new token at a block's
     first, last and middle slot, past one workgroup's 512 tokens, in the
     context splits of small batches, and in a block whose id is invalid (no
-    cache write on either path)."""
+    cache write on either path); GQA groups of 1 to 16 query heads."""
     from rngd_pd_amd import kernels as K
-    NH, NKV, D = 32, 8, 128
+    D = 128
     ctx_pool = [1, 16, 17, 512, 511, 300, 1000, 33, 64, 129, 700, 2, 48, 250, 999, 15]
     ctx = ctx_pool[:B]
-    rng = np.random.default_rng(300 + 7 * B + splits)
+    rng = np.random.default_rng(300 + 7 * B + splits + NH + NKV)
     max_blocks = (max(ctx) + 15) // 16
     nb = B * max_blocks + 3
     tables = rng.permutation(nb)[:B * max_blocks].astype(np.int32).reshape(B, max_blocks)
@@ -171,7 +173,7 @@ def test_fused_rope_attention_equals_two_calls(cuda, B, splits):
     tab = torch.from_numpy(tables).to(cuda)
     part_d = torch.from_numpy(part).to(cuda)
     scale = 1.0 / math.sqrt(D)
-    print(f"fused rope+attention B={B} splits={splits} ctx={ctx}", flush=True)
+    print(f"fused rope+attention B={B} splits={splits} heads={NH}/{NKV} ctx={ctx}", flush=True)
     ck_a, cv_a = to_dev(ck0), to_dev(cv0)
     q = K.rope_cache_append_partials(part_d, inv, ctx_t, tab, ck_a, cv_a, NH)
     out_a = K.decode_attention(q, ck_a, cv_a, tab, ctx_t, max(ctx), scale=scale)
