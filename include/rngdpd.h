@@ -305,6 +305,30 @@ int pdk_linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N,
                       uint16_t* logits, uint64_t* keys, int32_t* tokens,
                       uintptr_t stream);
 
+/* Tiled weights: the four GEMMs above also take w as a tiled copy, written
+ * once (at weight load) by pdk_weight_tile, in which every 16-row x 128-column
+ * block is contiguous in the order the kernels' load instructions read it, so
+ * that the weight stream is read linearly. The copy holds
+ * pdk_weight_tiled_elems(N, K) = ceil(N/16)*16*K bf16 (rows >= N zero):
+ * element ((c*4 + kg)*16 + col)*8 + e of block (t, s), which starts at
+ * (t*(K/128) + s)*2048, is w[16t + col][128s + 32c + 8kg + e]. A gate|up
+ * weight [2M][K] is tiled as one matrix and needs M % 16 == 0. Results are
+ * bit-identical to the [out][in] entry points. No reference counterpart: the
+ * reference's weights stay in their torch layout (engines/decode_batch.py:
+ * 458-460); this is a load-time relayout of the same values.
+ * pdk_weight_tiled_elems returns 0 for an invalid shape. */
+int64_t pdk_weight_tiled_elems(int N, int K);
+int pdk_weight_tile(const uint16_t* w, int N, int K, uint16_t* wt, uintptr_t stream);
+int pdk_linear_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                     const uint16_t* residual, uint16_t* y, uintptr_t stream);
+int pdk_linear_splitk_tiled(const uint16_t* x, const uint16_t* wt, int B, int K,
+                            int N, int splits, float* partials, uintptr_t stream);
+int pdk_linear_swiglu_tiled(const uint16_t* x, const uint16_t* wt_gate_up, int B,
+                            int K, int M, uint16_t* y, uintptr_t stream);
+int pdk_linear_argmax_tiled(const uint16_t* x, const uint16_t* wt, int B, int K,
+                            int N, uint16_t* logits, uint64_t* keys,
+                            int32_t* tokens, uintptr_t stream);
+
 /* ---- KONI token blocks (second frame format) --------------------------------
  * The Furiosa native connector's KV payload (native_v4/kv.py:1-20): units of
  * one token of one tensor (t = 2*layer + 0 for K, 1 for V), each [Hkv][D] bf16,

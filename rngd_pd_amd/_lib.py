@@ -87,6 +87,12 @@ SIGNATURES = {
     "pdk_linear_splitk": (_I, [_P, _P, _I, _I, _I, _I, _P, _U]),
     "pdk_rmsnorm_partials": (_I, [_P, _P, _I, _P, _I, _I, ctypes.c_float, _P, _U]),
     "pdk_linear_argmax": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _U]),
+    "pdk_weight_tiled_elems": (_I64, [_I, _I]),
+    "pdk_weight_tile": (_I, [_P, _I, _I, _P, _U]),
+    "pdk_linear_tiled": (_I, [_P, _P, _I, _I, _I, _P, _P, _U]),
+    "pdk_linear_swiglu_tiled": (_I, [_P, _P, _I, _I, _I, _P, _U]),
+    "pdk_linear_splitk_tiled": (_I, [_P, _P, _I, _I, _I, _I, _P, _U]),
+    "pdk_linear_argmax_tiled": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _U]),
     "pdk_scatter_koni": (_I, [_P, _I64, _P, _I, _I, _P, _I, _P, _P, _I64, _I, _I, _I, _U]),
     "pdk_host_alloc": (_I, [_SZ, ctypes.POINTER(_P)]),
     "pdk_host_free": (_I, [_P]),

@@ -19,6 +19,15 @@
 //     SwiGLU) runs on the fp32 sums before the single bf16 rounding.
 // W is read with ordinary loads: non-temporal ones measured 10-25 % slower
 // here, although a decode step streams every weight once.
+//
+// Tiled weights. The same GEMMs also take W as a tiled copy (pdk_weight_tile)
+// in which the 4 KiB that a wavefront reads for one 16-column tile and one
+// 128-long k step are contiguous, in the order the lanes read them: each load
+// instruction then reads 1 KiB of consecutive bytes instead of 64 bytes of
+// each of 16 rows, and a workgroup streams its columns' weights linearly.
+//   tile t = rows 16t .. 16t+15 (rows >= N zero), K/128 step blocks of 2048
+//   elements each; element ((c * 4 + kg) * 16 + col) * 8 + e of step block s
+//   is W[16t + col][128 s + 32 c + 8 kg + e].
 
 #include <math.h>
 
@@ -66,7 +75,7 @@ constexpr int depth_for(int tiles) {
 // its waves share them and split K); kEpi selects the epilogue. For kSwiGLU the
 // workgroup also computes the matching up columns (rows n and M + n of W) and
 // writes silu(g) * u.
-template <int kTiles, int kCols, int kEpi>
+template <int kTiles, int kCols, int kEpi, bool kTiled>
 __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w, int B,
                                                             int K, int N,
@@ -80,11 +89,17 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   const int col = lane & 15, kg = lane >> 4;
   const int n0 = blockIdx.x * 16 * kCols;
   const uint16_t* wp[kW];
+  const int n_tiles = (N + 15) >> 4;
 #pragma unroll
   for (int p = 0; p < kPairs; ++p)
 #pragma unroll
-    for (int c = 0; c < kCols; ++c)
-      wp[p * kCols + c] = w + ((int64_t)p * N + min(n0 + 16 * c + col, N - 1)) * K + kg * 8;
+    for (int c = 0; c < kCols; ++c) {
+      if (kTiled)   // tile of columns n0 + 16c (the last one past N), rows of pair p after it
+        wp[p * kCols + c] =
+            w + ((int64_t)p * n_tiles + min((n0 >> 4) + c, n_tiles - 1)) * 16 * K + lane * 8;
+      else
+        wp[p * kCols + c] = w + ((int64_t)p * N + min(n0 + 16 * c + col, N - 1)) * K + kg * 8;
+    }
   const uint16_t* xp[kTiles];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) xp[t] = x + (int64_t)min(t * 16 + col, B - 1) * K + kg * 8;
@@ -104,17 +119,13 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   const int s_lo = (int)((int64_t)blockIdx.y * steps_all / gridDim.y);
   const int s_hi = (int)((int64_t)(blockIdx.y + 1) * steps_all / gridDim.y);
   const int steps = s_hi - s_lo;
-  // Steps of this wave: interleaved (wave, wave + kWaves, ...), or, for the
-  // SwiGLU GEMM, a contiguous block (the workgroup then streams whole weight
-  // rows a quarter at a time instead of 2 KiB of each of its 128 rows: gate|up
-  // at Llama-8B shape 49.1 -> 47.1 us at B=16 with cold weights; the other
-  // shapes measured 2-20 % slower that way).
-  constexpr bool kBlocked = kEpi == kSwiGLU;
-  const int per = steps / kWaves, rem = steps % kWaves;
-  const int first = kBlocked ? wave * per + min(wave, rem) : wave;
-  const int n_mine = kBlocked ? per + (wave < rem ? 1 : 0)
-                              : (steps > wave ? (steps - wave + kWaves - 1) / kWaves : 0);
-  const int stride = kBlocked ? 1 : kWaves;
+  // Steps of this wave: wave, wave + kWaves, ... (so the workgroup's waves
+  // read consecutive k blocks together; with tiled weights that is one
+  // contiguous 32 KiB run per column tile). Each wave's share, and so the
+  // order of the fp32 sums, is the same for both weight layouts.
+  const int first = wave;
+  const int n_mine = steps > wave ? (steps - wave + kWaves - 1) / kWaves : 0;
+  constexpr int stride = kWaves;
   const int last = min(first + (max(n_mine, 1) - 1) * stride, steps - 1);
   v8 wv[kDepth][kW][4], xv[kDepth][kTiles][4];
   auto load = [&](int slot, int j) {
@@ -122,7 +133,8 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
 #pragma unroll
     for (int q = 0; q < kW; ++q)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) wv[slot][q][c] = pdk::ld16(wp[q] + k + 32 * c);
+      for (int c = 0; c < 4; ++c)
+        wv[slot][q][c] = pdk::ld16(wp[q] + (kTiled ? (int64_t)k * 16 + 512 * c : k + 32 * c));
 #pragma unroll
     for (int t = 0; t < kTiles; ++t)
 #pragma unroll
@@ -210,17 +222,20 @@ __global__ void argmax_finish_kernel(uint64_t* keys, int B, int32_t* tokens) {
   keys[b] = 0;
 }
 
-template <int kCols, int kEpi>
+template <int kCols, int kEpi, bool kTiled>
 int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
                 uint16_t* y, uint64_t* keys, hipStream_t st, float* part = nullptr,
                 int splits = 1) {
   const dim3 grid((N + 16 * kCols - 1) / (16 * kCols), splits), block(kWaves * 64);
+#define PDK_WGEMM(T) \
+  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part)
   switch ((B + 15) / 16) {
-    case 1: hipLaunchKernelGGL((wgemm_kernel<1, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part); break;
-    case 2: hipLaunchKernelGGL((wgemm_kernel<2, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part); break;
-    case 3: hipLaunchKernelGGL((wgemm_kernel<3, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part); break;
-    default: hipLaunchKernelGGL((wgemm_kernel<4, kCols, kEpi>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part); break;
+    case 1: PDK_WGEMM(1); break;
+    case 2: PDK_WGEMM(2); break;
+    case 3: PDK_WGEMM(3); break;
+    default: PDK_WGEMM(4); break;
   }
+#undef PDK_WGEMM
   return pdk::check_launch("wgemm_kernel");
 }
 
@@ -229,15 +244,32 @@ int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const
 // itself at B = 16 with one tile) but leave fewer workgroups. Measured at the
 // Llama-3.1-8B shapes: gate|up (M = 14336) and the lm_head at B > 8 run best
 // with 4 tiles; N = 4096 and 6144 need every workgroup one tile gives.
-template <int kEpi>
+template <int kEpi, bool kTiled>
 int launch(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
            uint16_t* y, uint64_t* keys, hipStream_t st) {
   const int64_t wide = (N + 63) / 64;                // workgroups with 4 tiles
   // Wide SwiGLU tiles hold 8 weight tiles per step in registers: beyond 32
   // streams they would spill, and one tile is used instead.
   const bool four = kEpi == kSwiGLU ? (wide >= 192 && B <= 32) : (B > 8 && wide >= 1024);
-  if (four) return launch_cols<4, kEpi>(x, w, B, K, N, r, y, keys, st);
-  return launch_cols<1, kEpi>(x, w, B, K, N, r, y, keys, st);
+  if (four) return launch_cols<4, kEpi, kTiled>(x, w, B, K, N, r, y, keys, st);
+  return launch_cols<1, kEpi, kTiled>(x, w, B, K, N, r, y, keys, st);
+}
+
+// Tiled copy of W [N][K]: one thread per 16-byte group of the copy.
+__global__ void weight_tile_kernel(const uint16_t* __restrict__ w, int N, int K,
+                                   uint16_t* __restrict__ wt, int64_t groups) {
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gi >= groups) return;
+  const int lane = (int)(gi & 63);                   // (kg, col) = (lane >> 4, lane & 15)
+  const int c = (int)((gi >> 6) & 3);
+  const int64_t blk = gi >> 8;                       // step block: tile * (K / 128) + step
+  const int steps = K / kStepK;
+  const int64_t t = blk / steps;
+  const int s = (int)(blk - t * steps);
+  const int64_t row = t * 16 + (lane & 15);
+  v8 v = pdk::zero8();
+  if (row < N) v = pdk::ld16(w + row * K + s * kStepK + 32 * c + 8 * (lane >> 4));
+  pdk::st16(wt + gi * 8, v);
 }
 
 int check_shape(const void* x, const void* w, const void* y, int B, int K, int N) {
@@ -250,40 +282,45 @@ int check_shape(const void* x, const void* w, const void* y, int B, int K, int N
   return PDK_OK;
 }
 
-}  // namespace
 
-extern "C" int pdk_linear(const uint16_t* x, const uint16_t* w, int B, int K, int N,
-                          const uint16_t* residual, uint16_t* y, uintptr_t stream) {
+template <bool kTiled>
+int linear(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* residual,
+           uint16_t* y, uintptr_t stream) {
   pdk::clear_error();
   if (int rc = check_shape(x, w, y, B, K, N)) return rc;
   if (residual)
-    return launch<kResidual>(x, w, B, K, N, residual, y, nullptr, pdk::as_stream(stream));
-  return launch<kPlain>(x, w, B, K, N, nullptr, y, nullptr, pdk::as_stream(stream));
+    return launch<kResidual, kTiled>(x, w, B, K, N, residual, y, nullptr, pdk::as_stream(stream));
+  return launch<kPlain, kTiled>(x, w, B, K, N, nullptr, y, nullptr, pdk::as_stream(stream));
 }
 
-extern "C" int pdk_linear_swiglu(const uint16_t* x, const uint16_t* w_gate_up, int B, int K, int M,
-                                 uint16_t* y, uintptr_t stream) {
+template <bool kTiled>
+int linear_swiglu(const uint16_t* x, const uint16_t* w_gate_up, int B, int K, int M, uint16_t* y,
+                  uintptr_t stream) {
   pdk::clear_error();
   if (int rc = check_shape(x, w_gate_up, y, B, K, M)) return rc;
-  return launch<kSwiGLU>(x, w_gate_up, B, K, M, nullptr, y, nullptr, pdk::as_stream(stream));
+  // The up rows start at tile M / 16 of the tiled copy of [2M][K].
+  PDK_REQUIRE(!kTiled || M % 16 == 0, "tiled gate|up weights need M %% 16 == 0 (got %d)", M);
+  return launch<kSwiGLU, kTiled>(x, w_gate_up, B, K, M, nullptr, y, nullptr,
+                                 pdk::as_stream(stream));
 }
 
-extern "C" int pdk_linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N,
-                                 uint16_t* logits, uint64_t* keys, int32_t* tokens,
-                                 uintptr_t stream) {
+template <bool kTiled>
+int linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N, uint16_t* logits,
+                  uint64_t* keys, int32_t* tokens, uintptr_t stream) {
   pdk::clear_error();
   // y may be null here: check_shape only needs a non-null stand-in.
   if (int rc = check_shape(x, w, keys, B, K, N)) return rc;
   PDK_REQUIRE(tokens, "null pointer argument");
   PDK_REQUIRE(((uintptr_t)keys & 7u) == 0, "keys must be 8-byte aligned");
   hipStream_t st = pdk::as_stream(stream);
-  if (int rc = launch<kArgmax>(x, w, B, K, N, nullptr, logits, keys, st)) return rc;
+  if (int rc = launch<kArgmax, kTiled>(x, w, B, K, N, nullptr, logits, keys, st)) return rc;
   hipLaunchKernelGGL(argmax_finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, keys, B, tokens);
   return pdk::check_launch("argmax_finish_kernel");
 }
 
-extern "C" int pdk_linear_splitk(const uint16_t* x, const uint16_t* w, int B, int K, int N,
-                                 int splits, float* partials, uintptr_t stream) {
+template <bool kTiled>
+int linear_splitk(const uint16_t* x, const uint16_t* w, int B, int K, int N, int splits,
+                  float* partials, uintptr_t stream) {
   pdk::clear_error();
   if (int rc = check_shape(x, w, partials, B, K, N)) return rc;
   PDK_REQUIRE(splits >= 1 && splits <= 16 && splits <= K / kStepK,
@@ -292,7 +329,72 @@ extern "C" int pdk_linear_splitk(const uint16_t* x, const uint16_t* w, int B, in
   // workgroup count.
   hipStream_t st = pdk::as_stream(stream);
   if (N >= 1024)
-    return launch_cols<4, kPartial>(x, w, B, K, N, nullptr, nullptr, nullptr, st, partials,
-                                    splits);
-  return launch_cols<1, kPartial>(x, w, B, K, N, nullptr, nullptr, nullptr, st, partials, splits);
+    return launch_cols<4, kPartial, kTiled>(x, w, B, K, N, nullptr, nullptr, nullptr, st,
+                                            partials, splits);
+  return launch_cols<1, kPartial, kTiled>(x, w, B, K, N, nullptr, nullptr, nullptr, st, partials,
+                                          splits);
+}
+
+}  // namespace
+
+extern "C" int pdk_linear(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                          const uint16_t* residual, uint16_t* y, uintptr_t stream) {
+  return linear<false>(x, w, B, K, N, residual, y, stream);
+}
+
+extern "C" int pdk_linear_swiglu(const uint16_t* x, const uint16_t* w_gate_up, int B, int K, int M,
+                                 uint16_t* y, uintptr_t stream) {
+  return linear_swiglu<false>(x, w_gate_up, B, K, M, y, stream);
+}
+
+extern "C" int pdk_linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                                 uint16_t* logits, uint64_t* keys, int32_t* tokens,
+                                 uintptr_t stream) {
+  return linear_argmax<false>(x, w, B, K, N, logits, keys, tokens, stream);
+}
+
+extern "C" int pdk_linear_splitk(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                                 int splits, float* partials, uintptr_t stream) {
+  return linear_splitk<false>(x, w, B, K, N, splits, partials, stream);
+}
+
+extern "C" int64_t pdk_weight_tiled_elems(int N, int K) {
+  if (N < 1 || K < kStepK || K % kStepK != 0) return 0;
+  return (int64_t)((N + 15) / 16) * 16 * K;
+}
+
+extern "C" int pdk_weight_tile(const uint16_t* w, int N, int K, uint16_t* wt, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(w && wt, "null pointer argument");
+  PDK_REQUIRE(N >= 1, "N must be positive (got %d)", N);
+  PDK_REQUIRE(K >= kStepK && K % kStepK == 0, "K must be a positive multiple of %d (got %d)",
+              kStepK, K);
+  PDK_REQUIRE(pdk::aligned16(w) && pdk::aligned16(wt), "w and wt must be 16-byte aligned");
+  const int64_t groups = pdk_weight_tiled_elems(N, K) / 8;
+  const int64_t blocks = (groups + 255) / 256;
+  PDK_REQUIRE(blocks < (1ll << 31), "weight too large");
+  hipLaunchKernelGGL(weight_tile_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     pdk::as_stream(stream), w, N, K, wt, groups);
+  return pdk::check_launch("weight_tile_kernel");
+}
+
+extern "C" int pdk_linear_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                                const uint16_t* residual, uint16_t* y, uintptr_t stream) {
+  return linear<true>(x, wt, B, K, N, residual, y, stream);
+}
+
+extern "C" int pdk_linear_swiglu_tiled(const uint16_t* x, const uint16_t* wt_gate_up, int B,
+                                       int K, int M, uint16_t* y, uintptr_t stream) {
+  return linear_swiglu<true>(x, wt_gate_up, B, K, M, y, stream);
+}
+
+extern "C" int pdk_linear_argmax_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                                       uint16_t* logits, uint64_t* keys, int32_t* tokens,
+                                       uintptr_t stream) {
+  return linear_argmax<true>(x, wt, B, K, N, logits, keys, tokens, stream);
+}
+
+extern "C" int pdk_linear_splitk_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                                       int splits, float* partials, uintptr_t stream) {
+  return linear_splitk<true>(x, wt, B, K, N, splits, partials, stream);
 }

@@ -17,7 +17,10 @@ Replaces the reference's BatchDecodeEngine.step / step_logits
 then the final norm (which adds the last layer's partials) and the lm_head
 GEMM with the first-maximum argmax in its epilogue (pdk_linear_argmax).
 Weights are [out, in] contiguous (torch Linear layout) with q|k|v and gate|up
-stacked, so each projection is one pass over its weights. Activations are bf16 at every tensor boundary, as the
+stacked, so each projection is one pass over its weights. By default the
+decoder streams tiled copies of them (pdk_weight_tile, made once at
+construction: each 16-row x 128-column block contiguous in the order the GEMM
+reads it) through the *_tiled entry points, with bit-identical results. Activations are bf16 at every tensor boundary, as the
 reference's are; the kernels accumulate in fp32 and round once.
 """
 import contextlib
@@ -27,6 +30,7 @@ import torch
 
 from .. import _lib
 from ..kernels import attention as _attn
+from ..kernels.decode_step import tile_weight
 from ..kernels.handoff import stream_handle
 
 BF16 = torch.bfloat16
@@ -111,7 +115,10 @@ class LlamaWeights:
 class LlamaDecoder:
     """B-stream decode steps over a PagedKVCache (same n_layers, Hkv, head_dim)."""
 
-    def __init__(self, weights, cache, max_batch):
+    def __init__(self, weights, cache, max_batch, tiled=True):
+        """``tiled``: stream tiled copies of the projection and lm_head weights
+        (the copies take as much device memory as those weights again; the
+        originals are left untouched)."""
         cfg = self.cfg = weights.cfg
         if (cache.n_layers, cache.n_kv_heads, cache.head_dim) != (cfg.n_layers, cfg.n_kv_heads,
                                                                   cfg.head_dim):
@@ -146,9 +153,19 @@ class LlamaDecoder:
         w = weights
         if max_batch > 64:
             raise ValueError("the decode GEMMs take at most 64 streams")
-        self._layers = [tuple(t.data_ptr() for t in (w.norm1[i], w.wqkv[i], w.wo[i], w.norm2[i],
-                                                     w.wgu[i], w.wd[i], cache.k[i], cache.v[i]))
-                        for i in range(cfg.n_layers)]
+        # Tiled copies need M % 16 == 0 for gate|up and K % 128 == 0 (as the
+        # GEMMs themselves do).
+        self.tiled = bool(tiled) and cfg.inter % 16 == 0
+        prep = tile_weight if self.tiled else (lambda t: t)
+        self._wt = [tuple(prep(t) for t in (w.wqkv[i], w.wo[i], w.wgu[i], w.wd[i]))
+                    for i in range(cfg.n_layers)]
+        self._lm_head = prep(w.lm_head)
+        self._gemm = {n: n + "_tiled" if self.tiled else n for n in
+                      ("pdk_linear", "pdk_linear_splitk", "pdk_linear_swiglu",
+                       "pdk_linear_argmax")}
+        self._layers = [tuple(t.data_ptr() for t in (w.norm1[i], wt[0], wt[1], w.norm2[i], wt[2],
+                                                     wt[3], cache.k[i], cache.v[i]))
+                        for i, wt in enumerate(self._wt)]
 
     def reserve(self, max_ctx):
         """Allocate the attention workspace for max_batch streams at ``max_ctx``
@@ -195,6 +212,9 @@ class LlamaDecoder:
         xp, hp = x.data_ptr(), self.h.data_ptr()
         aop, actp, inv = self.ao.data_ptr(), self.act.data_ptr(), self.inv.data_ptr()
         call = _lib.call
+        g = self._gemm
+        lin, lin_sk, lin_sw, lin_am = (g["pdk_linear"], g["pdk_linear_splitk"],
+                                       g["pdk_linear_swiglu"], g["pdk_linear_argmax"])
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
             torch.index_select(w.embed, 0, tokens.long(), out=x)
             partp, sp = self.part.data_ptr(), self.down_splits
@@ -204,15 +224,15 @@ class LlamaDecoder:
                     call("pdk_rmsnorm_partials", xp, partp, sp, n1, B, H, eps, hp, st)
                 else:
                     call("pdk_rmsnorm", xp, None, n1, B, H, eps, hp, st)
-                call("pdk_linear_splitk", hp, wqkv, B, H, QKV, qs, pqp, st)
+                call(lin_sk, hp, wqkv, B, H, QKV, qs, pqp, st)
                 call("pdk_decode_attn_rope", pqp, qs, inv, ck, cv, nb, tp, mb, cp, int(max_ctx),
                      B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, st)
-                call("pdk_linear", aop, wo, B, NH * HD, H, xp, xp, st)
+                call(lin, aop, wo, B, NH * HD, H, xp, xp, st)
                 call("pdk_rmsnorm", xp, None, n2, B, H, eps, hp, st)
-                call("pdk_linear_swiglu", hp, wgu, B, H, M, actp, st)
-                call("pdk_linear_splitk", actp, wd, B, M, H, sp, partp, st)
+                call(lin_sw, hp, wgu, B, H, M, actp, st)
+                call(lin_sk, actp, wd, B, M, H, sp, partp, st)
             call("pdk_rmsnorm_partials", xp, partp, sp, w.norm_f.data_ptr(), B, H, eps, hp, st)
-            call("pdk_linear_argmax", hp, w.lm_head.data_ptr(), B, H, cfg.vocab,
+            call(lin_am, hp, self._lm_head.data_ptr(), B, H, cfg.vocab,
                  self.logits.data_ptr(), self.keys.data_ptr(), self.tokens.data_ptr(), st)
         return self.tokens[:B]
 

@@ -109,16 +109,58 @@ def swiglu(gate_up, out=None, stream=None):
     return out
 
 
+class TiledWeight:
+    """A weight [N, K] in the tiled layout of pdk_weight_tile: every 16-row x
+    128-column block contiguous, in the order the GEMM kernels read it, so the
+    weight stream is read linearly. ``data`` is the flat bf16 device tensor;
+    ``shape`` is the (N, K) of the weight it was made from. The GEMM wrappers
+    below take it wherever they take a [N, K] weight, with identical results."""
+
+    __slots__ = ("data", "shape")
+
+    def __init__(self, data, N, K):
+        self.data = data
+        self.shape = (int(N), int(K))
+
+    def data_ptr(self):
+        return self.data.data_ptr()
+
+
+def tile_weight(w, stream=None):
+    """Tiled copy of a contiguous bf16 weight w [N, K] (K % 128 == 0)."""
+    _need(w, "w")
+    if w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("w must be a contiguous [N, K] tensor")
+    N, K = w.shape
+    n = int(_lib.lib().pdk_weight_tiled_elems(N, K))
+    if n == 0:
+        raise ValueError(f"cannot tile a [{N}, {K}] weight: K must be a positive multiple of 128")
+    data = torch.empty(n, dtype=w.dtype, device=w.device)
+    _lib.call("pdk_weight_tile", w.data_ptr(), N, K, data.data_ptr(), stream_handle(stream))
+    return TiledWeight(data, N, K)
+
+
 def _check_linear(x, w, rows_per_col=1):
     _need(x, "x")
-    _need(w, "w")
-    if x.dim() != 2 or not x.is_contiguous() or w.dim() != 2 or not w.is_contiguous():
-        raise ValueError("x [B, K] and w [N, K] must be contiguous 2-D tensors")
-    if x.shape[1] != w.shape[1]:
-        raise ValueError(f"x has K={x.shape[1]}, w has K={w.shape[1]}")
-    if w.shape[0] % rows_per_col:
+    if isinstance(w, TiledWeight):
+        _need(w.data, "w")
+        N, K = w.shape
+    else:
+        _need(w, "w")
+        if w.dim() != 2 or not w.is_contiguous():
+            raise ValueError("w must be a contiguous [N, K] tensor or a TiledWeight")
+        N, K = w.shape
+    if x.dim() != 2 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous [B, K] tensor")
+    if x.shape[1] != K:
+        raise ValueError(f"x has K={x.shape[1]}, w has K={K}")
+    if N % rows_per_col:
         raise ValueError("w must hold 2M rows (gate rows, then up rows)")
-    return x.shape[0], x.shape[1], w.shape[0] // rows_per_col
+    return x.shape[0], K, N // rows_per_col
+
+
+def _entry(name, w):
+    return name + "_tiled" if isinstance(w, TiledWeight) else name
 
 
 def linear(x, w, residual=None, out=None, stream=None):
@@ -133,7 +175,7 @@ def linear(x, w, residual=None, out=None, stream=None):
         out = torch.empty((B, N), dtype=x.dtype, device=x.device)
     elif tuple(out.shape) != (B, N) or not out.is_contiguous():
         raise ValueError(f"out must be contiguous [{B}, {N}]")
-    _lib.call("pdk_linear", x.data_ptr(), w.data_ptr(), B, K, N,
+    _lib.call(_entry("pdk_linear", w), x.data_ptr(), w.data_ptr(), B, K, N,
               residual.data_ptr() if residual is not None else None, out.data_ptr(),
               stream_handle(stream))
     return out
@@ -146,7 +188,8 @@ def linear_swiglu(x, w_gate_up, out=None, stream=None):
         out = torch.empty((B, M), dtype=x.dtype, device=x.device)
     elif tuple(out.shape) != (B, M) or not out.is_contiguous():
         raise ValueError(f"out must be contiguous [{B}, {M}]")
-    _lib.call("pdk_linear_swiglu", x.data_ptr(), w_gate_up.data_ptr(), B, K, M, out.data_ptr(),
+    _lib.call(_entry("pdk_linear_swiglu", w_gate_up), x.data_ptr(), w_gate_up.data_ptr(), B, K, M,
+              out.data_ptr(),
               stream_handle(stream))
     return out
 
@@ -164,7 +207,7 @@ def linear_argmax(x, w, keys, tokens=None, logits=None, stream=None):
         tokens = torch.empty(B, dtype=torch.int32, device=x.device)
     if logits is not None and (tuple(logits.shape) != (B, N) or not logits.is_contiguous()):
         raise ValueError(f"logits must be contiguous [{B}, {N}]")
-    _lib.call("pdk_linear_argmax", x.data_ptr(), w.data_ptr(), B, K, N,
+    _lib.call(_entry("pdk_linear_argmax", w), x.data_ptr(), w.data_ptr(), B, K, N,
               logits.data_ptr() if logits is not None else None, keys.data_ptr(),
               tokens.data_ptr(), stream_handle(stream))
     return tokens
@@ -179,7 +222,7 @@ def linear_splitk(x, w, splits, partials=None, stream=None):
     elif partials.dtype != torch.float32 or partials.numel() < splits * B * N or \
             not partials.is_contiguous():
         raise ValueError(f"partials must be contiguous float32 holding {splits}x{B}x{N}")
-    _lib.call("pdk_linear_splitk", x.data_ptr(), w.data_ptr(), B, K, N, int(splits),
+    _lib.call(_entry("pdk_linear_splitk", w), x.data_ptr(), w.data_ptr(), B, K, N, int(splits),
               partials.data_ptr(), stream_handle(stream))
     return partials
 

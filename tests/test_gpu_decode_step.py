@@ -303,6 +303,65 @@ def test_linear_argmax(cuda, B, K, N):
             xd = xd.flip(0).contiguous()
 
 
+def _tiled_layout(w):
+    """The documented tiled layout of a [N, K] weight, by reshapes: block (t, s)
+    element ((c*4 + kg)*16 + col)*8 + e = w[16t + col][128s + 32c + 8kg + e]."""
+    N, K = w.shape
+    nt = (N + 15) // 16
+    pad = np.zeros((nt * 16, K), w.dtype)
+    pad[:N] = w
+    v = pad.reshape(nt, 16, K // 128, 4, 4, 8)            # t, col, s, c, kg, e
+    return np.ascontiguousarray(v.transpose(0, 2, 3, 4, 1, 5)).reshape(-1)
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (1000, 256), (7, 128), (6144, 4096), (128256, 128)])
+def test_weight_tile_layout(cuda, N, K):
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(N + K)
+    w = rand_bf16(rng, (N, K))
+    print(f"weight_tile N={N} K={K}", flush=True)
+    t = K_.tile_weight(to_dev(w))
+    torch.cuda.synchronize()
+    assert t.shape == (N, K)
+    np.testing.assert_array_equal(to_host(t.data), _tiled_layout(w))
+
+
+@pytest.mark.parametrize("B,K,N", [(1, 128, 16), (4, 4096, 6144), (16, 14336, 4096),
+                                   (16, 4096, 4096), (33, 1024, 2048), (5, 256, 1000),
+                                   (64, 256, 32), (2, 128, 7)])
+def test_tiled_gemms_equal_untiled(cuda, B, K, N):
+    """Every GEMM entry point gives bit-identical results on the tiled copy of
+    its weight: the same products, summed in the same order."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B * 31 + K + N)
+    x, w, r = rand_bf16(rng, (B, K)), rand_bf16(rng, (N, K), 0.05), rand_bf16(rng, (B, N), 4.0)
+    xd, wd, rd = to_dev(x), to_dev(w), to_dev(r)
+    wt = K_.tile_weight(wd)
+    print(f"tiled gemms B={B} K={K} N={N}", flush=True)
+    pairs = [(K_.linear(xd, wd), K_.linear(xd, wt)),
+             (K_.linear(xd, wd, residual=rd), K_.linear(xd, wt, residual=rd))]
+    for splits in sorted({1, min(4, K // 128)}):
+        pairs.append((K_.linear_splitk(xd, wd, splits), K_.linear_splitk(xd, wt, splits)))
+    keys = torch.zeros(B, dtype=torch.int64, device=cuda)
+    pairs.append((K_.linear_argmax(xd, wd, keys), K_.linear_argmax(xd, wt, keys)))
+    if N % 32 == 0:                                   # gate|up: 2M rows with M % 16 == 0
+        pairs.append((K_.linear_swiglu(xd, wd), K_.linear_swiglu(xd, wt)))
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(pairs):
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b), i
+
+
+def test_tiled_swiglu_needs_m_multiple_of_16(cuda):
+    from rngd_pd_amd import kernels as K_
+    from rngd_pd_amd._lib import PdkError
+    rng = np.random.default_rng(5)
+    x, w = rand_bf16(rng, (2, 128)), rand_bf16(rng, (2 * 24, 128))
+    wt = K_.tile_weight(to_dev(w))
+    with pytest.raises(PdkError, match="M % 16"):
+        K_.linear_swiglu(to_dev(x), wt)
+
+
 # ---- whole steps -------------------------------------------------------------
 
 class _OCfg:
