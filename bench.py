@@ -437,9 +437,11 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
 
 def bench_step(args, torch, dev, out, batches=(4, 16), ctx=512):
     """Full Llama-3.1-8B decode step (32 layers, random-init bf16 weights, no
-    checkpoint): embed -> per layer RMSNorm, fused QKV GEMM, RoPE + cache write,
-    paged decode attention, o GEMM + residual, RMSNorm, gate|up GEMM, SwiGLU,
-    down GEMM + residual -> final norm, lm_head GEMM, greedy argmax. Every
+    checkpoint): embed -> per layer RMSNorm, q|k|v GEMM split over K, RoPE +
+    new-token cache write + paged decode attention in one kernel, o GEMM +
+    residual, RMSNorm, gate|up GEMM with SwiGLU, down GEMM split over K (its
+    residual add in the next norm) -> final norm, lm_head GEMM with the greedy
+    argmax; the GEMMs read the decoder's tiled copies of the weights. Every
     stream at context ctx (its new token at slot ctx-1; the reference's S=512
     step attends over the whole S). Bytes per step = every weight read once
     (16.06 GB; the embedding contributes B rows) + the K/V of all layers."""
@@ -502,6 +504,7 @@ def bench_step(args, torch, dev, out, batches=(4, 16), ctx=512):
             "hbm_frac": round(step_bytes / (dev_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "reference_ms_per_step": published[B],
             "speedup_vs_reference": round(published[B] / ms, 2),
+            "weight_layout": "tiled" if dec.tiled else "out_in",
         }
         log(f"step B={B} ctx={ctx}: graph {ms:.3f} ms ({B / graphed:.0f} tok/s, "
             f"{res[f'B{B}']['hbm_frac'] * 100:.1f}% of HBM), eager {eager * 1e3:.3f} ms; "
