@@ -602,12 +602,12 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 // Launch plan. One workgroup per (stream, KV head, split), up to 8
 // wavefronts of 64 tokens each in flight. The context is split across
 // workgroups until about 256 of them (one per CU) exist, in splits of at least
-// 128 tokens; once B*Hkv alone reaches 128 workgroups, only contexts of 1024
-// tokens or more are split, because below that the partial-result merge (an
-// extra launch) costs more than the CUs gained. Measured per layer on MI355X,
-// Hq=32, Hkv=8, cold cache: B=16 ctx 512 one split 10.5 us vs two 11.7 us;
-// B=16 ctx 2048 two splits 28.9 us vs one 32.3 us; B=4 ctx 512 four splits
-// 8.2 us vs eight 9.0 us.
+// min_split tokens, because a split costs the partial-result merge (an extra
+// launch): 1024 once B*Hkv alone reaches 128 workgroups, 512 from 32, 128
+// below. Measured per layer on MI355X, Hq=32, Hkv=8, ctx 512 (32-layer graph):
+// B=4 one split 7.7 us vs four 9.1 us, B=8 one 8.4 us vs two 10.6 us; cold
+// cache: B=16 one 10.5 us vs two 11.7 us, B=16 ctx 2048 two 28.9 us vs one
+// 32.3 us.
 struct Plan {
   int nsplit, split_tokens, waves;
 };
@@ -616,7 +616,7 @@ constexpr int kTargetWorkgroups = 256;
 
 Plan plan_for(int B, int Hkv, int max_ctx) {
   const int64_t pairs = (int64_t)B * Hkv;
-  const int min_split = pairs >= 128 ? 1024 : 128;
+  const int min_split = pairs >= 128 ? 1024 : pairs >= 32 ? 512 : 128;
   int64_t nsplit = (kTargetWorkgroups + pairs - 1) / pairs;
   nsplit = std::min<int64_t>(nsplit, (max_ctx + min_split - 1) / min_split);
   nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, kMaxSplits));
