@@ -160,6 +160,10 @@ class LlamaDecoder:
         self._wt = [tuple(prep(t) for t in (w.wqkv[i], w.wo[i], w.wgu[i], w.wd[i]))
                     for i in range(cfg.n_layers)]
         self._lm_head = prep(w.lm_head)
+        if self.tiled:
+            # The copies are written on the current stream; a step may run on
+            # another one, so they are complete before the constructor returns.
+            torch.cuda.current_stream(dev).synchronize()
         self._gemm = {n: n + "_tiled" if self.tiled else n for n in
                       ("pdk_linear", "pdk_linear_splitk", "pdk_linear_swiglu",
                        "pdk_linear_argmax")}
