@@ -329,7 +329,7 @@ def test_weight_tile_layout(cuda, N, K):
 @pytest.mark.parametrize("B,K,N", [(1, 128, 16), (4, 4096, 6144), (16, 14336, 4096),
                                    (16, 4096, 4096), (33, 1024, 2048), (5, 256, 1000),
                                    (64, 256, 32), (2, 128, 7), (4, 128, 70000),
-                                   (16, 256, 28672)])
+                                   (16, 256, 28672), (24, 256, 24576), (40, 128, 131072)])
 def test_tiled_gemms_equal_untiled(cuda, B, K, N):
     """Every GEMM entry point gives bit-identical results on the tiled copy of
     its weight: the same products, summed in the same order."""
