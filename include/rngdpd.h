@@ -364,6 +364,20 @@ int pdk_memcpy_d2d(void* dev_dst, const void* dev_src, size_t bytes,
  * calibrate HBM traffic counters against a known byte count. */
 int pdk_copy_kernel(void* dev_dst, const void* dev_src, size_t bytes,
                     uintptr_t stream);
+/* Streaming probes for the HBM ceilings the handoff kernels are compared with:
+ * kind PDK_STREAM_READ reads `bytes` of dev_src, PDK_STREAM_WRITE writes `key`
+ * to every word of dev_dst, PDK_STREAM_COPY copies dev_src to dev_dst; 16-byte
+ * vectors (bytes % 16 == 0), four in flight per lane over a grid of `blocks`
+ * 256-lane workgroups (0: one per 4 KiB, at most 8192). PDK_STREAM_NONTEMPORAL
+ * asks for streaming (non-temporal) accesses. A read folds what it loads and
+ * stores into dev_sink[0..255] only where a fold equals `key` (pick a key no
+ * fold is expected to take). No counterpart in the reference: measurement only. */
+#define PDK_STREAM_READ 0
+#define PDK_STREAM_WRITE 1
+#define PDK_STREAM_COPY 2
+#define PDK_STREAM_NONTEMPORAL 1
+int pdk_stream_probe(int kind, void* dev_dst, const void* dev_src, size_t bytes, int flags,
+                     int blocks, uint32_t key, uint32_t* dev_sink, uintptr_t stream);
 
 /* ---- layer-wise staging pipeline ---------------------------------------------
  * The reference hands each layer group to the writer while the next computes

@@ -26,6 +26,10 @@ PDK_EVENT_SYNC = 2
 PDK_COPY_D2H = 0
 PDK_COPY_H2D = 1
 PDK_COPY_D2D = 2
+PDK_STREAM_READ = 0
+PDK_STREAM_WRITE = 1
+PDK_STREAM_COPY = 2
+PDK_STREAM_NONTEMPORAL = 1
 
 
 class PdkError(RuntimeError):
@@ -102,6 +106,7 @@ SIGNATURES = {
     "pdk_memcpy_h2d": (_I, [_P, _P, _SZ, _U]),
     "pdk_memcpy_d2d": (_I, [_P, _P, _SZ, _U]),
     "pdk_copy_kernel": (_I, [_P, _P, _SZ, _U]),
+    "pdk_stream_probe": (_I, [_I, _P, _P, _SZ, _I, _I, ctypes.c_uint32, _P, _U]),
     "pdk_stream_create": (_I, [ctypes.POINTER(_U)]),
     "pdk_stream_destroy": (_I, [_U]),
     "pdk_stream_sync": (_I, [_U]),

@@ -135,6 +135,61 @@ __global__ __launch_bounds__(256) void copy_kernel(uint4* dst, const uint4* src,
     dst[i] = src[i];
 }
 
+// Streaming probes: a linear read, a linear write and a copy of 16-byte
+// vectors, four independent vectors in flight per lane (grid-stride), with
+// ordinary or non-temporal accesses. The read folds what it loads into an XOR
+// and stores a word only where a fold equals `key`, so its loads cannot be
+// dropped while in practice it writes nothing.
+typedef uint32_t su4 __attribute__((ext_vector_type(4)));
+
+template <bool kNT>
+__device__ __forceinline__ su4 probe_ld(const su4* p) {
+  if (kNT) return __builtin_nontemporal_load(p);
+  return *p;
+}
+
+template <bool kNT>
+__device__ __forceinline__ void probe_st(su4* p, su4 v) {
+  if (kNT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+template <int kKind, bool kNT>
+__global__ __launch_bounds__(256) void stream_probe_kernel(su4* dst, const su4* src, int64_t n,
+                                                           uint32_t key, uint32_t* sink) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  su4 acc = {0u, 0u, 0u, 0u};
+  const su4 fill = {key, key, key, key};
+  for (; i + 3 * stride < n; i += 4 * stride) {
+    if (kKind == PDK_STREAM_WRITE) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) probe_st<kNT>(dst + i + u * stride, fill);
+    } else {
+      su4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = probe_ld<kNT>(src + i + u * stride);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (kKind == PDK_STREAM_COPY) probe_st<kNT>(dst + i + u * stride, v[u]);
+        else acc ^= v[u];
+      }
+    }
+  }
+  for (; i < n; i += stride) {
+    if (kKind == PDK_STREAM_WRITE) probe_st<kNT>(dst + i, fill);
+    else if (kKind == PDK_STREAM_COPY) probe_st<kNT>(dst + i, probe_ld<kNT>(src + i));
+    else acc ^= probe_ld<kNT>(src + i);
+  }
+  if (kKind == PDK_STREAM_READ && (acc.x ^ acc.y ^ acc.z ^ acc.w) == key)
+    sink[blockIdx.x & 255] = key;
+}
+
+int64_t stream_blocks(int64_t n16) {
+  const int64_t blocks = (n16 + 255) / 256;
+  return blocks > 8192 ? 8192 : blocks;
+}
+
 }  // namespace
 
 extern "C" {
@@ -243,6 +298,35 @@ int pdk_copy_kernel(void* dev_dst, const void* dev_src, size_t bytes, uintptr_t 
   hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, pdk::as_stream(stream),
                      static_cast<uint4*>(dev_dst), static_cast<const uint4*>(dev_src), n);
   return pdk::check_launch("copy_kernel");
+}
+
+int pdk_stream_probe(int kind, void* dev_dst, const void* dev_src, size_t bytes, int flags,
+                     int blocks, uint32_t key, uint32_t* dev_sink, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(kind == PDK_STREAM_READ || kind == PDK_STREAM_WRITE || kind == PDK_STREAM_COPY,
+              "bad kind %d", kind);
+  PDK_REQUIRE((flags & ~PDK_STREAM_NONTEMPORAL) == 0, "unknown flags 0x%x", flags);
+  PDK_REQUIRE(blocks >= 0 && blocks <= (1 << 20), "blocks must be in [0, 2^20] (got %d)", blocks);
+  const bool reads = kind != PDK_STREAM_WRITE, writes = kind != PDK_STREAM_READ;
+  PDK_REQUIRE(!reads || (dev_src && pdk::aligned16(dev_src)), "src null or not 16-byte aligned");
+  PDK_REQUIRE(!writes || (dev_dst && pdk::aligned16(dev_dst)), "dst null or not 16-byte aligned");
+  PDK_REQUIRE(kind != PDK_STREAM_READ || dev_sink, "a read needs a 256-word sink");
+  PDK_REQUIRE(bytes % 16 == 0, "bytes must be a multiple of 16");
+  const int64_t n = (int64_t)(bytes / 16);
+  if (n == 0) return PDK_OK;
+  const dim3 grid((unsigned)(blocks ? blocks : stream_blocks(n)));
+  su4* d = static_cast<su4*>(dev_dst);
+  const su4* s = static_cast<const su4*>(dev_src);
+  hipStream_t st = pdk::as_stream(stream);
+  const bool nt = (flags & PDK_STREAM_NONTEMPORAL) != 0;
+#define PDK_PROBE(K)                                                                        \
+  if (nt) hipLaunchKernelGGL((stream_probe_kernel<K, true>), grid, dim3(256), 0, st, d, s, n, key, dev_sink); \
+  else hipLaunchKernelGGL((stream_probe_kernel<K, false>), grid, dim3(256), 0, st, d, s, n, key, dev_sink)
+  if (kind == PDK_STREAM_READ) PDK_PROBE(PDK_STREAM_READ);
+  else if (kind == PDK_STREAM_WRITE) PDK_PROBE(PDK_STREAM_WRITE);
+  else PDK_PROBE(PDK_STREAM_COPY);
+#undef PDK_PROBE
+  return pdk::check_launch("stream_probe_kernel");
 }
 
 int pdk_stream_create(uintptr_t* out) {

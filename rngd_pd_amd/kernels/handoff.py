@@ -212,3 +212,27 @@ def copy_kernel(dst, src, stream=None):
     """Plain 16-byte-vector device copy (traffic-counter calibration)."""
     n = src.numel() * src.element_size()
     _lib.call("pdk_copy_kernel", dst.data_ptr(), src.data_ptr(), n, stream_handle(stream))
+
+
+
+_SINKS = {}
+
+
+def stream_probe(kind, dst=None, src=None, nbytes=None, nontemporal=False, blocks=0,
+                 key=0x9E3779B9, stream=None):
+    """One streaming-probe launch: kind "read" (src), "write" (dst) or "copy".
+    A read stores nothing in practice (a word lands in a 1 KiB per-device sink
+    only where its fold equals ``key``)."""
+    kinds = {"read": _lib.PDK_STREAM_READ, "write": _lib.PDK_STREAM_WRITE,
+             "copy": _lib.PDK_STREAM_COPY}
+    t = src if src is not None else dst
+    dev = t.device
+    sink = _SINKS.get(dev)
+    if sink is None:
+        sink = _SINKS[dev] = torch.zeros(256, dtype=torch.int32, device=dev)
+    if nbytes is None:
+        nbytes = t.numel() * t.element_size()
+    _lib.call("pdk_stream_probe", kinds[kind], dst.data_ptr() if dst is not None else None,
+              src.data_ptr() if src is not None else None, int(nbytes),
+              _lib.PDK_STREAM_NONTEMPORAL if nontemporal else 0, int(blocks), key & 0xFFFFFFFF,
+              sink.data_ptr(), stream_handle(stream))
