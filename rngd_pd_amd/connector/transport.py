@@ -7,7 +7,7 @@
                     + push_parts / pull_into: the same files written from and
                     read into pinned staging buffers without intermediate copies
   FencedTransport   a tier-to-tier rm-core transport behind push/pull        (:238-289)
-  select_transport  by name: $AIRM_KV_TRANSPORT, default "shm"; no fallback  (:330-350)
+  select_transport  by name: $AIRM_KV_TRANSPORT, default "shm"; no fallback  (:292-350)
 
   tcp               the cross-node relay transport, native (connector/tcp.py)
   ipc               same-GPU frames through hipIpc handles (connector/ipc.py)
@@ -77,6 +77,10 @@ class InProcTransport(Transport):
             if time.time() - t0 > timeout:
                 raise TimeoutError(f"pull timeout: {key}")
             time.sleep(0.001)
+
+    def discard(self, key):
+        with self._lock:
+            self._store.pop(key, None)
 
     def close(self):
         self._store.clear()
@@ -163,6 +167,32 @@ class ShmTransport(Transport):
             raise IOError(f"{key}: short read ({got} of {size} bytes)")
         return size
 
+    def discard(self, key):
+        """Remove ``key``'s file if it is there (a consumer is done with it)."""
+        try:
+            os.unlink(self._path(key))
+        except FileNotFoundError:
+            pass
+
+    def discard_request(self, req_id):
+        """Remove every file of request ``req_id`` ("<req_id>__..."): the consumer's
+        purge once a request's KV is loaded (serving/cluster.py:461-466).
+        Returns the number of files removed."""
+        prefix = req_id.replace("/", "__") + "__"
+        n = 0
+        try:
+            names = os.listdir(self.root)
+        except FileNotFoundError:
+            return 0
+        for f in names:
+            if f.startswith(prefix):
+                try:
+                    os.unlink(os.path.join(self.root, f))
+                    n += 1
+                except FileNotFoundError:
+                    pass
+        return n
+
     def close(self):
         pass                     # files persist for the peer; the consumer removes them
 
@@ -182,12 +212,18 @@ class NixlTransport(Transport):
 
 
 class FencedTransport(Transport):
-    """The connector's key -> bytes contract over an rm-core tier-to-tier transport.
+    """The connector's key -> bytes contract over an rm-core tier-to-tier
+    transport (one that moves KV between memory tiers itself and knows nothing
+    of keys). push() plans and submits one transfer per key; pull() blocks
+    until that key has been pushed, then on its transfer's completion fence,
+    and only then returns the bytes. A failed fence raises TransportError, a
+    second push of a key that was not pulled yet raises ValueError. Handles are
+    process-local, so both ends live in one process (connector/transport.py:238-289).
 
-    push() plans and submits one transfer per key; pull() waits on that transfer's
-    fence and only then returns the bytes. A failed fence raises TransportError,
-    a key pushed twice before its pull raises ValueError. Handles are process-local.
-    """
+    Pushes and pulls meet at a condition variable: a pull sleeps until the
+    key's push has submitted (or the timeout passes) instead of polling."""
+
+    _SUBMITTING = object()               # a push holds the key while it submits
 
     def __init__(self, impl, src=None, dst=None):
         from ..rm_compat import KVLayout, MemoryTier
@@ -195,103 +231,141 @@ class FencedTransport(Transport):
         self.name = impl.name
         self.src = src or MemoryTier("prefill", "host-dram", 1 << 40)
         self.dst = dst or MemoryTier("decode", "host-dram", 1 << 40)
+        # One "token" per 2 bytes (1 layer x 1 head x 1 dim of int8 K and V),
+        # so a plan of ceil(n / 2) tokens covers an n-byte blob.
         self._layout = KVLayout(num_layers=1, num_kv_heads=1, head_dim=1, dtype="int8")
-        self._pending = {}
-        self._lock = threading.Lock()
+        self._cv = threading.Condition()
+        self._fences = {}                # key -> (handle, buf), or _SUBMITTING
 
     def push(self, key, buf):
-        n = len(buf)
-        plan = self.impl.plan(key, self.src, self.dst, self._layout, self._layout,
-                              (0, max(1, (n + 1) // 2)))
-        with self._lock:
-            if key in self._pending:
-                raise ValueError(f"{self.name}: {key} pushed twice before it was pulled")
-            self._pending[key] = None
-        handle = self.impl.submit(plan)
-        with self._lock:
-            self._pending[key] = (handle, buf)
+        tokens = (0, max(1, (len(buf) + 1) // 2))
+        plan = self.impl.plan(key, self.src, self.dst, self._layout, self._layout, tokens)
+        with self._cv:
+            if key in self._fences:
+                raise ValueError(f"{self.name}: key {key!r} is still waiting for its pull")
+            self._fences[key] = self._SUBMITTING
+        try:
+            handle = self.impl.submit(plan)
+        except BaseException:
+            with self._cv:
+                del self._fences[key]
+            raise
+        with self._cv:
+            self._fences[key] = (handle, buf)
+            self._cv.notify_all()
 
     def pull(self, key, timeout=5.0):
         from ..rm_compat import TransportError
-        t0 = time.time()
-        while True:
-            with self._lock:
-                entry = self._pending.get(key)
-            if entry is not None:
-                break
-            if time.time() - t0 > timeout:
+        deadline = time.monotonic() + timeout
+        with self._cv:
+            if not self._cv.wait_for(lambda: isinstance(self._fences.get(key), tuple), timeout):
                 raise TimeoutError(f"pull timeout: {key}")
-            time.sleep(0.001)
-        handle, buf = entry
+            handle, buf = self._fences[key]
         try:
-            res = self.impl.wait(handle, timeout_s=max(0.0, timeout - (time.time() - t0)))
+            res = self.impl.wait(handle, timeout_s=max(0.0, deadline - time.monotonic()))
         finally:
-            with self._lock:
-                self._pending.pop(key, None)
+            with self._cv:
+                self._fences.pop(key, None)      # a handle is waited at most once
         if not res.ok:
-            raise TransportError(f"{self.name}: transfer {key} failed: {res.error}")
+            raise TransportError(f"{self.name}: the transfer of {key!r} did not complete: "
+                                 f"{res.error}")
         return buf
 
     def close(self):
-        with _LOCK:
-            for k in [k for k, v in _FENCED.items() if v is self]:
-                del _FENCED[k]
+        _SELECTOR.forget(self)
         self.impl.close()
 
 
-# Our own adapters, used when the registry has no entry point of that name.
-_OWN = {"shm": "rngd_pd_amd.airm:ShmTransport",
-        "tcp": "rngd_pd_amd.airm:TcpTransport",            # native relay (librngdpd_net.so)
-        "ipc": "rngd_pd_amd.connector.ipc:IpcTransport"}   # same-GPU frames in HBM
-_NOT_HERE = ("nixl-ucx", "nixl")
-_CLASSES = {}          # name -> implementation class, resolved once per process
-_FENCED = {}           # name -> the process's one FencedTransport
-_SHARED = {}           # name -> the process's one instance of a connection-holding transport
-_LOCK = threading.Lock()
+class _Selector:
+    """Transport names -> implementations, resolved once per process.
+
+    Resolution: rm-core's ``airm.kv_transports`` registry when rm-core is
+    installed, then this package's own table; without rm-core, only the own
+    table. Anything else is a KeyError -- there is no fallback path. A
+    tier-to-tier implementation is wrapped in one FencedTransport per process
+    (both ends must share its handles); an implementation that declares
+    ``shared`` (it holds connections) is one instance per process; every other
+    is made anew per call (connector/transport.py:292-350)."""
+
+    OWN = {"shm": "rngd_pd_amd.airm:ShmTransport",
+           "tcp": "rngd_pd_amd.airm:TcpTransport",              # native relay client
+           "ipc": "rngd_pd_amd.connector.ipc:IpcTransport"}     # same-GPU frames in HBM
+    ABSENT = ("nixl", "nixl-ucx")       # vendor P2P paths this package does not provide
+
+    def __init__(self):
+        self._lock = threading.RLock()
+        self._factories = {}             # name -> class
+        self._held = {}                  # name -> the instance kept for the process
+
+    def reset(self):
+        """Forget every resolution and held instance (tests)."""
+        with self._lock:
+            self._factories.clear()
+            self._held.clear()
+
+    def held(self):
+        with self._lock:
+            return dict(self._held)
+
+    def forget(self, instance):
+        with self._lock:
+            for name in [n for n, t in self._held.items() if t is instance]:
+                del self._held[name]
+
+    def _construct(self, name, kw):
+        cls = self._factories.get(name)
+        if cls is not None:
+            return cls(**kw)
+        from .. import rm_compat
+        impl = None
+        if rm_compat.registry is not None:
+            try:
+                impl = rm_compat.registry.load("airm.kv_transports", name, **kw)
+            except KeyError:
+                impl = None
+        if impl is None:
+            target = self.OWN.get(name)
+            if target is None:
+                if name in self.ABSENT:
+                    raise KeyError(f"kv transport {name!r} is a vendor P2P path this package "
+                                   f"does not provide")
+                hint = "" if rm_compat.registry is not None else " (rm-core is not installed)"
+                raise KeyError(f"no kv transport named {name!r}{hint}")
+            import importlib
+            module, attr = target.split(":")
+            impl = getattr(importlib.import_module(module), attr)(**kw)
+        self._factories[name] = type(impl)
+        return impl
+
+    def select(self, name, kw):
+        with self._lock:
+            if not kw and name in self._held:
+                return self._held[name]
+            impl = self._construct(name, kw)
+            if isinstance(impl, Transport):
+                if not kw and getattr(impl, "shared", False):
+                    self._held[name] = impl
+                return impl
+            fenced = FencedTransport(impl)
+            if not kw:
+                self._held[name] = fenced
+            return fenced
 
 
-def _resolve(name, kw):
-    cls = _CLASSES.get(name)
-    if cls is not None:
-        return cls(**kw)
-    from .. import rm_compat
-    try:
-        impl = rm_compat.registry.load("airm.kv_transports", name, **kw)
-    except KeyError:
-        if name in _NOT_HERE:
-            raise KeyError(f"AIRM_KV_TRANSPORT={name!r} is a cross-node transport this "
-                           f"package does not provide")
-        if name not in _OWN:
-            raise
-        import importlib
-        mod, obj = _OWN[name].split(":")
-        impl = getattr(importlib.import_module(mod), obj)(**kw)
-    _CLASSES[name] = type(impl)
-    return impl
+_SELECTOR = _Selector()
+
+
+def reset_selection():
+    """Drop the process's resolved transports (for tests that change the environment)."""
+    _SELECTOR.reset()
 
 
 def select_transport(name=None, **kw) -> Transport:
     """The connector's KV path by name: ``name``, else $AIRM_KV_TRANSPORT, else "shm".
 
-    An implementation that speaks push/pull is returned as is (one shared instance
-    per process if it declares ``shared``); a tier-to-tier transport is wrapped in
-    FencedTransport. An unknown name raises KeyError: there is no fallback.
-    """
-    name = name or os.environ.get("AIRM_KV_TRANSPORT") or "shm"
-    with _LOCK:
-        if not kw and name in _FENCED:
-            return _FENCED[name]
-        if not kw and name in _SHARED:
-            return _SHARED[name]
-        impl = _resolve(name, kw)
-        if isinstance(impl, Transport):
-            if not kw and getattr(impl, "shared", False):
-                _SHARED[name] = impl
-            return impl
-        t = FencedTransport(impl)
-        if not kw:
-            _FENCED[name] = t
-        return t
+    Keyword arguments go to the implementation's constructor (and then bypass
+    the per-process instances). An unknown name raises KeyError."""
+    return _SELECTOR.select(name or os.environ.get("AIRM_KV_TRANSPORT") or "shm", kw)
 
 
 def make_transport(backend="shm", **kw) -> Transport:

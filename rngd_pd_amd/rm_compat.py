@@ -16,21 +16,19 @@ behaviour the reference's call sites rely on:
   Measurement(name, value, tags).validate()             airm.py:121-123
   ContractError, TransportError, conformance.NoHardware
 
-The stand-in is a test double for the contract: rm-core's own conformance
-checks (``rm_core.conformance.check_kv_transport``) are not reproduced bit for
-bit; ``check_kv_transport`` here runs the plan/submit/wait/take/close sequence
-the adapter's ``conformance_case`` is built for (airm.py:204-221).
+Without rm-core there is no ``registry`` (None): transport selection then
+knows only this package's own transports, as the reference's does
+(connector/transport.py:307-318). rm-core's conformance runner
+(``rm_core.conformance.check_kv_transport``) and its reference transports are
+not part of this package; the tests carry doubles of them.
 """
-import collections
-import importlib
-import time
 from dataclasses import dataclass, field
 
 try:  # pragma: no cover - exercised only where rm-core is installed
     import rm_core as _rm
     from rm_core import (ContractError, KVLayout, Measurement, MemoryTier, TransferHandle,  # noqa: F401
                          TransferPlan, TransferResult, TransportError, prometheus_name)
-    from rm_core.conformance import NoHardware, check_kv_transport  # noqa: F401
+    from rm_core.conformance import NoHardware  # noqa: F401
     from rm_core import registry  # noqa: F401
     HAVE_RM_CORE = True
 except ImportError:
@@ -122,83 +120,6 @@ if not HAVE_RM_CORE:
     def prometheus_name(name):
         return "airm_" + name
 
-    class _Registry:
-        """Entry-point registry over this package's own ``airm.kv_transports``."""
-
-        GROUPS = {"airm.kv_transports": {"shm": "rngd_pd_amd.airm:ShmTransport"}}
-
-        def available(self, group):
-            return dict(self.GROUPS.get(group, {}))
-
-        def load(self, group, name, **kw):
-            target = self.GROUPS.get(group, {}).get(name)
-            if target is None:
-                raise KeyError(f"{group}: no entry point named {name!r}")
-            mod, obj = target.split(":")
-            return getattr(importlib.import_module(mod), obj)(**kw)
-
-    registry = _Registry()
-
-    def check_kv_transport(t, timeout_s=5.0):
-        """plan -> submit -> wait -> take -> close on the transport's own case,
-        checking the bf16 round trip and the refusal of a bad token range."""
-        import numpy as np
-        src, dst, layout = t.conformance_case()
-        try:
-            try:
-                t.plan("conf-bad", src, dst, layout, layout, (4, 4))
-            except TransportError:
-                pass
-            else:
-                raise AssertionError("empty token range was not refused")
-            plan = t.plan("conf", src, dst, layout, layout, (0, 4))
-            n = plan.nbytes // 2
-            kv = np.random.default_rng(7).standard_normal(n).astype(np.float32)
-            res = t.wait(t.submit(plan, kv=kv), timeout_s=timeout_s)
-            if not res.ok or res.nbytes != plan.nbytes:
-                raise AssertionError(f"transfer failed: {res}")
-            got = np.asarray(t.take(plan), np.float32).reshape(-1)
-            want = (kv.view(np.uint32) >> 16 << 16).view(np.float32)
-            if plan.detail.get("wire", "bf16") == "bf16" and not np.array_equal(
-                    got.view(np.uint32), want.view(np.uint32)):
-                raise AssertionError("payload changed in transit")
-            if not t.measurements or t.measurements[-1].name != "kv_transfer_ms":
-                raise AssertionError("no kv_transfer_ms measurement recorded")
-        finally:
-            t.close()
-
-    class LoopbackTransport:
-        """Tier-to-tier transport that completes at once (a test double for the
-        ``FencedTransport`` path; rm-core ships one as rm_core.reference)."""
-
-        name = "loopback"
-
-        def __init__(self, fail_request_ids=()):
-            self.fail = set(fail_request_ids)
-            self._handles = {}
-            self.measurements = collections.deque(maxlen=1024)
-
-        def plan(self, request_id, src, dst, src_layout, dst_layout, tokens):
-            start, end = tokens
-            if not 0 <= start < end:
-                raise TransportError(f"bad token range {tokens}")
-            return TransferPlan(request_id, src, dst, src_layout, dst_layout, tokens,
-                                (end - start) * src_layout.bytes_per_token())
-
-        def submit(self, plan, kv=None):
-            token = f"{len(self._handles)}.{time.perf_counter_ns()}"
-            self._handles[token] = plan
-            return TransferHandle(plan.request_id, self.name, token)
-
-        def wait(self, handle, timeout_s):
-            plan = self._handles.pop(handle.token, None)
-            if plan is None:
-                raise TransportError(f"unknown handle {handle.token}")
-            if plan.request_id in self.fail:
-                return TransferResult(plan.request_id, False, 0, 0.0, "injected failure")
-            return TransferResult(plan.request_id, True, plan.nbytes, 0.0)
-
-        def close(self):
-            self._handles.clear()
-
-    registry.GROUPS["airm.kv_transports"]["loopback"] = "rngd_pd_amd.rm_compat:LoopbackTransport"
+    # Without rm-core there is no entry-point registry: select_transport then
+    # resolves only this package's own transports (shm, tcp, ipc).
+    registry = None

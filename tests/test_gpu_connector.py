@@ -97,7 +97,7 @@ def test_device_to_device_through_selected_shm(cuda, monkeypatch):
     with _tmpdir() as root:
         monkeypatch.setenv("PD_SHM_ROOT", root)
         monkeypatch.setenv("AIRM_KV_TRANSPORT", "shm")
-        kv._CLASSES.clear()
+        kv.reset_selection()
         pf = RngdKVConnector(KVConnectorRole.WORKER, req_id="g3", n_layers=L, frame_tokens=S)
         dk, dv = to_dev(k), to_dev(v)
         for i in range(L):
@@ -114,7 +114,7 @@ def test_device_to_device_through_selected_shm(cuda, monkeypatch):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(to_host(back), orc.pack_kv(k, v, P, S))
         dc.close()
-        kv._CLASSES.clear()
+        kv.reset_selection()
 
 
 def test_device_to_device_through_tcp_relay(cuda, monkeypatch):

@@ -17,7 +17,8 @@ import numpy as np
 import pytest
 
 from oracle import tcpkv as otcp
-from rngd_pd_amd import airm, rm_compat
+from rngd_pd_amd import airm, rm_compat  # noqa: F401
+from tests.rm_doubles import check_kv_transport
 from rngd_pd_amd.connector import tcp
 from rngd_pd_amd.connector import transport as kv
 
@@ -165,15 +166,11 @@ def tcp_env(monkeypatch):
     srv = tcp.TcpKVServer(0, "127.0.0.1").start()
     monkeypatch.setenv("AIRM_KV_TCP_ADDR", f"127.0.0.1:{srv.wait_ready()}")
     monkeypatch.delenv("AIRM_KV_TRANSPORT", raising=False)
-    kv._FENCED.clear()
-    kv._CLASSES.clear()
-    kv._SHARED.clear()
+    kv.reset_selection()
     yield srv
-    for t in list(kv._SHARED.values()):
+    for t in kv._SELECTOR.held().values():
         t.close()
-    kv._FENCED.clear()
-    kv._CLASSES.clear()
-    kv._SHARED.clear()
+    kv.reset_selection()
     srv.stop()
 
 
@@ -195,7 +192,7 @@ def test_needs_an_address(monkeypatch):
 def test_adapter_conformance_and_payload(tcp_env, monkeypatch):
     monkeypatch.delenv("AIRM_KV_TCP_ADDR")
     t = airm.TcpTransport()                                  # conformance starts its own relay
-    rm_compat.check_kv_transport(t)
+    check_kv_transport(t)
     assert t.measurements[-1].tags["kv_transport"] == "tcp"
     t.close()
     monkeypatch.setenv("AIRM_KV_TCP_ADDR", f"127.0.0.1:{tcp_env.port}")
