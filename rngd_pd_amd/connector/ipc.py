@@ -12,7 +12,8 @@ save_kv_layer / wait_for_save on the prefill side and register_kv_caches(view)
 Producer. An IpcFramePool owns one device allocation of n_slots request frames
 [L][2][Hkv*D*S] bf16 (the layout of the shm wire payload), kept below 2 GiB
 because IPC mappings on this platform must be. An IpcSaver (one request) packs
-each saved layer into its slot on the process's save stream. wait() waits on
+each saved layer into its slot on the process's save stream, writing only the
+valid columns (the consumer's scatter never reads the S-wide zero tail). wait() waits on
 the host for those packs to finish, then publishes the descriptor "<req>/ipc"
 (a small JSON file) with the shm publish sequence (tmp + fsync + rename): a
 descriptor only ever names a complete frame. (Interprocess events, which would
@@ -144,8 +145,10 @@ class IpcSaver:
             for t in (k, v):
                 t.record_stream(self.stream)
             layer_bytes = pool.frame_bytes // pool.L
+            # Narrow: the consumer's scatter reads only columns < P, so the
+            # S-wide zero tail would be bytes written that nobody reads.
             _h.pack_kv(k, v, self.P, pool.S, stream=self.stream,
-                       frame_ptr=pool.frame_ptr(self.slot) + li * layer_bytes)
+                       frame_ptr=pool.frame_ptr(self.slot) + li * layer_bytes, narrow=True)
         self._layers.add(li)
 
     def wait(self):
@@ -160,7 +163,8 @@ class IpcSaver:
         ev.sync()                                    # the frame is complete in HBM
         desc = {"v": 1, "pool": pool.mem_handle, "pool_bytes": pool.buf.nbytes,
                 "offset": self.slot * pool.frame_bytes, "L": pool.L, "H": pool.H,
-                "D": pool.D, "S": pool.S, "P": self.P, "pid": os.getpid()}
+                "D": pool.D, "S": pool.S, "P": self.P, "pid": os.getpid(),
+                "columns": "valid"}         # columns >= P of the frame are not written
         self.t.push(f"{self.req_id}/ipc", json.dumps(desc).encode())
         self._published = True
 

@@ -19,6 +19,15 @@ CUDA tensors take the device path, with the signatures unchanged:
       wait_for_layer_load(name) pulls the layer's files into pinned memory,
       copies the payloads to the device and scatters them into the paged cache;
       it returns the layer's device frames (k [Hkv, D, S], v [Hkv, S, D]).
+      The load consumes the handoff: once every layer start_load_kv named has
+      loaded, the files of those layers are removed from the transport (what
+      the reference's decode worker does after its load, serving/cluster.py:
+      461-466; a kept request would hold 64 MiB of /dev/shm at S=512). Only
+      this request's own keys are removed.
+
+load_request() is that decode-worker load on the host path (serving/cluster.py:
+438-467): zeroed float32 K/V, every layer through the connector, then the
+request's files removed.
 """
 import os
 from dataclasses import dataclass, field
@@ -80,6 +89,7 @@ class RngdKVConnector(KVConnectorBase_V1):
         self._saver = None
         self._loader = None
         self._sent_reqs = set()
+        self._loaded = set()
 
     @property
     def role(self):
@@ -182,7 +192,10 @@ class RngdKVConnector(KVConnectorBase_V1):
                 self._loader = Loader(self.t, self.req_id, view, view.cache.n_layers,
                                       view.cache.n_kv_heads, view.cache.head_dim,
                                       device=view.cache.device, timeout=t)
-            return self._loader.load(layer_name, li)
+            frames = self._loader.load(layer_name, li)
+            self._loaded.add(layer_name)
+            self._consume_if_complete()
+            return frames
         k = deser(self.t.pull(f"{self.req_id}/{layer_name}/k", timeout=t))
         v = deser(self.t.pull(f"{self.req_id}/{layer_name}/v", timeout=t))
         if self._kv_caches is not None:
@@ -197,6 +210,18 @@ class RngdKVConnector(KVConnectorBase_V1):
                 self._kv_caches[1][li][:] = v
         return k, v
 
+    def _consume_if_complete(self):
+        """Remove the loaded layers' keys once every expected layer is in."""
+        expected = set(self._loading or [f"layer.{i}" for i in range(self.n_layers)])
+        if not expected or not expected <= self._loaded or getattr(self.t, "device_ipc", False):
+            return
+        discard = getattr(self.t, "discard", None)
+        if discard is None:              # a transport whose pull already consumed (tcp)
+            return
+        for name in sorted(expected):
+            discard(f"{self.req_id}/{name}/k")
+            discard(f"{self.req_id}/{name}/v")
+
     def get_finished(self, finished_req_ids):
         """(requests whose asynchronous save completed, None)."""
         sent, self._sent_reqs = self._sent_reqs, set()
@@ -209,3 +234,31 @@ class RngdKVConnector(KVConnectorBase_V1):
         if self._loader is not None:
             self._loader.close()
             self._loader = None
+
+
+def load_request(req_id, n_layers, n_kv_heads, head_dim, S, transport=None):
+    """One request's load on the decode side's host path (serving/cluster.py:438-467).
+
+    K [L, Hkv, D, S] and V [L, Hkv, S, D] float32 start at zero (a producer may
+    ship only the prompt's columns), every layer is loaded through the
+    connector, and the request's files are then removed from the transport.
+    Returns (K, V, load_ms)."""
+    import time
+    K = np.zeros((n_layers, n_kv_heads, head_dim, S), np.float32)
+    V = np.zeros((n_layers, n_kv_heads, S, head_dim), np.float32)
+    t = transport or select_transport()
+    conn = RngdKVConnector(KVConnectorRole.WORKER, req_id=req_id, transport=t, n_layers=n_layers)
+    conn.register_kv_caches(([K[i] for i in range(n_layers)], [V[i] for i in range(n_layers)]))
+    conn.bind_connector_metadata(conn.build_connector_meta(None))
+    t0 = time.perf_counter()
+    conn.start_load_kv()
+    for i in range(n_layers):
+        conn.wait_for_layer_load(f"layer.{i}")
+    load_ms = (time.perf_counter() - t0) * 1e3
+    if hasattr(t, "discard_request"):
+        t.discard_request(req_id)
+    elif hasattr(t, "discard"):
+        for i in range(n_layers):
+            t.discard(f"{req_id}/layer.{i}/k")
+            t.discard(f"{req_id}/layer.{i}/v")
+    return K, V, load_ms

@@ -63,14 +63,16 @@ def _as_layers(k, v):
     return k, v
 
 
-def pack_kv(k, v, num_tokens, S, frame=None, stream=None, frame_ptr=None):
+def pack_kv(k, v, num_tokens, S, frame=None, stream=None, frame_ptr=None, narrow=False):
     """Pack the first ``num_tokens`` tokens of every layer into an S-wide frame.
 
     Replaces engines/prefill_full.py:378-382 (zero-pad to S, download) and the
     bf16 encode of connector/transport.py:33-35. ``frame_ptr`` (instead of
     ``frame``) packs into any device-visible memory of the frame's size, such
     as a pinned host buffer: the kernel's own stores then carry the download,
-    with no staging copy. Returns the frame tensor, or None with frame_ptr."""
+    with no staging copy. ``narrow`` leaves the columns >= num_tokens unwritten,
+    for a consumer that reads only the valid columns (the same-GPU scatter).
+    Returns the frame tensor, or None with frame_ptr."""
     _need(k, "k")
     _need(v, "v")
     k, v = _as_layers(k, v)
@@ -87,8 +89,9 @@ def pack_kv(k, v, num_tokens, S, frame=None, stream=None, frame_ptr=None):
         elif tuple(frame.shape) != frame_shape(L, H, D, S) or not frame.is_contiguous():
             raise ValueError(f"frame must be contiguous {frame_shape(L, H, D, S)}")
         ptr = frame.data_ptr()
-    _lib.call("pdk_pack_kv", k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), L,
-              int(num_tokens), S, H, D, ptr, stream_handle(stream))
+    req = PackReq(k.data_ptr(), v.data_ptr(), ptr, k.stride(0), k.stride(1), int(num_tokens),
+                  _lib.PDK_PACK_NARROW if narrow else 0)
+    _lib.call("pdk_pack_kv_batch", ctypes.byref(req), 1, L, S, H, D, stream_handle(stream))
     return frame
 
 

@@ -4,33 +4,39 @@
     python tests/ipc_peer.py consumer ROOT N
 
 The producer saves N requests through RngdKVConnector on the ipc transport,
-with 2 frame slots, so slots must come back from the consumer. The consumer
-loads them into a paged cache through the connector and checks each against a
-local pack + scatter of the same seeded KV, bit for bit. Both print one line
-per step and exit non-zero on any mismatch.
+with 2 frame slots, so slots must come back from the consumer. Request r's KV
+is random bf16 bit patterns from numpy seed 100 + r, which both sides draw.
+The consumer loads every request into a paged cache through the connector and
+checks the whole cache, bit for bit, against the oracle's pack + scatter of
+the same bits into the same block ids, and each request's frame read back from
+the cache against the oracle's S-wide frame. Both print one line per step and
+exit non-zero on any mismatch.
 """
 import os
 import sys
 
 sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 
+import numpy as np  # noqa: E402
+
 L, H, D, S = 4, 8, 128, 512
 LENGTHS = [509, 64, 300, 512]
 
 
-def kv_of(torch, r, dev):
-    gen = torch.Generator(device=dev).manual_seed(100 + r)
-    return torch.randn((L, 2, S, H, D), generator=gen, device=dev).to(torch.bfloat16)
+def kv_bits(r):
+    """Request r's prefill KV [L, 2, S, H, D] as bf16 bit patterns."""
+    return np.random.default_rng(100 + r).integers(0, 1 << 16, (L, 2, S, H, D), dtype=np.uint16)
 
 
 def producer(root, n):
     import torch
     from rngd_pd_amd.connector.ipc import IpcTransport
     from rngd_pd_amd.connector.rngd_kv import KVConnectorRole, RngdKVConnector
+    from tests._util import to_dev
     dev = torch.device("cuda:0")
     t = IpcTransport(root, n_slots=2)
     for r in range(n):
-        kv = kv_of(torch, r, dev)
+        kv = to_dev(kv_bits(r), dev)
         c = RngdKVConnector(KVConnectorRole.WORKER, req_id=f"req{r}", transport=t, n_layers=L,
                             frame_tokens=S)
         for layer in range(L):
@@ -45,15 +51,18 @@ def producer(root, n):
 
 def consumer(root, n):
     import torch
+    from oracle import native as orc
     from rngd_pd_amd.connector import ipc
     from rngd_pd_amd.connector.ipc import IpcTransport
     from rngd_pd_amd.connector.rngd_kv import KVConnectorRole, RngdKVConnector
     from rngd_pd_amd.engines.paged_cache import PagedKVCache
-    from rngd_pd_amd.kernels import handoff as K
+    from tests._util import to_host
     dev = torch.device("cuda:0")
     t = IpcTransport(root)
-    cache = PagedKVCache(L, n * (S // 16) + 4, H, D, device=dev, seed=7)
-    want = PagedKVCache(L, n * (S // 16) + 4, H, D, device=dev, seed=7)
+    nb = n * (S // 16) + 4
+    cache = PagedKVCache(L, nb, H, D, device=dev, seed=7)
+    want_k = np.zeros((L, nb, H, 16, D), np.uint16)      # the cache starts zeroed
+    want_v = np.zeros((L, nb, H, D, 16), np.uint16)
     bad = 0
     for r in range(n):
         P = LENGTHS[r % len(LENGTHS)]
@@ -65,19 +74,16 @@ def consumer(root, n):
         for layer in range(L):
             c.wait_for_layer_load(f"layer.{layer}")
         c.close()
-        # The same KV packed and scattered locally, into the same block ids.
-        kv = kv_of(torch, r, dev)
-        frame = K.pack_kv(kv[:, 0], kv[:, 1], P, S)
-        want.allocate(req, P)
-        assert want.blocks(req) == cache.blocks(req)
-        K.scatter_paged(frame, want.table(req), P, S, want.k, want.v)
+        kv = kv_bits(r)
+        frame = orc.pack_kv(kv[:, 0], kv[:, 1], P, S)
+        orc.scatter_paged(frame, np.asarray(cache.blocks(req), np.int32), P, S, H, D,
+                          want_k, want_v)
         back = cache.read_frame(req, P, S)
         torch.cuda.synchronize()
-        ok = (torch.equal(cache.k.view(torch.int16), want.k.view(torch.int16))
-              and torch.equal(cache.v.view(torch.int16), want.v.view(torch.int16))
-              and torch.equal(back.view(torch.int16), frame.view(torch.int16)))
+        ok = (np.array_equal(to_host(cache.k), want_k) and np.array_equal(to_host(cache.v), want_v)
+              and np.array_equal(to_host(back), frame))
         bad += not ok
-        print(f"consumer req{r} P={P}: {'bit-exact' if ok else 'MISMATCH'}", flush=True)
+        print(f"consumer req{r} P={P}: {'bit-exact vs oracle' if ok else 'MISMATCH'}", flush=True)
     ipc.close_opened()
     print(f"ipc consumer {'ok' if bad == 0 else 'FAILED'} {n}", flush=True)
     return 1 if bad else 0

@@ -122,3 +122,34 @@ def test_dict_caches_and_stacked_layer():
             np.testing.assert_array_equal(v, want[1])
     finally:
         kv.WIRE = old
+
+
+def test_load_request_consumes_only_its_own_files():
+    """The decode worker's host-path load (serving/cluster.py:438-467): zeroed f32
+    K [L, Hkv, D, S] / V [L, Hkv, S, D], every layer loaded, then the request's
+    files gone; another request whose id shares a prefix keeps its files."""
+    from rngd_pd_amd.connector.rngd_kv import load_request
+    rng = np.random.default_rng(SEED)
+    K = rng.standard_normal((NL, NKV, HD, S)).astype(np.float32)
+    V = rng.standard_normal((NL, NKV, S, HD)).astype(np.float32)
+    with tempfile.TemporaryDirectory(dir="/dev/shm" if os.access("/dev/shm", os.W_OK) else None) as root:
+        t = kv.ShmTransport(root)
+        for req in ("r7", "r77"):
+            conn = RngdKVConnector(KVConnectorRole.WORKER, req_id=req, transport=t, n_layers=NL)
+            for i in range(NL):
+                conn.save_kv_layer(f"layer.{i}", (K[i], V[i]))
+        old = kv.WIRE
+        try:
+            kv.WIRE = "bf16"
+            for i in range(NL):                       # r7 goes over the bf16 wire
+                for which, arr in (("k", K[i]), ("v", V[i])):
+                    t.push(f"r7/layer.{i}/{which}", kv.ser(arr))
+        finally:
+            kv.WIRE = old
+        gotK, gotV, ms = load_request("r7", NL, NKV, HD, S, transport=t)
+        trunc = lambda a: (a.view(np.uint32) >> 16 << 16).view(np.float32)   # noqa: E731
+        np.testing.assert_array_equal(gotK, trunc(K))
+        np.testing.assert_array_equal(gotV, trunc(V))
+        assert ms >= 0
+        left = sorted(os.listdir(root))
+        assert left == sorted(f"r77__layer.{i}__{w}" for i in range(NL) for w in "kv")

@@ -87,33 +87,45 @@ def test_device_load_matches_oracle_scatter(cuda, P, S):
         conn.close()
 
 
-def test_device_to_device_through_selected_shm(cuda, monkeypatch):
+@pytest.mark.parametrize("nl,P", [(4, 333), (32, 512)])
+def test_device_to_device_through_selected_shm(cuda, monkeypatch, nl, P):
+    """Device save -> /dev/shm -> device load through select_transport("shm"); at
+    nl=32, P=S=512 this is one whole Llama-3.1-8B request (64 MiB on the wire).
+    The load consumes the request's files and nothing else: files of another
+    request (one whose id extends this one's) survive the load and close()."""
     from rngd_pd_amd.connector import transport as kv
     from rngd_pd_amd.connector.rngd_kv import KVConnectorRole, RngdKVConnector
     from rngd_pd_amd.engines.paged_cache import PagedKVCache
-    S, P = 512, 333
-    rng = np.random.default_rng(77)
-    k, v = rand_bf16(rng, (L, S, H, D)), rand_bf16(rng, (L, S, H, D))
+    S = 512
+    rng = np.random.default_rng(77 + nl)
+    k, v = rand_bf16(rng, (nl, S, H, D)), rand_bf16(rng, (nl, S, H, D))
     with _tmpdir() as root:
         monkeypatch.setenv("PD_SHM_ROOT", root)
         monkeypatch.setenv("AIRM_KV_TRANSPORT", "shm")
         kv.reset_selection()
-        pf = RngdKVConnector(KVConnectorRole.WORKER, req_id="g3", n_layers=L, frame_tokens=S)
+        pf = RngdKVConnector(KVConnectorRole.WORKER, req_id="g3", n_layers=nl, frame_tokens=S)
         dk, dv = to_dev(k), to_dev(v)
-        for i in range(L):
+        for i in range(nl):
             pf.save_kv_layer(f"layer.{i}", torch.stack([dk[i], dv[i]]), num_tokens=P)
         pf.wait_for_save()
         pf.close()
-        cache = PagedKVCache(L, 64, H, D, device=cuda, seed=1)
-        dc = RngdKVConnector(KVConnectorRole.WORKER, req_id="g3", n_layers=L)
+        decoys = ["g33__layer.0__k", "other__layer.0__v"]
+        for name in decoys:
+            with open(os.path.join(root, name), "wb") as f:
+                f.write(b"not mine")
+        assert len(os.listdir(root)) == 2 * nl + len(decoys)
+        cache = PagedKVCache(nl, 2 * ((S + 15) // 16), H, D, device=cuda, seed=1)
+        dc = RngdKVConnector(KVConnectorRole.WORKER, req_id="g3", n_layers=nl)
         dc.register_kv_caches(cache.view("g3", P, S))
         dc.start_load_kv()
-        for i in range(L):
+        for i in range(nl):
             dc.wait_for_layer_load(f"layer.{i}")
         back = cache.read_frame("g3", P, S)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(to_host(back), orc.pack_kv(k, v, P, S))
+        assert sorted(os.listdir(root)) == sorted(decoys)     # consumed, decoys kept
         dc.close()
+        assert sorted(os.listdir(root)) == sorted(decoys)
         kv.reset_selection()
 
 
