@@ -177,6 +177,24 @@ int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k,
                     void* workspace, size_t workspace_bytes, uint16_t* out,
                     uintptr_t stream);
 
+/* pdk_decode_attn without the workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The split
+ * partials live in a file-scope device array of PDK_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends; a launch whose plan needs more than that
+ * (pdk_decode_attn_workspace_bytes) is refused with PDK_ENOMEM. The call
+ * allocates nothing. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be ordered
+ * by the caller. Results are bit-identical to pdk_decode_attn's. Llama-3.1-8B
+ * shapes (32 query heads over 8 KV heads) need at most about 1 MiB. */
+#define PDK_NOALLOC_SCRATCH_BYTES (4u << 20)
+int pdk_decode_attn_noalloc(const uint16_t* q, const uint16_t* cache_k,
+                            const uint16_t* cache_v, int num_blocks,
+                            const int32_t* block_tables, int max_blocks,
+                            const int32_t* ctx_lens, int max_ctx, int B,
+                            int n_q_heads, int n_kv_heads, int head_dim,
+                            float scale, uint16_t* out, uintptr_t stream);
+
 /* pdk_rope_cache_append_partials followed by pdk_decode_attn, in one launch:
  * q, k and v of the new token come as split-K partial sums of the q|k|v
  * projection (qkv_partials [splits][B][(n_q_heads + 2 n_kv_heads) head_dim]

@@ -18,6 +18,7 @@ PDK_ENOMEM = -12
 PDK_EINVAL = -22
 PDK_ENOTSUP = -95
 PDK_MAX_BATCH = 16
+PDK_NOALLOC_SCRATCH_BYTES = 4 << 20
 PDK_BLOCK_SIZE = 16
 PDK_IPC_HANDLE_BYTES = 64
 PDK_EVENT_TIMING = 0
@@ -76,6 +77,8 @@ SIGNATURES = {
     "pdk_decode_attn_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "pdk_decode_attn": (_I, [_P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, ctypes.c_float,
                              _P, _SZ, _P, _U]),
+    "pdk_decode_attn_noalloc": (_I, [_P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I,
+                                     ctypes.c_float, _P, _U]),
     "pdk_decode_attn_rope": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I,
                                   ctypes.c_float, _P, _SZ, _P, _U]),
     "pdk_cache_append": (_I, [_P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _U]),

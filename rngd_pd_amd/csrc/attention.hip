@@ -34,6 +34,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "pdk_common.h"
 
@@ -599,6 +600,41 @@ __global__ void cache_append_kernel(const uint16_t* k_new, const uint16_t* v_new
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// Scratch of pdk_decode_attn_noalloc: the split partials (what the workspace
+// argument of pdk_decode_attn holds) in a file-scope device array, so that a
+// caller that cannot allocate needs none. Each GPU holds its own copy. Host
+// code never passes `scratch` itself to a kernel (in host code the name is a
+// stand-in, not a device address): the device address comes from
+// hipGetSymbolAddress, once per device, and is kept in scratch_ptr.
+static __device__ __align__(256) char scratch[PDK_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+void* scratch_ptr[kMaxDevices];
+std::mutex scratch_mu;
+
+// The current device's scratch address (looked up on the first call on that
+// device, with it current); null and an error message on failure.
+void* device_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    pdk::set_error("no current HIP device (or device index >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      pdk::hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                    "hipGetSymbolAddress(scratch)");
+      return nullptr;
+    }
+    scratch_ptr[dev] = p;
+  }
+  return scratch_ptr[dev];
+}
+
 // Launch plan. One workgroup per (stream, KV head, split), up to 8
 // wavefronts of 64 tokens each in flight. The context is split across
 // workgroups until about 256 of them (one per CU) exist, in splits of at least
@@ -740,6 +776,37 @@ extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const
   return launch_attn(q, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens, max_ctx,
                      B, n_q_heads, n_kv_heads, head_dim, scale, workspace, workspace_bytes, out,
                      stream, RopeIn{nullptr, 0, nullptr, nullptr, nullptr});
+}
+
+extern "C" int pdk_decode_attn_noalloc(const uint16_t* q, const uint16_t* cache_k,
+                                       const uint16_t* cache_v, int num_blocks,
+                                       const int32_t* block_tables, int max_blocks,
+                                       const int32_t* ctx_lens, int max_ctx, int B,
+                                       int n_q_heads, int n_kv_heads, int head_dim, float scale,
+                                       uint16_t* out, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(q, "null pointer argument");
+  PDK_REQUIRE(B >= 1 && n_q_heads >= 1 && n_kv_heads >= 1 && max_ctx >= 1 && head_dim == kD,
+              "bad shape (B=%d, Hq=%d, Hkv=%d, max_ctx=%d, D=%d)", B, n_q_heads, n_kv_heads,
+              max_ctx, head_dim);
+  PDK_REQUIRE(n_q_heads % n_kv_heads == 0, "n_q_heads=%d must be a multiple of n_kv_heads=%d",
+              n_q_heads, n_kv_heads);
+  const Plan p = plan_for(B, n_kv_heads, max_ctx);
+  const size_t need = ws_bytes(B, n_q_heads, p.nsplit);
+  if (need > PDK_NOALLOC_SCRATCH_BYTES) {
+    pdk::set_error("this launch needs %zu bytes of split partials; the no-allocation entry "
+                   "point holds at most %zu (use pdk_decode_attn with a workspace)",
+                   need, (size_t)PDK_NOALLOC_SCRATCH_BYTES);
+    return PDK_ENOMEM;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = device_scratch();
+    if (!ws) return PDK_EHIP;
+  }
+  return launch_attn(q, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens, max_ctx,
+                     B, n_q_heads, n_kv_heads, head_dim, scale, ws, need, out, stream,
+                     RopeIn{nullptr, 0, nullptr, nullptr, nullptr});
 }
 
 extern "C" int pdk_decode_attn_rope(const float* qkv_partials, int splits, const float* inv_freq,
