@@ -206,7 +206,11 @@ int pdk_decode_attn_noalloc(const uint16_t* q, const uint16_t* cache_k,
  * bit-identical to the two calls. Replaces the RoPE rotation, the one-hot
  * cache injection and the attention of DecodeLayer.forward
  * (kernels/decode_batch.py:69-85) as one step. Other arguments and limits as
- * pdk_decode_attn (same workspace size). */
+ * pdk_decode_attn (same workspace size).
+ * plan_batch (0: B; else >= B) is the batch size the launch plan (how the
+ * context is split across workgroups, hence the order of the fp32 sums) is
+ * chosen for. A decoder that passes the same plan_batch at every step makes
+ * each stream's result independent of how many other streams share the step. */
 int pdk_decode_attn_rope(const float* qkv_partials, int splits,
                          const float* inv_freq, uint16_t* cache_k,
                          uint16_t* cache_v, int num_blocks,
@@ -214,7 +218,7 @@ int pdk_decode_attn_rope(const float* qkv_partials, int splits,
                          const int32_t* ctx_lens, int max_ctx, int B,
                          int n_q_heads, int n_kv_heads, int head_dim,
                          float scale, void* workspace, size_t workspace_bytes,
-                         uint16_t* out, uintptr_t stream);
+                         uint16_t* out, int plan_batch, uintptr_t stream);
 
 /* Write one new token's k and v per stream at slot ctx[b]-1 of the paged
  * cache: the one-hot cache injection Kf = Kp + k*oh, Vf = Vp + v*oh

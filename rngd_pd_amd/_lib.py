@@ -80,7 +80,7 @@ SIGNATURES = {
     "pdk_decode_attn_noalloc": (_I, [_P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I,
                                      ctypes.c_float, _P, _U]),
     "pdk_decode_attn_rope": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I,
-                                  ctypes.c_float, _P, _SZ, _P, _U]),
+                                  ctypes.c_float, _P, _SZ, _P, _I, _U]),
     "pdk_cache_append": (_I, [_P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _U]),
     "pdk_greedy_argmax": (_I, [_P, _I, _I, _I64, _P, _U]),
     "pdk_rmsnorm": (_I, [_P, _P, _P, _I, _I, ctypes.c_float, _P, _U]),

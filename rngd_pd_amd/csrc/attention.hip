@@ -691,7 +691,7 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
                 int num_blocks, const int32_t* block_tables, int max_blocks,
                 const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads, int n_kv_heads,
                 int head_dim, float scale, void* workspace, size_t workspace_bytes, uint16_t* out,
-                uintptr_t stream, const RopeIn& rope) {
+                uintptr_t stream, const RopeIn& rope, int plan_B) {
   if (head_dim != kD) {
     pdk::set_error("decode attention implements head_dim %d only (got %d)", kD, head_dim);
     return PDK_ENOTSUP;
@@ -712,7 +712,8 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1, "num_blocks and max_blocks must be >= 1");
   PDK_REQUIRE(max_ctx >= 1 && max_ctx <= max_blocks * 16,
               "max_ctx=%d outside [1, max_blocks*16=%d]", max_ctx, max_blocks * 16);
-  const Plan p = plan_for(B, n_kv_heads, max_ctx);
+  PDK_REQUIRE(plan_B >= B && plan_B <= 65535, "plan_batch=%d must be in [B=%d, 65535]", plan_B, B);
+  const Plan p = plan_for(plan_B, n_kv_heads, max_ctx);
   AttnArgs a{};
   a.q = q;
   a.ck = cache_k;
@@ -775,7 +776,7 @@ extern "C" int pdk_decode_attn(const uint16_t* q, const uint16_t* cache_k, const
   PDK_REQUIRE(q, "null pointer argument");
   return launch_attn(q, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens, max_ctx,
                      B, n_q_heads, n_kv_heads, head_dim, scale, workspace, workspace_bytes, out,
-                     stream, RopeIn{nullptr, 0, nullptr, nullptr, nullptr});
+                     stream, RopeIn{nullptr, 0, nullptr, nullptr, nullptr}, B);
 }
 
 extern "C" int pdk_decode_attn_noalloc(const uint16_t* q, const uint16_t* cache_k,
@@ -806,7 +807,7 @@ extern "C" int pdk_decode_attn_noalloc(const uint16_t* q, const uint16_t* cache_
   }
   return launch_attn(q, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens, max_ctx,
                      B, n_q_heads, n_kv_heads, head_dim, scale, ws, need, out, stream,
-                     RopeIn{nullptr, 0, nullptr, nullptr, nullptr});
+                     RopeIn{nullptr, 0, nullptr, nullptr, nullptr}, B);
 }
 
 extern "C" int pdk_decode_attn_rope(const float* qkv_partials, int splits, const float* inv_freq,
@@ -814,7 +815,8 @@ extern "C" int pdk_decode_attn_rope(const float* qkv_partials, int splits, const
                                     const int32_t* block_tables, int max_blocks,
                                     const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads,
                                     int n_kv_heads, int head_dim, float scale, void* workspace,
-                                    size_t workspace_bytes, uint16_t* out, uintptr_t stream) {
+                                    size_t workspace_bytes, uint16_t* out, int plan_batch,
+                                    uintptr_t stream) {
   pdk::clear_error();
   PDK_REQUIRE(qkv_partials && inv_freq, "null pointer argument");
   PDK_REQUIRE(splits == 1 || splits == 2 || splits == 4, "splits must be 1, 2 or 4 (got %d)",
@@ -822,7 +824,8 @@ extern "C" int pdk_decode_attn_rope(const float* qkv_partials, int splits, const
   return launch_attn(nullptr, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens,
                      max_ctx, B, n_q_heads, n_kv_heads, head_dim, scale, workspace,
                      workspace_bytes, out, stream,
-                     RopeIn{qkv_partials, splits, inv_freq, cache_k, cache_v});
+                     RopeIn{qkv_partials, splits, inv_freq, cache_k, cache_v},
+                     plan_batch > 0 ? plan_batch : B);
 }
 
 extern "C" int pdk_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* cache_k,

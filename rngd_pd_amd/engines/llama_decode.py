@@ -115,10 +115,15 @@ class LlamaWeights:
 class LlamaDecoder:
     """B-stream decode steps over a PagedKVCache (same n_layers, Hkv, head_dim)."""
 
-    def __init__(self, weights, cache, max_batch, tiled=True):
+    def __init__(self, weights, cache, max_batch, tiled=True, plan_batch=None):
         """``tiled``: stream tiled copies of the projection and lm_head weights
         (the copies take as much device memory as those weights again; the
-        originals are left untouched)."""
+        originals are left untouched). ``plan_batch`` (default max_batch): the
+        batch size every step's attention plans its context split for. Each
+        stream's result then does not depend on how many streams share a step:
+        every other kernel of the step computes a row independently of the
+        others, so a stream's tokens are the same at B = 1 as in any batch of
+        a decoder with the same plan_batch."""
         cfg = self.cfg = weights.cfg
         if (cache.n_layers, cache.n_kv_heads, cache.head_dim) != (cfg.n_layers, cfg.n_kv_heads,
                                                                   cfg.head_dim):
@@ -127,6 +132,10 @@ class LlamaDecoder:
         dev = self.device = cache.k.device          # the real device (cuda:N)
         B, H = max_batch, cfg.hidden
         self.max_batch = B
+        self.plan_batch = int(plan_batch or max_batch)
+        if self.plan_batch < max_batch:
+            raise ValueError(f"plan_batch={plan_batch} below max_batch={max_batch}")
+        self._captured = False
         e = lambda *s: torch.empty(s, dtype=BF16, device=dev)   # noqa: E731
         self.x, self.h = e(B, H), e(B, H)
         self.ao = e(B, cfg.n_heads, cfg.head_dim)
@@ -174,11 +183,19 @@ class LlamaDecoder:
     def reserve(self, max_ctx):
         """Allocate the attention workspace for max_batch streams at ``max_ctx``
         now, so that no later step (or graph capture) allocates it."""
-        self._workspace(self.max_batch, max_ctx)
+        self._workspace(self.plan_batch, max_ctx)
 
     def _workspace(self, B, max_ctx):
+        """The attention workspace, grown when a step needs more. A captured
+        graph holds the address it was captured with, so once any graph exists
+        a step that would need a larger one raises instead (reserve() the
+        largest max_ctx before capturing)."""
         need = _attn.workspace_bytes(B, self.cfg.n_heads, max_ctx, self.cfg.head_dim)
         if need and (self._ws is None or self._ws.numel() * 4 < need):
+            if self._captured:
+                raise RuntimeError(f"the attention workspace would have to grow to {need} bytes "
+                                   f"after a graph was captured with the old one; reserve() the "
+                                   f"largest max_ctx before capturing")
             self._ws = torch.zeros(need // 4 + 64, dtype=torch.float32, device=self.device)
         return self._ws if need else None
 
@@ -208,7 +225,7 @@ class LlamaDecoder:
         H, NH, NKV, HD, M = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.inter
         QKV, eps = cfg.qkv_dim, cfg.eps
         x = self.x[:B]
-        ws = self._workspace(B, max_ctx)
+        ws = self._workspace(max(B, self.plan_batch), max_ctx)
         ws_ptr = ws.data_ptr() if ws is not None else None
         ws_bytes = ws.numel() * 4 if ws is not None else 0
         mb, nb = tables.shape[1], cache.num_blocks
@@ -230,7 +247,7 @@ class LlamaDecoder:
                     call("pdk_rmsnorm", xp, None, n1, B, H, eps, hp, st)
                 call(lin_sk, hp, wqkv, B, H, QKV, qs, pqp, st)
                 call("pdk_decode_attn_rope", pqp, qs, inv, ck, cv, nb, tp, mb, cp, int(max_ctx),
-                     B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, st)
+                     B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, self.plan_batch, st)
                 call(lin, aop, wo, B, NH * HD, H, xp, xp, st)
                 call("pdk_rmsnorm", xp, None, n2, B, H, eps, hp, st)
                 call(lin_sw, hp, wgu, B, H, M, actp, st)
@@ -256,6 +273,7 @@ class LlamaDecoder:
         graph = torch.cuda.CUDAGraph()
         # Thread-local capture: other threads of the process (cache loaders)
         # may synchronise on their own streams while this one captures.
+        self._captured = True
         with torch.cuda.graph(graph, capture_error_mode="thread_local"):
             self.step(tokens, ctx_lens, tables, max_ctx)
         return graph

@@ -85,12 +85,15 @@ def decode_attention(q, cache_k, cache_v, block_tables, ctx_lens, max_ctx, scale
 
 
 def decode_attention_rope(qkv_partials, inv_freq, cache_k, cache_v, block_tables, ctx_lens,
-                          max_ctx, n_q_heads, scale=1.0, out=None, workspace=None, stream=None):
+                          max_ctx, n_q_heads, scale=1.0, out=None, workspace=None, stream=None,
+                          plan_batch=0):
     """RoPE, the new token's cache write and attention for one layer in one launch.
 
     qkv_partials float32 [splits, B, (n_q + 2 n_kv) D] (split-K partial sums of
     the q|k|v projection, splits in {1, 2, 4}); inv_freq float32 [D/2]. Same
-    result, bit for bit, as rope_cache_append_partials then decode_attention."""
+    result, bit for bit, as rope_cache_append_partials then decode_attention.
+    ``plan_batch`` (>= B; 0 means B) is the batch size the split plan is chosen
+    for: equal plan_batch gives each stream the same result whatever B is."""
     _need(qkv_partials, "qkv_partials", torch.float32)
     _need(inv_freq, "inv_freq", torch.float32)
     nb, H, D = _check_layer_cache(cache_k, cache_v)
@@ -123,7 +126,7 @@ def decode_attention_rope(qkv_partials, inv_freq, cache_k, cache_v, block_tables
               block_tables.shape[1], ctx_lens.data_ptr(), int(max_ctx), B, n_q_heads, H, D,
               float(scale), ws.data_ptr() if ws is not None else None,
               ws.numel() * ws.element_size() if ws is not None else 0, out.data_ptr(),
-              stream_handle(stream))
+              int(plan_batch), stream_handle(stream))
     return out
 
 

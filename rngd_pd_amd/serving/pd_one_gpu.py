@@ -127,7 +127,8 @@ def consumer(args):
     per = math.ceil((args.max_len + args.max_new) / 16)
     cache = PagedKVCache(cfg.n_layers, per * (args.requests + args.batch), cfg.n_kv_heads,
                          cfg.head_dim, device="cuda")
-    dec = LlamaDecoder(w, cache, max_batch=args.batch)
+    dec = LlamaDecoder(w, cache, max_batch=args.batch,
+                       plan_batch=max(args.batch, args.plan_batch))
     t = IpcTransport(args.root)
     S = frame_tokens(args)
 
@@ -179,7 +180,8 @@ def consumer(args):
 # ---------------------------------------------------------------------------
 def control(args):
     """Prefill and decode each request in one process, one at a time: the
-    tokens a correct disaggregated run with --batch 1 must reproduce."""
+    tokens a correct disaggregated run must reproduce at any --batch (the
+    decoder plans its attention for the consumer's plan batch)."""
     import torch
     from ..engines.llama_decode import LlamaDecoder, LlamaWeights
     from ..engines.llama_prefill import LlamaPrefill
@@ -190,7 +192,9 @@ def control(args):
     pre = LlamaPrefill(w, max_tokens=frame_tokens(args))
     per = math.ceil((args.max_len + args.max_new) / 16)
     cache = PagedKVCache(cfg.n_layers, per + 1, cfg.n_kv_heads, cfg.head_dim, device="cuda")
-    dec = LlamaDecoder(w, cache, max_batch=1)
+    # The consumer's attention plan (plan_batch), so that a correct run
+    # reproduces these tokens exactly whatever batches it forms.
+    dec = LlamaDecoder(w, cache, max_batch=1, plan_batch=max(args.batch, args.plan_batch))
     S = frame_tokens(args)
     for r in workload(args):
         first, k, v = pre.forward(r["tokens"])
@@ -220,7 +224,8 @@ def _child(role, args, root, env):
            "--seed", str(args.seed), "--requests", str(args.requests),
            "--min-len", str(args.min_len), "--max-len", str(args.max_len),
            "--max-new", str(args.max_new), "--batch", str(args.batch),
-           "--ipc-slots", str(args.ipc_slots), "--layers", str(args.layers or 0)]
+           "--ipc-slots", str(args.ipc_slots), "--layers", str(args.layers or 0),
+           "--plan-batch", str(args.plan_batch)]
     if args.small:
         cmd.append("--small")
     if args.eager:
@@ -349,6 +354,10 @@ def parse(argv=None):
     ap.add_argument("--eager", action="store_true", help="decode without HIP graphs")
     ap.add_argument("--timeout", type=float, default=120.0)
     ap.add_argument("--tokens-out", default=None, help="write each request's tokens (JSON)")
+    ap.add_argument("--plan-batch", type=int, default=16,
+                    help="batch size the decode attention plans its context split for (the "
+                         "consumer and the control use max(--batch, this)): equal values give "
+                         "each request the same tokens whatever batches it shares")
     return ap.parse_args(argv)
 
 

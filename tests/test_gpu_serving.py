@@ -2,12 +2,16 @@
 
 * LlamaPrefill against the oracle (oracle/decode.py, pinned to transformers'
   Llama): the prompt's K/V per layer and the first token.
-* The 2-producer / 1-consumer run (rngd_pd_amd.serving.pd_one_gpu) on a small
-  model: every request completes, and its greedy tokens equal those of a
-  one-process control that prefills and decodes the same prompts with the
-  same weights. At these sizes every kernel's launch plan is the same for 1
-  and 4 streams (one row tile, one column tile, the same attention split
-  count), so continuous batching must not change a single token.
+* The 2-producer / 1-consumer run (rngd_pd_amd.serving.pd_one_gpu): every
+  request completes, and its greedy tokens equal those of a one-process
+  control that prefills and decodes the same prompts with the same weights,
+  one request at a time. The decode step is batch-invariant: every kernel
+  computes a stream's row independently of the others, and attention plans
+  its context split for a fixed plan batch, not for the streams present. So
+  continuous batching, admission order and the handoff must not change a
+  single token. Checked on a small model at widths 1 and 4, and at the
+  Llama-3.1-8B shape (random-init weights, 32 layers) at width 16 with
+  prompts of 128 to 1024 tokens.
 """
 import json
 import os
@@ -92,3 +96,27 @@ def test_two_producers_one_consumer_match_control(tmp_path):
         assert summary["completed"] == 6 and summary["failed"] == 0
         got = json.loads(tok_file.read_text())
         assert got == want, f"batch {batch}: tokens differ from the one-process control"
+
+
+def test_llama8b_two_producers_one_consumer_match_control(tmp_path):
+    """The serving workload's shape: Llama-3.1-8B, two prefill producer processes
+    and one decode consumer at width 16 on this GPU, Poisson arrivals, prompts
+    U[128, 1024]; fewer requests and output tokens than the benchmark run so
+    the control (one request at a time) stays short."""
+    common = ["--requests", "24", "--rate", "40", "--min-len", "128", "--max-len", "1024",
+              "--max-new", "24", "--seed", "5"]
+    out = _run(["control"] + common)
+    want = {}
+    for line in out.splitlines():
+        if line.startswith("{"):
+            ev = json.loads(line)
+            want[ev["req"]] = ev["tokens"]
+    assert len(want) == 24 and all(len(t) == 24 for t in want.values())
+    tok_file = tmp_path / "tokens_8b.json"
+    out = _run(["run", "--batch", "16", "--producers", "2", "--tokens-out", str(tok_file)] + common)
+    summary = json.loads([ln for ln in out.splitlines() if ln.startswith("{")][-1])
+    print(f"llama-8b 2P:1D: {summary}", flush=True)
+    assert summary["completed"] == 24 and summary["failed"] == 0
+    got = json.loads(tok_file.read_text())
+    diff = [r for r in want if got.get(r) != want[r]]
+    assert not diff, f"{len(diff)} requests' tokens differ from the control: {diff[:4]}"
