@@ -82,10 +82,11 @@ typedef struct pdk_pack_req {
   int32_t flags;           /* 0 or PDK_PACK_NARROW                          */
 } pdk_pack_req;
 
-/* Leave frame columns >= P unwritten (except inside the 8-token group that
- * holds column P-1, which is zero-filled). For device-to-device handoffs whose
- * consumer reads only the first P columns; a frame bound for the shm wire
- * needs the zero tail and must not set it. */
+/* Leave the frame's zero tail unwritten: K columns >= min(64 * ceil(P / 64), S)
+ * (K is written in whole 64-token tiles, zeros past P inside the last one, so
+ * every K row ends on a 128-byte line) and V rows >= P. For consumers that
+ * read only the first P columns (the same-GPU scatter), and for frames in
+ * pinned host memory whose tail the host writes (pdk_host_zero_frame_tail). */
 #define PDK_PACK_NARROW 1
 
 /* One request: all L layers in one launch. Requires D % 64 == 0, S % 16 == 0,
@@ -412,9 +413,10 @@ int pdk_stream_probe(int kind, void* dev_dst, const void* dev_src, size_t bytes,
 #define PDK_COPY_H2D 1
 #define PDK_COPY_D2D 2
 
-/* One pack launch per layer l (frame slice l), then done_events[l]. */
-int pdk_pack_kv_layerwise(const pdk_pack_req* req, int n_layers, int S,
-                          int n_kv_heads, int head_dim,
+/* Per layer l: one pack launch of layer l of all n_reqs requests (1..16;
+ * each request's frame slice l), then done_events[l]. */
+int pdk_pack_kv_layerwise(const pdk_pack_req* reqs, int n_reqs, int n_layers,
+                          int S, int n_kv_heads, int head_dim,
                           const uintptr_t* done_events, uintptr_t stream);
 
 /* n_layers copies of layer_bytes at offsets l*layer_bytes: wait
@@ -424,9 +426,20 @@ int pdk_copy_layers(void* dst, const void* src, size_t layer_bytes,
                     int n_layers, int direction, const uintptr_t* wait_events,
                     const uintptr_t* done_events, uintptr_t stream);
 
-/* Wait wait_events[l], then scatter frame layer l into cache layer l. */
-int pdk_scatter_paged_layerwise(const pdk_scatter_req* req, int n_layers,
-                                int S, int n_kv_heads, int head_dim,
+/* Host side of a frame packed narrow (PDK_PACK_NARROW) into pinned memory:
+ * zero what the narrow pack leaves unwritten -- per layer, K rows' columns
+ * [round64(P), S) and V rows [P, S) -- with `threads` host threads (1..64), so
+ * the frame becomes the S-wide wire payload while the host link carries only
+ * the valid columns. Host memory only; no stream, no device work. Replaces
+ * the device-side zero padding of engines/prefill_full.py:378-379 for frames
+ * staged through the host. */
+int pdk_host_zero_frame_tail(uint16_t* frame, int n_layers, int n_kv_heads,
+                             int head_dim, int S, int P, int threads);
+
+/* Per layer l: wait wait_events[l], then one scatter launch of frame slice l
+ * of all n_reqs requests (1..16) into cache layer l. */
+int pdk_scatter_paged_layerwise(const pdk_scatter_req* reqs, int n_reqs,
+                                int n_layers, int S, int n_kv_heads, int head_dim,
                                 uint16_t* cache_k, uint16_t* cache_v,
                                 int64_t cache_layer_stride, int num_blocks,
                                 const uintptr_t* wait_events,

@@ -125,9 +125,10 @@ SIGNATURES = {
     "pdk_ipc_close_mem": (_I, [_P]),
     "pdk_ipc_export_event": (_I, [_U, _P]),
     "pdk_ipc_open_event": (_I, [_P, ctypes.POINTER(_U)]),
-    "pdk_pack_kv_layerwise": (_I, [ctypes.POINTER(PackReq), _I, _I, _I, _I, _P, _U]),
+    "pdk_pack_kv_layerwise": (_I, [ctypes.POINTER(PackReq), _I, _I, _I, _I, _I, _P, _U]),
     "pdk_copy_layers": (_I, [_P, _P, _SZ, _I, _I, _P, _P, _U]),
-    "pdk_scatter_paged_layerwise": (_I, [ctypes.POINTER(ScatterReq), _I, _I, _I, _I, _P, _P,
+    "pdk_host_zero_frame_tail": (_I, [_P, _I, _I, _I, _I, _I, _I]),
+    "pdk_scatter_paged_layerwise": (_I, [ctypes.POINTER(ScatterReq), _I, _I, _I, _I, _I, _P, _P,
                                          _I64, _I, _P, _U]),
 }
 

@@ -19,8 +19,12 @@
 // writes, scatter its frame reads. Scatter's cache-block stores stay ordinary:
 // on 8 Llama-3.1-8B requests (452 MiB scattered right after their pack) they
 // take the scatter from 95 us with streaming stores to 78 us, and the pack
-// that follows is no slower for it; ordinary frame stores in pack instead cost
-// the scatter 8 us. A smaller launch keeps ordinary accesses, so a
+// that follows is no slower for it. Ordinary stores for pack's transposed
+// tiles (the zero tails kept streaming) make the pack itself faster, 142 ->
+// 123 us when packs run back to back, but the write-back they defer lands in
+// whatever runs next: right before the scatter, pack takes 138 us and the
+// scatter 90 instead of 78, so the pair is slower (228 against 224 us) and
+// pack keeps streaming stores. A smaller launch keeps ordinary accesses, so a
 // just-written frame can still be in the cache when its consumer (a copy or
 // the scatter) reads it: one 512-token request packs in 22 us that way and in
 // 28 us streaming.
@@ -52,8 +56,12 @@ struct PackArgs {
   int n_req, S, Hkv, D, nD;
 };
 
-constexpr int kZeroInstr = 16;                    // 16-byte stores per lane per zero chunk
-constexpr int kZeroElems = kZeroInstr * 64 * 8;   // 8192 bf16 = 16 KiB per chunk
+// 16-byte stores per lane per zero chunk: 2 (2 KiB per wavefront, 8 KiB per
+// workgroup). On the 8-request Llama-3.1-8B batch the 311 MB of zero tails
+// take 48 us this way (6.5 TB/s) against 56 us with 16 stores per lane; one
+// store per lane was slower again (160 us for the whole pack against 142).
+constexpr int kZeroInstr = 2;
+constexpr int kZeroElems = kZeroInstr * 64 * 8;   // 1024 bf16 = 2 KiB per chunk
 
 // The all-zero tail of one (layer, head) of a frame: K rows (h, d) columns
 // [Pz, S) and the V block rows t in [Pz, S), flattened into 2 * D * (S - Pz)
@@ -139,8 +147,10 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
     }
   }
   if (t0 >= S) return;           // S % 8 == 0: the lane's 8 tokens are all in or all out
+  // Narrow frames still get whole 64-token tiles of K (zeros past P): a K row
+  // then ends on a 128-byte line, which keeps the stores whole lines when the
+  // frame is in host memory. V rows past P are left unwritten.
   const bool narrow = (R.flags & PDK_PACK_NARROW) != 0;
-  if (narrow && t0 >= P) return;
   uint16_t* fk = R.frame + (int64_t)(2 * l) * F;
   uint16_t* fv = fk + F;
 #pragma unroll

@@ -4,6 +4,11 @@
 // host never becomes the bottleneck of a pipeline whose per-layer device work
 // is a few microseconds (kernels) to ~40 us (2 MiB over the host link).
 
+#include <string.h>
+
+#include <thread>
+#include <vector>
+
 #include "pdk_common.h"
 
 namespace {
@@ -17,22 +22,27 @@ int check_events(const uintptr_t* ev, int n, const char* what) {
 
 }  // namespace
 
-extern "C" int pdk_pack_kv_layerwise(const pdk_pack_req* req, int n_layers, int S, int n_kv_heads,
-                                     int head_dim, const uintptr_t* done_events,
-                                     uintptr_t stream) {
+extern "C" int pdk_pack_kv_layerwise(const pdk_pack_req* reqs, int n_reqs, int n_layers, int S,
+                                     int n_kv_heads, int head_dim,
+                                     const uintptr_t* done_events, uintptr_t stream) {
   pdk::clear_error();
-  PDK_REQUIRE(req != nullptr && n_layers >= 1, "bad arguments");
+  PDK_REQUIRE(reqs != nullptr && n_layers >= 1, "bad arguments");
+  PDK_REQUIRE(n_reqs >= 1 && n_reqs <= PDK_MAX_BATCH, "n_reqs must be in [1, %d] (got %d)",
+              PDK_MAX_BATCH, n_reqs);
   int rc = check_events(done_events, n_layers, "done_events");
   if (rc) return rc;
   const int64_t F = (int64_t)n_kv_heads * head_dim * S;
+  pdk_pack_req layer[PDK_MAX_BATCH];
   for (int l = 0; l < n_layers; ++l) {
-    pdk_pack_req r = *req;
-    if (r.P > 0) {
-      r.src_k += (int64_t)l * req->layer_stride;
-      r.src_v += (int64_t)l * req->layer_stride;
+    for (int i = 0; i < n_reqs; ++i) {
+      layer[i] = reqs[i];
+      if (layer[i].P > 0) {
+        layer[i].src_k += (int64_t)l * reqs[i].layer_stride;
+        layer[i].src_v += (int64_t)l * reqs[i].layer_stride;
+      }
+      layer[i].frame += (int64_t)l * 2 * F;
     }
-    r.frame += (int64_t)l * 2 * F;
-    rc = pdk_pack_kv_batch(&r, 1, 1, S, n_kv_heads, head_dim, stream);
+    rc = pdk_pack_kv_batch(layer, n_reqs, 1, S, n_kv_heads, head_dim, stream);
     if (rc) return rc;
     if (done_events) PDK_TRY_HIP(hipEventRecord(pdk::as_event(done_events[l]), pdk::as_stream(stream)));
   }
@@ -67,27 +77,77 @@ extern "C" int pdk_copy_layers(void* dst, const void* src, size_t layer_bytes, i
   return PDK_OK;
 }
 
-extern "C" int pdk_scatter_paged_layerwise(const pdk_scatter_req* req, int n_layers, int S,
-                                           int n_kv_heads, int head_dim, uint16_t* cache_k,
+extern "C" int pdk_scatter_paged_layerwise(const pdk_scatter_req* reqs, int n_reqs, int n_layers,
+                                           int S, int n_kv_heads, int head_dim, uint16_t* cache_k,
                                            uint16_t* cache_v, int64_t cache_layer_stride,
                                            int num_blocks, const uintptr_t* wait_events,
                                            uintptr_t stream) {
   pdk::clear_error();
-  PDK_REQUIRE(req != nullptr && n_layers >= 1, "bad arguments");
+  PDK_REQUIRE(reqs != nullptr && n_layers >= 1, "bad arguments");
+  PDK_REQUIRE(n_reqs >= 1 && n_reqs <= PDK_MAX_BATCH, "n_reqs must be in [1, %d] (got %d)",
+              PDK_MAX_BATCH, n_reqs);
   PDK_REQUIRE(cache_k && cache_v, "null cache");
   int rc = check_events(wait_events, n_layers, "wait_events");
   if (rc) return rc;
   const int64_t F = (int64_t)n_kv_heads * head_dim * S;
   hipStream_t st = pdk::as_stream(stream);
+  pdk_scatter_req layer[PDK_MAX_BATCH];
   for (int l = 0; l < n_layers; ++l) {
     if (wait_events) PDK_TRY_HIP(hipStreamWaitEvent(st, pdk::as_event(wait_events[l]), 0));
-    pdk_scatter_req r = *req;
-    if (r.frame) r.frame += (int64_t)l * 2 * F;
-    rc = pdk_scatter_paged_batch(&r, 1, 1, S, n_kv_heads, head_dim,
+    for (int i = 0; i < n_reqs; ++i) {
+      layer[i] = reqs[i];
+      if (layer[i].frame) layer[i].frame += (int64_t)l * 2 * F;
+    }
+    rc = pdk_scatter_paged_batch(layer, n_reqs, 1, S, n_kv_heads, head_dim,
                                  cache_k + (int64_t)l * cache_layer_stride,
                                  cache_v + (int64_t)l * cache_layer_stride, cache_layer_stride,
                                  num_blocks, stream);
     if (rc) return rc;
   }
+  return PDK_OK;
+}
+
+// The host's half of a frame packed with PDK_PACK_NARROW into pinned memory:
+// the bytes the narrow pack leaves unwritten, which the S-wide wire frame
+// holds as zeros. Per layer: K rows (Hkv * D of them) from column
+// min(round64(P), S) to S (the narrow pack writes whole 64-token tiles of K),
+// and the V rows t in [P, S) of every head. Layers are spread over `threads`
+// host threads. Host memory takes these zeros at its own bandwidth, so the
+// host link carries only the valid columns.
+extern "C" int pdk_host_zero_frame_tail(uint16_t* frame, int n_layers, int n_kv_heads,
+                                        int head_dim, int S, int P, int threads) {
+  pdk::clear_error();
+  PDK_REQUIRE(frame != nullptr, "frame is null");
+  PDK_REQUIRE(n_layers >= 1 && n_kv_heads >= 1 && head_dim >= 8 && head_dim % 8 == 0,
+              "bad shape (L=%d, Hkv=%d, D=%d)", n_layers, n_kv_heads, head_dim);
+  PDK_REQUIRE(S >= 8 && S % 8 == 0, "S must be a positive multiple of 8 (got %d)", S);
+  PDK_REQUIRE(P >= 0 && P <= S, "P=%d outside [0, S=%d]", P, S);
+  PDK_REQUIRE(threads >= 1 && threads <= 64, "threads must be in [1, 64] (got %d)", threads);
+  const int k0 = ((P + 63) / 64) * 64;         // first K column the narrow pack leaves
+  if (k0 >= S && P >= S) return PDK_OK;
+  const int64_t F = (int64_t)n_kv_heads * head_dim * S;
+  auto layer = [&](int l) {
+    uint16_t* fk = frame + (int64_t)(2 * l) * F;
+    uint16_t* fv = fk + F;
+    if (k0 < S)
+      for (int64_t row = 0; row < (int64_t)n_kv_heads * head_dim; ++row)
+        memset(fk + row * S + k0, 0, (size_t)(S - k0) * 2);
+    if (P < S)
+      for (int h = 0; h < n_kv_heads; ++h)
+        memset(fv + ((int64_t)h * S + P) * head_dim, 0, (size_t)(S - P) * head_dim * 2);
+  };
+  const int nt = threads < n_layers ? threads : n_layers;
+  if (nt == 1) {
+    for (int l = 0; l < n_layers; ++l) layer(l);
+    return PDK_OK;
+  }
+  std::vector<std::thread> pool;
+  pool.reserve(nt - 1);
+  for (int t = 1; t < nt; ++t)
+    pool.emplace_back([&, t] {
+      for (int l = t; l < n_layers; l += nt) layer(l);
+    });
+  for (int l = 0; l < n_layers; l += nt) layer(l);
+  for (auto& th : pool) th.join();
   return PDK_OK;
 }

@@ -8,14 +8,19 @@ HostStagedHandoff does the same for a batch of requests on one GPU, layer by
 layer, with nothing synchronising the host between requests:
 
   mode "kernel" (the default, and the faster one here):
-    save stream   per (request, layer): pack_kernel stores the layer's S-wide
-                  K and V frames straight into the request's pinned host frame
-                  (pinned memory is device-visible, so the kernel's stores are
-                  the device->host leg), then an event;
-    load stream   per (request, layer): wait for that event, then
-                  scatter_kernel reads the layer's valid columns from the pinned
-                  frame (its loads are the host->device leg) and writes the
-                  paged cache blocks.
+    save stream   per layer, one launch for every request: pack_kernel stores
+                  the layer's valid K and V columns (K in whole 64-token
+                  tiles) straight into each request's pinned host frame
+                  (pinned memory is device-visible, so the kernel's stores
+                  are the device->host leg), then an event;
+    host threads  meanwhile write the frame's zero tail (K columns >=
+                  round64(P), V rows >= P) into the same pinned frame
+                  (pdk_host_zero_frame_tail): host memory takes those bytes
+                  at its own bandwidth instead of the link;
+    load stream   per layer, one launch for every request: wait for that
+                  layer's pack event, then scatter_kernel reads the layer's
+                  valid columns from the pinned frames (its loads are the
+                  host->device leg) and writes the paged cache blocks.
   mode "dma":
     the current stream packs into device frames; the DMA engines copy each
     layer to the pinned frame (save stream) and back into a second device
@@ -26,19 +31,23 @@ In both modes the pinned frame of a request ends up holding exactly the wire
 payload of every layer (K [Hkv, D, S] then V [Hkv, S, D], columns >= P zero),
 and the cache holds what pdk_scatter_paged writes from that frame. The caller's
 current stream waits for the last scatter, so work issued after run() sees the
-cache. Measured on MI355X (8 Llama-3.1-8B requests, P uniform in [64, 512]):
-the host link carries about 55 GB/s in total whichever way the bytes go
-(copies both ways at once share it), so "kernel" mode, which crosses it with
-S-wide frames one way and only the valid columns the other, takes 14.9 ms per
-batch; per-layer DMA copies both ways took 35 ms.
+cache; run() returns once the host's part is done.
+
+Measured on MI355X (8 Llama-3.1-8B requests, P uniform in [64, 512]): the
+host link carries about 55 GB/s in total whichever way the bytes go (copies
+both ways at once share it). With the device writing whole S-wide frames
+(537 MB down, 226 MB up) the batch took 14.9 ms; per-layer DMA copies of
+whole frames both ways took 25-35 ms.
 """
 import ctypes
+import os
+import threading
 
 import numpy as np
 import torch
 
 from .. import _lib
-from .._lib import PDK_COPY_D2H, PDK_COPY_H2D, PackReq, ScatterReq
+from .._lib import PDK_COPY_D2H, PDK_COPY_H2D, PDK_PACK_NARROW, PDK_EVENT_SYNC, PackReq, ScatterReq
 from ..hip import EventArray, PinnedBuffer
 from .handoff import _as_layers, _check_cache, _need
 
@@ -49,9 +58,12 @@ class HostStagedHandoff:
     """Pinned host frames for up to ``max_requests`` requests of one model shape."""
 
     def __init__(self, n_layers, n_kv_heads, head_dim, S, max_requests, device=None,
-                 mode="kernel"):
+                 mode="kernel", host_threads=None):
         if mode not in MODES:
             raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
+        if mode == "kernel" and not 1 <= max_requests <= _lib.PDK_MAX_BATCH:
+            raise ValueError(f"kernel mode batches up to {_lib.PDK_MAX_BATCH} requests per "
+                             f"launch; got max_requests={max_requests}")
         self.L, self.H, self.D, self.S = n_layers, n_kv_heads, head_dim, S
         self.max_requests, self.mode = max_requests, mode
         self.device = torch.device(device or "cuda")
@@ -59,7 +71,17 @@ class HostStagedHandoff:
         self.layer_bytes = 2 * self.F * 2
         self.frame_bytes = n_layers * self.layer_bytes
         self.pinned = PinnedBuffer(max_requests * self.frame_bytes)
-        self.ev_save = [EventArray(n_layers) for _ in range(max_requests)]
+        if mode == "kernel":
+            # One event per layer for the whole batch's pack, and one for the
+            # end of the last run's scatters (a later run's host zeros may not
+            # land where those scatters still read).
+            self.ev_layer = EventArray(n_layers)
+            self.ev_read = EventArray(1, PDK_EVENT_SYNC)
+        else:
+            self.ev_save = [EventArray(n_layers) for _ in range(max_requests)]
+            self.ev_read = None
+        self.slot_P = [None] * max_requests
+        self.host_threads = int(host_threads or min(8, os.cpu_count() or 1))
         self.ev_load = [EventArray(n_layers) for _ in range(max_requests)] if mode == "dma" else None
         if mode == "dma":
             shape = (max_requests, n_layers, 2, self.F)
@@ -80,7 +102,7 @@ class HostStagedHandoff:
         return self.pinned.view(np.uint16, r * self.frame_bytes,
                                 self.frame_bytes // 2).reshape(self.L, 2, self.F)
 
-    def _pack_req(self, k, v, P, dst):
+    def _pack_req(self, k, v, P, dst, flags=0):
         _need(k, "k")
         _need(v, "v")
         k, v = _as_layers(k, v)
@@ -89,7 +111,7 @@ class HostStagedHandoff:
                              f"(L={self.L}, Hkv={self.H}, D={self.D})")
         if not 0 <= P <= min(k.shape[1], self.S):
             raise ValueError(f"num_tokens={P} outside [0, min(T={k.shape[1]}, S={self.S})]")
-        return PackReq(k.data_ptr(), v.data_ptr(), dst, k.stride(0), k.stride(1), int(P), 0)
+        return PackReq(k.data_ptr(), v.data_ptr(), dst, k.stride(0), k.stride(1), int(P), flags)
 
     def _scatter_req(self, table, P, src):
         _need(table, "table", torch.int32)
@@ -112,9 +134,10 @@ class HostStagedHandoff:
         cur = torch.cuda.current_stream(self.device)
         L, S, H, D = self.L, self.S, self.H, self.D
         packs, scats = [], []
+        kernel = self.mode == "kernel"
         for r, (k, v, P, table) in enumerate(requests):
-            dst = self.host_ptr(r) if self.mode == "kernel" else self.out_frames[r].data_ptr()
-            packs.append(self._pack_req(k, v, P, dst))
+            dst = self.host_ptr(r) if kernel else self.out_frames[r].data_ptr()
+            packs.append(self._pack_req(k, v, P, dst, PDK_PACK_NARROW if kernel else 0))
             src = self.host_ptr(r) if self.mode == "kernel" else self.in_frames[r].data_ptr()
             scats.append(self._scatter_req(table, P, src))
 
@@ -122,20 +145,53 @@ class HostStagedHandoff:
             if rc:
                 raise _lib.PdkError(rc, what, _lib.last_error())
 
-        if self.mode == "kernel":
-            self.save_stream.wait_stream(cur)
-            self.load_stream.wait_stream(cur)
-            st_save, st_load = self.save_stream.cuda_stream, self.load_stream.cuda_stream
-            for r, pr in enumerate(packs):
-                ok(lib.pdk_pack_kv_layerwise(ctypes.byref(pr), L, S, H, D, self.ev_save[r].ptr,
-                                             st_save), "pdk_pack_kv_layerwise")
-            for r, sr in enumerate(scats):
-                ok(lib.pdk_scatter_paged_layerwise(ctypes.byref(sr), L, S, H, D,
+        n = len(requests)
+        if kernel:
+            # The zero tails, on host threads, while the device packs and
+            # scatters. A slot's new zeros start at its new P: if an earlier,
+            # longer request's scatter may still read that slot there, wait
+            # for the last run's scatters first.
+            lengths = [int(P) for _, _, P, _ in requests]
+            wait = any(self.slot_P[r] is not None and lengths[r] < self.slot_P[r]
+                       for r in range(n))
+            errors = []
+
+            def zero_tails():
+                try:
+                    if wait:
+                        self.ev_read.sync(0)
+                    for r, P in enumerate(lengths):
+                        ok(lib.pdk_host_zero_frame_tail(ctypes.c_void_p(self.host_ptr(r)), L, H,
+                                                        D, S, P, self.host_threads),
+                           "pdk_host_zero_frame_tail")
+                except BaseException as e:      # re-raised on the calling thread
+                    errors.append(e)
+
+            filler = threading.Thread(target=zero_tails, name="kv-zero-tails")
+            filler.start()
+            try:
+                self.save_stream.wait_stream(cur)
+                self.load_stream.wait_stream(cur)
+                # Layer by layer, all requests in one launch each way: 2 L
+                # launches for the batch.
+                ok(lib.pdk_pack_kv_layerwise((PackReq * n)(*packs), n, L, S, H, D,
+                                             self.ev_layer.ptr, self.save_stream.cuda_stream),
+                   "pdk_pack_kv_layerwise")
+                ok(lib.pdk_scatter_paged_layerwise((ScatterReq * n)(*scats), n, L, S, H, D,
                                                    cache_k.data_ptr(), cache_v.data_ptr(),
-                                                   cache_k.stride(0), nb, self.ev_save[r].ptr,
-                                                   st_load), "pdk_scatter_paged_layerwise")
-            cur.wait_stream(self.load_stream)
-            cur.wait_stream(self.save_stream)
+                                                   cache_k.stride(0), nb, self.ev_layer.ptr,
+                                                   self.load_stream.cuda_stream),
+                   "pdk_scatter_paged_layerwise")
+                ok(lib.pdk_event_record(self.ev_read[0], self.load_stream.cuda_stream),
+                   "pdk_event_record")
+                cur.wait_stream(self.load_stream)
+                cur.wait_stream(self.save_stream)
+            finally:
+                filler.join()
+            if errors:
+                raise errors[0]
+            for r, P in enumerate(lengths):
+                self.slot_P[r] = P
             return
         # dma: packs and scatters on the current stream (all packs first, so no
         # pack waits behind a scatter), copies on the two side streams.
@@ -143,7 +199,7 @@ class HostStagedHandoff:
         self.load_stream.wait_stream(cur)
         st = cur.cuda_stream
         for r, pr in enumerate(packs):
-            ok(lib.pdk_pack_kv_layerwise(ctypes.byref(pr), L, S, H, D, self.ev_pack[r].ptr, st),
+            ok(lib.pdk_pack_kv_layerwise(ctypes.byref(pr), 1, L, S, H, D, self.ev_pack[r].ptr, st),
                "pdk_pack_kv_layerwise")
         for r in range(len(requests)):
             ok(lib.pdk_copy_layers(ctypes.c_void_p(self.host_ptr(r)),
@@ -157,7 +213,7 @@ class HostStagedHandoff:
                                    PDK_COPY_H2D, self.ev_save[r].ptr, self.ev_load[r].ptr,
                                    self.load_stream.cuda_stream), "pdk_copy_layers (H2D)")
         for r, sr in enumerate(scats):
-            ok(lib.pdk_scatter_paged_layerwise(ctypes.byref(sr), L, S, H, D, cache_k.data_ptr(),
+            ok(lib.pdk_scatter_paged_layerwise(ctypes.byref(sr), 1, L, S, H, D, cache_k.data_ptr(),
                                                cache_v.data_ptr(), cache_k.stride(0), nb,
                                                self.ev_load[r].ptr, st),
                "pdk_scatter_paged_layerwise")
@@ -165,16 +221,22 @@ class HostStagedHandoff:
         cur.wait_stream(self.load_stream)
 
     def link_bytes(self, lengths):
-        """Bytes one run() moves over the host link: S-wide frames down; up, the
-        valid columns ("kernel": the scatter reads only those) or whole frames ("dma")."""
-        down = len(lengths) * self.frame_bytes
-        per_token = self.L * 2 * self.H * self.D * 2
-        up = sum(lengths) * per_token if self.mode == "kernel" else down
+        """Bytes one run() moves over the host link. "kernel": the valid columns
+        each way (K rows in whole 64-token tiles on the way down); "dma": whole
+        S-wide frames each way."""
+        if self.mode == "dma":
+            return 2 * len(lengths) * self.frame_bytes
+        half = self.L * self.H * self.D * 2              # one token of K (or V), all layers
+        down = sum((min((P + 63) // 64 * 64, self.S) + P) * half for P in lengths)
+        up = sum(2 * P * half for P in lengths)
         return down + up
 
     def close(self):
         torch.cuda.current_stream(self.device).synchronize()
-        for arrs in (self.ev_save, self.ev_load, getattr(self, "ev_pack", None)):
+        if self.ev_read is not None:
+            self.ev_read.close()
+            self.ev_layer.close()
+        for arrs in (getattr(self, "ev_save", None), self.ev_load, getattr(self, "ev_pack", None)):
             for e in arrs or ():
                 e.close()
         self.pinned.close()

@@ -112,3 +112,35 @@ def test_net_library_exports_its_header():
                         ("PDK_NET_EIO", tcp.EIO)):
         assert int(re.search(rf"#define {name}\s+\((-?\d+)\)", raw).group(1)) == value
     assert lib.pdk_tcp_client_open(None, 1, 1.0, None) == -22
+
+
+def test_host_zero_frame_tail_completes_a_narrow_frame():
+    """The host's half of a narrow-packed frame: what the device leaves unwritten
+    (K columns >= round64(P), V rows >= P) becomes zero, nothing else changes,
+    and the frame equals the oracle's S-wide frame. Host memory only."""
+    import ctypes
+    import numpy as np
+    from oracle import native as orc
+    lib = _lib.lib()
+    rng = np.random.default_rng(3)
+    L, H, D, S = 3, 2, 64, 144
+    for P in (0, 1, 7, 8, 9, 63, 64, 65, 79, 129, 143, 144):
+        k = rng.integers(0, 1 << 16, (L, S, H, D), dtype=np.uint16)
+        v = rng.integers(0, 1 << 16, (L, S, H, D), dtype=np.uint16)
+        want = orc.pack_kv(k, v, P, S)
+        frame = want.copy()
+        F = H * D * S
+        kf = frame[:, 0].reshape(L, H * D, S)
+        vf = frame[:, 1].reshape(L, H, S, D)
+        k0 = min((P + 63) // 64 * 64, S)
+        kf[:, :, k0:] = 0xBEEF                        # what the narrow pack leaves
+        vf[:, :, P:, :] = 0xBEEF
+        for threads in (1, 4):
+            f = frame.copy()
+            rc = lib.pdk_host_zero_frame_tail(f.ctypes.data_as(ctypes.c_void_p), L, H, D, S, P,
+                                              threads)
+            assert rc == 0, lib.pdk_last_error()
+            np.testing.assert_array_equal(f, want, err_msg=f"P={P} threads={threads}")
+    bad = np.zeros(16, np.uint16)
+    assert lib.pdk_host_zero_frame_tail(bad.ctypes.data_as(ctypes.c_void_p), 1, 1, 8, 8, 9, 1) \
+        == _lib.PDK_EINVAL

@@ -499,3 +499,64 @@ def test_graph_replays_match_eager(cuda):
         assert rel < 1e-3
         assert torch.equal(dec.tokens[:B], want_tok)
         _ = torch.randn(1000, device=cuda).sum().item()           # eager work between replays
+
+
+def _small_decoder(cuda, n_layers=2, max_batch=8, plan_batch=None, width_blocks=128, seed=21):
+    from rngd_pd_amd.engines.llama_decode import LlamaConfig, LlamaDecoder, LlamaWeights
+    from rngd_pd_amd.engines.paged_cache import PagedKVCache
+    cfg = LlamaConfig(hidden=512, n_heads=8, n_kv_heads=2, head_dim=128, inter=1024,
+                      vocab=1000, n_layers=n_layers)
+    w = LlamaWeights.random(cfg, seed=seed, device=cuda)
+    nb = max_batch * width_blocks + 3
+    cache = PagedKVCache(n_layers, nb, cfg.n_kv_heads, cfg.head_dim, device=cuda)
+    gen = torch.Generator(device=cuda).manual_seed(seed)
+    for li in range(n_layers):
+        cache.k[li].copy_(torch.randn(cache.k[li].shape, generator=gen, device=cuda))
+        cache.v[li].copy_(torch.randn(cache.v[li].shape, generator=gen, device=cuda))
+    perm = np.random.default_rng(seed).permutation(nb)[:max_batch * width_blocks]
+    tables = torch.from_numpy(perm.astype(np.int32).reshape(max_batch, width_blocks)).to(cuda)
+    dec = LlamaDecoder(w, cache, max_batch=max_batch, plan_batch=plan_batch)
+    return cfg, dec, tables
+
+
+def test_batch_invariant_step(cuda):
+    """With a fixed plan batch a stream's step is bit for bit the same alone
+    (B = 1) as in row 3 of a batch of 8, at contexts the attention splits."""
+    cfg, dec, tables = _small_decoder(cuda, max_batch=8)
+    rng = np.random.default_rng(4)
+    ctx = torch.tensor([600, 31, 1200, 777, 5, 2047, 64, 900], dtype=torch.int32, device=cuda)
+    tok = torch.from_numpy(rng.integers(0, cfg.vocab, 8)).to(cuda)
+    max_ctx = tables.shape[1] * 16
+    print("batch invariance: B=8 then row 3 alone", flush=True)
+    dec.step(tok, ctx, tables, max_ctx)
+    torch.cuda.synchronize()
+    want_x, want_tok = dec.x[3].clone(), int(dec.tokens[3])
+    dec.step(tok[3:4], ctx[3:4], tables[3:4].contiguous(), max_ctx)
+    torch.cuda.synchronize()
+    assert torch.equal(dec.x[0].view(torch.int16), want_x.view(torch.int16))
+    assert int(dec.tokens[0]) == want_tok
+
+
+def test_workspace_never_grows_under_a_graph(cuda):
+    """A graph captured where attention needs no workspace keeps no address for
+    one: a later step that would allocate it raises instead of leaving the
+    graph pointing at freed memory; reserve() first makes both work."""
+    cfg, dec, tables = _small_decoder(cuda, max_batch=4)
+    tables = tables[:4].contiguous()
+    B = 4
+    tok = torch.zeros(B, dtype=torch.int64, device=cuda)
+    short = torch.full((B,), 60, dtype=torch.int32, device=cuda)
+    long = torch.full((B,), 2000, dtype=torch.int32, device=cuda)
+    print("workspace under a graph", flush=True)
+    graph = dec.capture(tok, short, tables, 64)
+    graph.replay()
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError, match="reserve"):
+        dec.step(tok, long, tables, 2048)
+    cfg, dec2, tables2 = _small_decoder(cuda, max_batch=4)
+    tables2 = tables2[:4].contiguous()
+    dec2.reserve(2048)
+    graph2 = dec2.capture(tok, short, tables2, 64)
+    dec2.step(tok, long, tables2, 2048)
+    graph2.replay()
+    torch.cuda.synchronize()

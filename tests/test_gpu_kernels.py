@@ -235,7 +235,8 @@ def test_greedy_argmax(cuda, B, V, ld):
 
 
 def test_pack_narrow_leaves_tail(cuda):
-    """PDK_PACK_NARROW writes columns < P (rounded to the 8-token group) and nothing past it."""
+    """PDK_PACK_NARROW writes K in whole 64-token tiles (zeros past P) and V rows < P,
+    and nothing past them."""
     from rngd_pd_amd.kernels import pack_kv_batch, frame_shape
     rng = np.random.default_rng(21)
     L, H, D, S, P = 2, 8, 128, 128, 37
@@ -249,7 +250,7 @@ def test_pack_narrow_leaves_tail(cuda):
     vf = got[:, 1].reshape(L, H, S, D)
     wk = full.reshape(L, 2, -1)[:, 0].reshape(L, H, D, S)
     wv = full.reshape(L, 2, -1)[:, 1].reshape(L, H, S, D)
-    group_end = (P + 7) // 8 * 8
+    group_end = min((P + 63) // 64 * 64, S)
     np.testing.assert_array_equal(kf[..., :group_end], wk[..., :group_end])
     np.testing.assert_array_equal(vf[:, :, :P], wv[:, :, :P])
     three = np.uint16(0x4040)
