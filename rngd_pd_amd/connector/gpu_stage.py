@@ -2,13 +2,15 @@
 
 FrameSaver (prefill side) replaces the download + encode + write of
 engines/prefill_full.py:378-384 and serving/cluster.py:187-218:
-  side stream: wait for the producer's stream -> pack one layer straight into
-  a pinned host slot (device-visible memory: the pack kernel's stores carry the
-  download, with no device staging slot and no copy) -> event;
+  side stream: wait for the producer's stream -> pack one layer's valid
+  columns straight into a pinned host slot (device-visible memory: the pack
+  kernel's stores carry the download, with no device staging slot and no
+  copy) -> event;
   one writer thread, in save order (the reference's single ordered writer):
-  wait for the event -> publish "<req>/<layer>/k" and ".../v" as
-  header + payload + trailer straight from pinned memory (byte-identical to
-  ser() of the same bf16 KV) -> free the slot.
+  wait for the event -> write the frame's zero tail (columns >= P) into the
+  slot on the host, so only valid columns cross the host link -> publish
+  "<req>/<layer>/k" and ".../v" as header + payload + trailer straight from
+  pinned memory (byte-identical to ser() of the same bf16 KV) -> free the slot.
   wait() is the wait_for_save fence: every file of the request is published.
 
 FrameLoader (decode side) replaces wait_for_layer_load's pull + deser + place
@@ -97,9 +99,9 @@ class FrameSaver:
             # GEMM fills the chip. Packing into the pinned slot needs one launch
             # of half as many workgroups and no device slot.
             _h.pack_kv(k, v, num_tokens, self.S, stream=self.stream,
-                       frame_ptr=self.pinned.ptr + slot * self.slot_bytes)
+                       frame_ptr=self.pinned.ptr + slot * self.slot_bytes, narrow=True)
             _lib.call("pdk_event_record", self.events[slot], self.stream.cuda_stream)
-        self._jobs.put((slot, layer_name))
+        self._jobs.put((slot, layer_name, int(num_tokens)))
 
     def _write_loop(self):
         while True:
@@ -107,11 +109,13 @@ class FrameSaver:
             if job is None:
                 self._jobs.task_done()
                 return
-            slot, layer = job
+            slot, layer, P = job
             try:
                 if self._error is None:
                     self.events.sync(slot)
                     base = slot * self.slot_bytes
+                    _lib.call("pdk_host_zero_frame_tail", self.pinned.ptr + base, 1, self.H,
+                              self.D, self.S, P, 1)
                     half = self.F * 2
                     kmv = self.pinned.memoryview(base, half)
                     vmv = self.pinned.memoryview(base + half, half)
