@@ -390,8 +390,10 @@ int pdk_copy_kernel(void* dev_dst, const void* dev_src, size_t bytes,
 /* Streaming probes for the HBM ceilings the handoff kernels are compared with:
  * kind PDK_STREAM_READ reads `bytes` of dev_src, PDK_STREAM_WRITE writes `key`
  * to every word of dev_dst, PDK_STREAM_COPY copies dev_src to dev_dst; 16-byte
- * vectors (bytes % 16 == 0), four in flight per lane over a grid of `blocks`
- * 256-lane workgroups (0: one per 4 KiB, at most 8192). PDK_STREAM_NONTEMPORAL
+ * vectors (bytes % 16 == 0). blocks == 0: one-shot, one vector per lane and
+ * one 256-lane workgroup per 4 KiB (bytes <= 32 GiB); blocks > 0: a grid-stride
+ * loop over that many 256-lane workgroups, four vectors in flight per lane.
+ * PDK_STREAM_NONTEMPORAL
  * asks for streaming (non-temporal) accesses. A read folds what it loads and
  * stores into dev_sink[0..255] only where a fold equals `key` (pick a key no
  * fold is expected to take). No counterpart in the reference: measurement only. */

@@ -224,8 +224,10 @@ _SINKS = {}
 def stream_probe(kind, dst=None, src=None, nbytes=None, nontemporal=False, blocks=0,
                  key=0x9E3779B9, stream=None):
     """One streaming-probe launch: kind "read" (src), "write" (dst) or "copy".
-    A read stores nothing in practice (a word lands in a 1 KiB per-device sink
-    only where its fold equals ``key``)."""
+    blocks=0 is one-shot (one 16-byte vector per lane, a workgroup per 4 KiB);
+    blocks>0 a grid-stride loop over that many workgroups. A read stores
+    nothing in practice (a word lands in a 1 KiB per-device sink only where its
+    fold equals ``key``)."""
     kinds = {"read": _lib.PDK_STREAM_READ, "write": _lib.PDK_STREAM_WRITE,
              "copy": _lib.PDK_STREAM_COPY}
     t = src if src is not None else dst

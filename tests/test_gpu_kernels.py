@@ -344,3 +344,26 @@ def test_streaming_launches_match_cached_launches(cuda):
     got = gather_paged(to_dev(ck), to_dev(cv), torch.from_numpy(t2).to(cuda), 2000, S2)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(to_host(got), orc.gather_paged(ck, cv, t2, 2000, S2))
+
+
+@pytest.mark.parametrize("blocks", [0, 7])
+@pytest.mark.parametrize("nontemporal", [False, True])
+def test_stream_probe_moves_every_vector(cuda, blocks, nontemporal):
+    """The streaming probes behind the HBM ceilings: a copy reproduces its
+    source and a write sets every word, one-shot and grid-stride, including a
+    size that is not a whole number of 4 KiB workgroups."""
+    from rngd_pd_amd.kernels import stream_probe
+    n = (1 << 20) + 48
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.zeros(n + 16, dtype=torch.uint8, device="cuda")
+    stream_probe("copy", dst=dst, src=src, nbytes=n, nontemporal=nontemporal, blocks=blocks)
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:n], src)
+    assert int(dst[n:].sum()) == 0
+    key = 0x01020304
+    stream_probe("write", dst=dst, nbytes=n, nontemporal=nontemporal, blocks=blocks, key=key)
+    stream_probe("read", src=src, nbytes=n, nontemporal=nontemporal, blocks=blocks)
+    torch.cuda.synchronize()
+    words = dst[:n].view(torch.int32)
+    assert bool((words == key).all())
+    assert int(dst[n:].sum()) == 0
