@@ -428,6 +428,17 @@ int pdk_copy_layers(void* dst, const void* src, size_t layer_bytes,
                     int n_layers, int direction, const uintptr_t* wait_events,
                     const uintptr_t* done_events, uintptr_t stream);
 
+/* The valid columns of frame layers [layer0, layer0 + n_layers) -- K rows'
+ * columns [0, min(round64(P), S)) and V rows [0, P) -- copied by the DMA
+ * engines between a device frame and a pinned host frame (dst and src are
+ * frame bases, layer 0), two rectangular copies in all; direction PDK_COPY_D2H
+ * or PDK_COPY_H2D. The device->host and host->device legs of the reference's
+ * download / upload (engines/prefill_full.py:378-384, engines/decode_batch.py:
+ * 305-351) for the bytes that are not padding. P = 0 copies nothing. */
+int pdk_copy_frame_valid(void* dst, const void* src, int layer0, int n_layers,
+                         int n_kv_heads, int head_dim, int S, int P,
+                         int direction, uintptr_t stream);
+
 /* Host side of a frame packed narrow (PDK_PACK_NARROW) into pinned memory:
  * zero what the narrow pack leaves unwritten -- per layer, K rows' columns
  * [round64(P), S) and V rows [P, S) -- with `threads` host threads (1..64), so

@@ -128,6 +128,7 @@ SIGNATURES = {
     "pdk_pack_kv_layerwise": (_I, [ctypes.POINTER(PackReq), _I, _I, _I, _I, _I, _P, _U]),
     "pdk_copy_layers": (_I, [_P, _P, _SZ, _I, _I, _P, _P, _U]),
     "pdk_host_zero_frame_tail": (_I, [_P, _I, _I, _I, _I, _I, _I]),
+    "pdk_copy_frame_valid": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _U]),
     "pdk_scatter_paged_layerwise": (_I, [ctypes.POINTER(ScatterReq), _I, _I, _I, _I, _I, _P, _P,
                                          _I64, _I, _P, _U]),
 }

@@ -6,6 +6,8 @@
 
 #include <string.h>
 
+#include <algorithm>
+
 #include <thread>
 #include <vector>
 
@@ -104,6 +106,57 @@ extern "C" int pdk_scatter_paged_layerwise(const pdk_scatter_req* reqs, int n_re
                                  num_blocks, stream);
     if (rc) return rc;
   }
+  return PDK_OK;
+}
+
+// The valid columns of layers [layer0, layer0 + n_layers) of one frame, copied
+// by the DMA engines in two rectangular copies: K as rows (Hkv * D of them per
+// layer) of the first min(round64(P), S) columns, V as runs (Hkv per layer) of
+// the first P rows of D. Frame layers are 2F elements apart, so a layer is a
+// slice of 2 * Hkv * D K-pitch rows (and of 2 * Hkv V-pitch runs): one 3-D
+// copy covers every layer of the range. Host memory is pinned (hipHostMalloc),
+// so the copies run on the SDMA engines; one engine moves each direction, and
+// a copy down and a copy up on two streams run at once (about 98 GB/s in total
+// on MI355X against 55-57 GB/s for either alone).
+extern "C" int pdk_copy_frame_valid(void* dst, const void* src, int layer0, int n_layers,
+                                    int n_kv_heads, int head_dim, int S, int P, int direction,
+                                    uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(dst && src, "null frame");
+  PDK_REQUIRE(direction == PDK_COPY_D2H || direction == PDK_COPY_H2D, "bad direction %d",
+              direction);
+  PDK_REQUIRE(layer0 >= 0 && n_layers >= 1, "bad layer range [%d, %d + %d)", layer0, layer0,
+              n_layers);
+  PDK_REQUIRE(n_kv_heads >= 1 && head_dim >= 8 && head_dim % 8 == 0,
+              "bad shape (Hkv=%d, D=%d)", n_kv_heads, head_dim);
+  PDK_REQUIRE(S >= 8 && S % 8 == 0, "S must be a positive multiple of 8 (got %d)", S);
+  PDK_REQUIRE(P >= 0 && P <= S, "P=%d outside [0, S=%d]", P, S);
+  if (P == 0) return PDK_OK;
+  const int k1 = std::min(((P + 63) / 64) * 64, S);
+  const size_t e = sizeof(uint16_t);
+  const size_t F = (size_t)n_kv_heads * head_dim * S;
+  const size_t base = (size_t)layer0 * 2 * F * e;
+  const hipMemcpyKind kind = direction == PDK_COPY_D2H ? hipMemcpyDeviceToHost
+                                                       : hipMemcpyHostToDevice;
+  char* d = static_cast<char*>(dst) + base;
+  char* s = const_cast<char*>(static_cast<const char*>(src)) + base;
+  hipStream_t st = pdk::as_stream(stream);
+  // K: rows of S elements; a layer spans 2 * Hkv * D of them.
+  hipMemcpy3DParms k{};
+  const size_t kp = (size_t)S * e, ky = 2 * (size_t)n_kv_heads * head_dim;
+  k.srcPtr = make_hipPitchedPtr(s, kp, kp, ky);
+  k.dstPtr = make_hipPitchedPtr(d, kp, kp, ky);
+  k.extent = make_hipExtent((size_t)k1 * e, (size_t)n_kv_heads * head_dim, (size_t)n_layers);
+  k.kind = kind;
+  PDK_TRY_HIP(hipMemcpy3DAsync(&k, st));
+  // V: runs of S * D elements (one head's [S, D] block); a layer spans 2 * Hkv.
+  hipMemcpy3DParms v{};
+  const size_t vp = (size_t)S * head_dim * e, vy = 2 * (size_t)n_kv_heads;
+  v.srcPtr = make_hipPitchedPtr(s + F * e, vp, vp, vy);
+  v.dstPtr = make_hipPitchedPtr(d + F * e, vp, vp, vy);
+  v.extent = make_hipExtent((size_t)P * head_dim * e, (size_t)n_kv_heads, (size_t)n_layers);
+  v.kind = kind;
+  PDK_TRY_HIP(hipMemcpy3DAsync(&v, st));
   return PDK_OK;
 }
 

@@ -4,10 +4,10 @@ The reference moves every request through host memory: the prefill side pads
 each layer group to S columns and downloads it (engines/prefill_full.py:366-384),
 the wire carries the S-wide frame (connector/transport.py:29-37, 80-101), and the
 decode side uploads and writes it into its cache (engines/decode_batch.py:305-377).
-HostStagedHandoff does the same for a batch of requests on one GPU, layer by
-layer, with nothing synchronising the host between requests:
+HostStagedHandoff does the same for a batch of requests on one GPU, pipelined
+over layers and requests, with nothing synchronising the host between them:
 
-  mode "kernel" (the default, and the faster one here):
+  mode "kernel":
     save stream   per layer, one launch for every request: pack_kernel stores
                   the layer's valid K and V columns (K in whole 64-token
                   tiles) straight into each request's pinned host frame
@@ -21,11 +21,21 @@ layer, with nothing synchronising the host between requests:
                   layer's pack event, then scatter_kernel reads the layer's
                   valid columns from the pinned frames (its loads are the
                   host->device leg) and writes the paged cache blocks.
-  mode "dma":
-    the current stream packs into device frames; the DMA engines copy each
-    layer to the pinned frame (save stream) and back into a second device
-    frame (load stream); the current stream scatters from it. This is the
-    reference's download / upload shape with copy engines.
+  mode "dma" (the default, and the faster one here):
+    current stream  per request, one narrow pack into a device frame (all
+                    layers), then an event;
+    save stream     per request, after its pack: the DMA engine copies the
+                    valid columns down into the pinned frame, a few layers
+                    per copy (two rectangular copies each: K rows, V runs),
+                    an event after each;
+    load stream     after each of those copies, the same layers' valid
+                    columns back up into a second device frame (the other
+                    DMA engine);
+    current stream  per request, after its last upload: one scatter launch
+                    (all layers) into the paged cache;
+    host threads    the frames' zero tails, as in "kernel" mode.
+    This is the reference's download / upload shape with copy engines, minus
+    the padding: each direction has an engine of its own and no CU is used.
 
 In both modes the pinned frame of a request ends up holding exactly the wire
 payload of every layer (K [Hkv, D, S] then V [Hkv, S, D], columns >= P zero),
@@ -33,11 +43,15 @@ and the cache holds what pdk_scatter_paged writes from that frame. The caller's
 current stream waits for the last scatter, so work issued after run() sees the
 cache; run() returns once the host's part is done.
 
-Measured on MI355X (8 Llama-3.1-8B requests, P uniform in [64, 512]): the
-host link carries about 55 GB/s in total whichever way the bytes go (copies
-both ways at once share it). With the device writing whole S-wide frames
-(537 MB down, 226 MB up) the batch took 14.9 ms; per-layer DMA copies of
-whole frames both ways took 25-35 ms.
+Measured on MI355X: one direction alone moves 53-57 GB/s, by a kernel's
+loads or stores through pinned memory or by a DMA engine. Both directions at
+once reach about 98 GB/s in total with one DMA engine each way, 77-87 GB/s
+with a kernel on either side. On 8 Llama-3.1-8B requests (P uniform in
+[64, 512], 486 MB over the link) "dma" mode takes 6.0 ms (80 GB/s of link
+traffic) and "kernel" mode, whose pack and scatter kernels overlap layer by
+layer, 9.5 ms (50 GB/s). Each DMA copy costs about 10 us besides its bytes,
+so "dma" mode copies several layers per command (``copy_bytes`` of valid
+columns, 16 MiB by default).
 """
 import ctypes
 import os
@@ -58,7 +72,7 @@ class HostStagedHandoff:
     """Pinned host frames for up to ``max_requests`` requests of one model shape."""
 
     def __init__(self, n_layers, n_kv_heads, head_dim, S, max_requests, device=None,
-                 mode="kernel", host_threads=None):
+                 mode="dma", host_threads=None, copy_bytes=16 << 20):
         if mode not in MODES:
             raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
         if mode == "kernel" and not 1 <= max_requests <= _lib.PDK_MAX_BATCH:
@@ -78,16 +92,20 @@ class HostStagedHandoff:
             self.ev_layer = EventArray(n_layers)
             self.ev_read = EventArray(1, PDK_EVENT_SYNC)
         else:
-            self.ev_save = [EventArray(n_layers) for _ in range(max_requests)]
-            self.ev_read = None
-        self.slot_P = [None] * max_requests
-        self.host_threads = int(host_threads or min(8, os.cpu_count() or 1))
-        self.ev_load = [EventArray(n_layers) for _ in range(max_requests)] if mode == "dma" else None
-        if mode == "dma":
+            # Per request: its pack, each of its down copies (at most one per
+            # layer), its last up copy; and the run's last up copy.
+            self.ev_pack = EventArray(max_requests)
+            self.ev_down = EventArray(max_requests * n_layers)
+            self.ev_up = EventArray(max_requests)
+            self.ev_read = EventArray(1, PDK_EVENT_SYNC)
             shape = (max_requests, n_layers, 2, self.F)
             self.out_frames = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
             self.in_frames = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
-            self.ev_pack = [EventArray(n_layers) for _ in range(max_requests)]
+        if copy_bytes < 1:
+            raise ValueError(f"copy_bytes must be positive, got {copy_bytes}")
+        self.copy_bytes = int(copy_bytes)
+        self.slot_P = [None] * max_requests
+        self.host_threads = int(host_threads or min(8, os.cpu_count() or 1))
         # Two side streams per process at most (the hardware has four queues
         # per process, and the caller's stream is a third).
         from ..connector.gpu_stage import side_stream
@@ -137,7 +155,7 @@ class HostStagedHandoff:
         kernel = self.mode == "kernel"
         for r, (k, v, P, table) in enumerate(requests):
             dst = self.host_ptr(r) if kernel else self.out_frames[r].data_ptr()
-            packs.append(self._pack_req(k, v, P, dst, PDK_PACK_NARROW if kernel else 0))
+            packs.append(self._pack_req(k, v, P, dst, PDK_PACK_NARROW))
             src = self.host_ptr(r) if self.mode == "kernel" else self.in_frames[r].data_ptr()
             scats.append(self._scatter_req(table, P, src))
 
@@ -146,97 +164,129 @@ class HostStagedHandoff:
                 raise _lib.PdkError(rc, what, _lib.last_error())
 
         n = len(requests)
-        if kernel:
-            # The zero tails, on host threads, while the device packs and
-            # scatters. A slot's new zeros start at its new P: if an earlier,
-            # longer request's scatter may still read that slot there, wait
-            # for the last run's scatters first.
-            lengths = [int(P) for _, _, P, _ in requests]
-            wait = any(self.slot_P[r] is not None and lengths[r] < self.slot_P[r]
-                       for r in range(n))
-            errors = []
+        # The zero tails, on host threads, while the device packs and
+        # scatters. A slot's new zeros start at its new P: if an earlier,
+        # longer request's upload may still read that slot there, wait for
+        # the last run's uploads first.
+        lengths = [int(P) for _, _, P, _ in requests]
+        wait = any(self.slot_P[r] is not None and lengths[r] < self.slot_P[r] for r in range(n))
+        errors = []
 
-            def zero_tails():
-                try:
-                    if wait:
-                        self.ev_read.sync(0)
-                    for r, P in enumerate(lengths):
-                        ok(lib.pdk_host_zero_frame_tail(ctypes.c_void_p(self.host_ptr(r)), L, H,
-                                                        D, S, P, self.host_threads),
-                           "pdk_host_zero_frame_tail")
-                except BaseException as e:      # re-raised on the calling thread
-                    errors.append(e)
-
-            filler = threading.Thread(target=zero_tails, name="kv-zero-tails")
-            filler.start()
+        def zero_tails():
             try:
-                self.save_stream.wait_stream(cur)
-                self.load_stream.wait_stream(cur)
-                # Layer by layer, all requests in one launch each way: 2 L
-                # launches for the batch.
-                ok(lib.pdk_pack_kv_layerwise((PackReq * n)(*packs), n, L, S, H, D,
-                                             self.ev_layer.ptr, self.save_stream.cuda_stream),
-                   "pdk_pack_kv_layerwise")
-                ok(lib.pdk_scatter_paged_layerwise((ScatterReq * n)(*scats), n, L, S, H, D,
-                                                   cache_k.data_ptr(), cache_v.data_ptr(),
-                                                   cache_k.stride(0), nb, self.ev_layer.ptr,
-                                                   self.load_stream.cuda_stream),
-                   "pdk_scatter_paged_layerwise")
-                ok(lib.pdk_event_record(self.ev_read[0], self.load_stream.cuda_stream),
-                   "pdk_event_record")
-                cur.wait_stream(self.load_stream)
-                cur.wait_stream(self.save_stream)
-            finally:
-                filler.join()
-            if errors:
-                raise errors[0]
-            for r, P in enumerate(lengths):
-                self.slot_P[r] = P
-            return
-        # dma: packs and scatters on the current stream (all packs first, so no
-        # pack waits behind a scatter), copies on the two side streams.
-        self.save_stream.wait_stream(cur)
-        self.load_stream.wait_stream(cur)
-        st = cur.cuda_stream
+                if wait:
+                    self.ev_read.sync(0)
+                for r, P in enumerate(lengths):
+                    ok(lib.pdk_host_zero_frame_tail(ctypes.c_void_p(self.host_ptr(r)), L, H, D, S,
+                                                    P, self.host_threads),
+                       "pdk_host_zero_frame_tail")
+            except BaseException as e:      # re-raised on the calling thread
+                errors.append(e)
+
+        filler = threading.Thread(target=zero_tails, name="kv-zero-tails")
+        filler.start()
+        try:
+            self.save_stream.wait_stream(cur)
+            self.load_stream.wait_stream(cur)
+            if kernel:
+                self._run_kernel(lib, ok, packs, scats, cache_k, cache_v, nb)
+            else:
+                self._run_dma(lib, ok, packs, scats, lengths, cache_k, cache_v, nb, cur)
+            cur.wait_stream(self.load_stream)
+            cur.wait_stream(self.save_stream)
+        finally:
+            filler.join()
+        if errors:
+            raise errors[0]
+        for r, P in enumerate(lengths):
+            self.slot_P[r] = P
+
+    def _run_kernel(self, lib, ok, packs, scats, cache_k, cache_v, nb):
+        # Layer by layer, all requests in one launch each way: 2 L launches
+        # for the batch.
+        L, S, H, D, n = self.L, self.S, self.H, self.D, len(packs)
+        ok(lib.pdk_pack_kv_layerwise((PackReq * n)(*packs), n, L, S, H, D, self.ev_layer.ptr,
+                                     self.save_stream.cuda_stream), "pdk_pack_kv_layerwise")
+        ok(lib.pdk_scatter_paged_layerwise((ScatterReq * n)(*scats), n, L, S, H, D,
+                                           cache_k.data_ptr(), cache_v.data_ptr(),
+                                           cache_k.stride(0), nb, self.ev_layer.ptr,
+                                           self.load_stream.cuda_stream),
+           "pdk_scatter_paged_layerwise")
+        ok(lib.pdk_event_record(self.ev_read[0], self.load_stream.cuda_stream),
+           "pdk_event_record")
+
+    def layer_chunks(self, P, ramp_up=False, ramp_down=False):
+        """(first layer, layers) of each DMA copy of a request of P tokens:
+        about ``copy_bytes`` of valid columns per copy. With ``ramp_up`` the
+        copies start at 1, 2 and 4 layers (the first request of a run: its
+        first upload can start sooner); with ``ramp_down`` they end at 4, 2
+        and 1 (the last request: less upload left once the last download is
+        done)."""
+        k1 = min((P + 63) // 64 * 64, self.S)
+        per_layer = max(1, (k1 + P) * self.H * self.D * 2)
+        n = max(1, min(self.L, self.copy_bytes // per_layer))
+        ramp = [m for m in (1, 2, 4) if m < n]
+        sizes, left = [], self.L
+        head = ramp if ramp_up else []
+        tail = ramp[::-1] if ramp_down else []
+        for m in head:
+            if left - m < sum(tail):
+                break
+            sizes.append(m)
+            left -= m
+        mid = left - sum(tail)
+        if mid < 0:                       # too few layers for both ramps
+            tail, mid = [], left
+        k = -(-mid // n)                  # copies of at most n layers, sizes within one
+        sizes += [mid // k + (1 if i < mid % k else 0) for i in range(k)]
+        sizes += tail
+        out, l0 = [], 0
+        for m in sizes:
+            out.append((l0, m))
+            l0 += m
+        return out
+
+    def _run_dma(self, lib, ok, packs, scats, lengths, cache_k, cache_v, nb, cur):
+        L, S, H, D = self.L, self.S, self.H, self.D
+        st, save, load = cur.cuda_stream, self.save_stream.cuda_stream, self.load_stream.cuda_stream
         for r, pr in enumerate(packs):
-            ok(lib.pdk_pack_kv_layerwise(ctypes.byref(pr), 1, L, S, H, D, self.ev_pack[r].ptr, st),
-               "pdk_pack_kv_layerwise")
-        for r in range(len(requests)):
-            ok(lib.pdk_copy_layers(ctypes.c_void_p(self.host_ptr(r)),
-                                   ctypes.c_void_p(self.out_frames[r].data_ptr()),
-                                   self.layer_bytes, L, PDK_COPY_D2H, self.ev_pack[r].ptr,
-                                   self.ev_save[r].ptr, self.save_stream.cuda_stream),
-               "pdk_copy_layers (D2H)")
-        for r in range(len(requests)):
-            ok(lib.pdk_copy_layers(ctypes.c_void_p(self.in_frames[r].data_ptr()),
-                                   ctypes.c_void_p(self.host_ptr(r)), self.layer_bytes, L,
-                                   PDK_COPY_H2D, self.ev_save[r].ptr, self.ev_load[r].ptr,
-                                   self.load_stream.cuda_stream), "pdk_copy_layers (H2D)")
+            ok(lib.pdk_pack_kv_batch(ctypes.byref(pr), 1, L, S, H, D, st), "pdk_pack_kv_batch")
+            ok(lib.pdk_event_record(self.ev_pack[r], st), "pdk_event_record")
+        for r, P in enumerate(lengths):
+            out_f, in_f, host = (self.out_frames[r].data_ptr(), self.in_frames[r].data_ptr(),
+                                 ctypes.c_void_p(self.host_ptr(r)))
+            ok(lib.pdk_stream_wait_event(save, self.ev_pack[r]), "pdk_stream_wait_event")
+            chunks = self.layer_chunks(P, ramp_up=r == 0, ramp_down=r == len(lengths) - 1)
+            for c, (l0, nl) in enumerate(chunks):
+                ev = self.ev_down[r * L + c]
+                ok(lib.pdk_copy_frame_valid(host, ctypes.c_void_p(out_f), l0, nl, H, D, S, P,
+                                            PDK_COPY_D2H, save), "pdk_copy_frame_valid (down)")
+                ok(lib.pdk_event_record(ev, save), "pdk_event_record")
+                ok(lib.pdk_stream_wait_event(load, ev), "pdk_stream_wait_event")
+                ok(lib.pdk_copy_frame_valid(ctypes.c_void_p(in_f), host, l0, nl, H, D, S, P,
+                                            PDK_COPY_H2D, load), "pdk_copy_frame_valid (up)")
+            ok(lib.pdk_event_record(self.ev_up[r], load), "pdk_event_record")
+        ok(lib.pdk_event_record(self.ev_read[0], load), "pdk_event_record")
         for r, sr in enumerate(scats):
-            ok(lib.pdk_scatter_paged_layerwise(ctypes.byref(sr), 1, L, S, H, D, cache_k.data_ptr(),
-                                               cache_v.data_ptr(), cache_k.stride(0), nb,
-                                               self.ev_load[r].ptr, st),
-               "pdk_scatter_paged_layerwise")
-        cur.wait_stream(self.save_stream)
-        cur.wait_stream(self.load_stream)
+            ok(lib.pdk_stream_wait_event(st, self.ev_up[r]), "pdk_stream_wait_event")
+            ok(lib.pdk_scatter_paged_batch(ctypes.byref(sr), 1, L, S, H, D, cache_k.data_ptr(),
+                                           cache_v.data_ptr(), cache_k.stride(0), nb, st),
+               "pdk_scatter_paged_batch")
 
     def link_bytes(self, lengths):
-        """Bytes one run() moves over the host link. "kernel": the valid columns
-        each way (K rows in whole 64-token tiles on the way down); "dma": whole
-        S-wide frames each way."""
-        if self.mode == "dma":
-            return 2 * len(lengths) * self.frame_bytes
+        """Bytes one run() moves over the host link: the valid columns each way
+        (K rows in whole 64-token tiles, V rows < P) in "dma" mode; the same
+        on the way up in "kernel" mode, whose scatter loads only columns < P."""
         half = self.L * self.H * self.D * 2              # one token of K (or V), all layers
         down = sum((min((P + 63) // 64 * 64, self.S) + P) * half for P in lengths)
-        up = sum(2 * P * half for P in lengths)
-        return down + up
+        if self.mode == "dma":
+            return 2 * down
+        return down + sum(2 * P * half for P in lengths)
 
     def close(self):
         torch.cuda.current_stream(self.device).synchronize()
-        if self.ev_read is not None:
-            self.ev_read.close()
-            self.ev_layer.close()
-        for arrs in (getattr(self, "ev_save", None), self.ev_load, getattr(self, "ev_pack", None)):
-            for e in arrs or ():
-                e.close()
+        for name in ("ev_layer", "ev_read", "ev_pack", "ev_down", "ev_up"):
+            arr = getattr(self, name, None)
+            if arr is not None:
+                arr.close()
         self.pinned.close()

@@ -76,12 +76,22 @@ def test_staged_batch_matches_oracle(cuda, mode):
         stager.close()
 
 
-def test_staged_edge_lengths(cuda):
-    """P = 0 (nothing to place, frame all zero), 1, 16, 17 and S in one batch."""
+@pytest.mark.parametrize("mode,copy_bytes", [("kernel", None), ("dma", 16 << 20),
+                                             ("dma", 1 << 20)])
+def test_staged_edge_lengths(cuda, mode, copy_bytes):
+    """P = 0 (nothing to place, frame all zero), 1, 16, 17 and S in one batch;
+    "dma" mode also with copies of about 1 MiB (several per request)."""
     from rngd_pd_amd.kernels.staging import HostStagedHandoff
     lengths = [0, 1, 16, 17, S]
     nb = sum((p + 15) // 16 for p in lengths) + 4
-    stager = HostStagedHandoff(L, H, D, S, len(lengths), device=cuda)
+    kw = {} if copy_bytes is None else {"copy_bytes": copy_bytes}
+    stager = HostStagedHandoff(L, H, D, S, len(lengths), device=cuda, mode=mode, **kw)
+    if mode == "dma":
+        # A full-length request has 2 MiB of valid columns per layer.
+        per_copy = max(1, min(L, copy_bytes // (2 * S * H * D * 2)))
+        chunks = stager.layer_chunks(S)
+        assert [l0 for l0, _ in chunks] == list(range(0, L, per_copy))
+        assert sum(n for _, n in chunks) == L
     try:
         reqs = _batch(np.random.default_rng(5), lengths, nb, cuda)
         reqs[0] = (reqs[0][0], np.zeros(1, np.int32), 0)
