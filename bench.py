@@ -621,11 +621,16 @@ def bench_serve(args, out):
     GPU (same-GPU IPC handoff, continuous batching at width 16), 64 requests
     with Poisson(20/s) arrivals, prompts U[128,1024], 128 greedy tokens each,
     random-init Llama-3.1-8B weights. Runs rngd_pd_amd.serving.pd_one_gpu as a
-    child process and records its summary."""
+    child process and records its summary: three passes of the same seeded
+    workload on the same processes (the first pass's figures at the top level,
+    every pass under "passes", the spread under "across_passes"), each with its
+    decode steps grouped by how many prefills overlapped them and its time to
+    first token split into queueing and prefill."""
     import subprocess
     cmd = [sys.executable, "-u", "-m", "rngd_pd_amd.serving.pd_one_gpu", "run",
            "--requests", "64", "--rate", "20", "--min-len", "128", "--max-len", "1024",
-           "--max-new", "128", "--batch", "16", "--producers", "2", "--seed", "0"]
+           "--max-new", "128", "--batch", "16", "--producers", "2", "--seed", "0",
+           "--repeats", "3"]
     log("serve: " + " ".join(cmd[3:]))
     r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=900,
                        cwd=os.path.dirname(os.path.abspath(__file__)))
@@ -633,7 +638,11 @@ def bench_serve(args, out):
         raise RuntimeError(f"pd_one_gpu exited with {r.returncode}")
     summary = json.loads([ln for ln in r.stdout.splitlines() if ln.startswith("{")][-1])
     out["extra"]["pd_one_gpu"] = summary
-    log(f"serve: {summary}")
+    for i, p in enumerate(summary.get("passes", [summary])):
+        log(f"serve pass {i}: {p['output_tokens_per_s']} tok/s, TTFT p50 {p['ttft_ms']['p50']} ms "
+            f"(queued {p['ttft_parts_ms']['queued_p50']}, prefill {p['ttft_parts_ms']['prefill_p50']}), "
+            f"TPOT p50/p90 {p['tpot_ms']['p50']}/{p['tpot_ms']['p90']} ms, steps by overlapping "
+            f"prefills {p['decode_steps_by_overlapping_prefills']}")
 
 
 def bench_long(args, torch, dev, out, n_req=16, T=2048, hidden=4096):

@@ -57,17 +57,20 @@ def frame_tokens(args):
     return (args.max_len + 15) // 16 * 16
 
 
-def workload(args):
+def workload(args, rep=0):
     """Seeded arrivals (exponential gaps at ``rate``/s), prompt lengths
-    U[min_len, max_len] and prompt token ids U[0, vocab)."""
+    U[min_len, max_len] and prompt token ids U[0, vocab). Every pass of a run
+    replays the same workload under request ids of its own."""
     import numpy as np
     rng = np.random.default_rng(args.seed)
     vocab = model_config(args).vocab
     t, out = 0.0, []
+    prefix = "q" if rep == 0 else f"r{rep}q"
     for i in range(args.requests):
         t += float(rng.exponential(1.0 / args.rate))
         n = int(rng.integers(args.min_len, args.max_len + 1))
-        out.append({"req": f"q{i}", "arrival": t, "tokens": rng.integers(0, vocab, n).tolist()})
+        out.append({"req": f"{prefix}{i}", "arrival": t,
+                    "tokens": rng.integers(0, vocab, n).tolist()})
     return out
 
 
@@ -106,8 +109,8 @@ def producer(args):
                                                                  num_tokens=T))
         conn.wait_for_save()
         conn.close()
-        _say({"ev": "prefilled", "req": req, "first": first, "P": T, "t": time.monotonic(),
-              "prefill_ms": round((time.monotonic() - t0) * 1e3, 2)})
+        _say({"ev": "prefilled", "req": req, "first": first, "P": T, "t0": t0,
+              "t": time.monotonic(), "prefill_ms": round((time.monotonic() - t0) * 1e3, 2)})
     t.close()
     _say({"ev": "exit", "role": "producer"})
 
@@ -161,6 +164,10 @@ def consumer(args):
         msg = json.loads(line)
         if msg.get("cmd") == "stop":
             break
+        if msg.get("cmd") == "steplog":
+            _say({"ev": "steplog", "steps": [[round(t, 6), round(d, 3), b]
+                                             for t, d, b in sched.take_step_log()]})
+            continue
         item = sched.submit_async({"req_id": msg["req"], "first": msg["first"], "P": msg["P"],
                                    "max_new": msg["max_new"]})
         th = threading.Thread(target=watch, args=(item,), daemon=True)
@@ -242,8 +249,113 @@ def _pump(name, proc, events):
     events.put((name, {"ev": "eof"}))
 
 
+def _pct(xs, q):
+    xs = sorted(xs)
+    return xs[min(len(xs) - 1, int(q * len(xs)))] if xs else None
+
+
+def contention(steps, prefills, t0, t_end):
+    """What the decode steps of one pass shared the GPU with.
+
+    steps: [(start s, ms, streams)] from the consumer; prefills: [(start s,
+    end s)] from the producers (one clock: CLOCK_MONOTONIC, system-wide).
+    Steps are grouped by how many prefills overlapped them; for each group the
+    count and the step-time p50 / p90 (the decode step is one HIP-graph replay,
+    so its time is the GPU's answer to what else was running)."""
+    out = {}
+    for t, ms, b in steps:
+        if not t0 <= t <= t_end:
+            continue
+        e = t + ms / 1e3
+        k = sum(1 for a, z in prefills if a < e and z > t)
+        out.setdefault(k, []).append(ms)
+    return {f"{k}_prefills": {"steps": len(v), "step_ms_p50": round(_pct(v, 0.5), 3),
+                              "step_ms_p90": round(_pct(v, 0.9), 3)}
+            for k, v in sorted(out.items())}
+
+
+def _pass(args, rep, procs, names, events):
+    """Feed one pass of the workload at its arrival times and collect it."""
+    work = workload(args, rep)
+    results, firsts, failed = {}, {}, []
+    t0 = time.monotonic()
+    arrivals = {r["req"]: t0 + r["arrival"] for r in work}
+    nxt = 0
+    while len(results) + len(failed) < len(work):
+        now = time.monotonic()
+        while nxt < len(work) and arrivals[work[nxt]["req"]] <= now:
+            r = work[nxt]
+            p = procs[names[1 + nxt % args.producers]]
+            p.stdin.write(json.dumps({"cmd": "prefill", "req": r["req"],
+                                      "tokens": r["tokens"]}) + "\n")
+            p.stdin.flush()
+            nxt += 1
+        wait = (arrivals[work[nxt]["req"]] - time.monotonic()) if nxt < len(work) else 1.0
+        try:
+            n, ev = events.get(timeout=max(0.0005, min(wait, 1.0)))
+        except queue.Empty:
+            continue
+        if ev["ev"] == "prefilled":
+            firsts[ev["req"]] = ev
+            procs["consumer"].stdin.write(json.dumps({
+                "cmd": "decode", "req": ev["req"], "first": ev["first"], "P": ev["P"],
+                "max_new": args.max_new}) + "\n")
+            procs["consumer"].stdin.flush()
+        elif ev["ev"] == "done":
+            results[ev["req"]] = ev
+        elif ev["ev"] == "failed":
+            failed.append(ev)
+            _log(f"failed: {ev}")
+        elif ev["ev"] == "eof":
+            raise RuntimeError(f"{n} exited during the run")
+    t_end = time.monotonic()
+    procs["consumer"].stdin.write(json.dumps({"cmd": "steplog"}) + "\n")
+    procs["consumer"].stdin.flush()
+    while True:
+        n, ev = events.get(timeout=args.timeout)
+        if ev["ev"] == "steplog":
+            steps = ev["steps"]
+            break
+        if ev["ev"] == "eof":
+            raise RuntimeError(f"{n} exited during the run")
+    ttft = [(firsts[r]["t"] - arrivals[r]) * 1e3 for r in results]
+    queued = [(firsts[r]["t0"] - arrivals[r]) * 1e3 for r in results]
+    e2e = [(results[r]["t"] - arrivals[r]) * 1e3 for r in results]
+    tpot = [results[r]["tpot_ms"] for r in results]
+    step_ms = [ms for t, ms, b in steps if t0 <= t <= t_end]
+    n_tok = sum(len(results[r]["tokens"]) for r in results)
+    summary = {
+        "requests": len(work), "completed": len(results), "failed": len(failed),
+        "output_tokens": n_tok, "makespan_s": round(t_end - t0, 3),
+        "output_tokens_per_s": round(n_tok / (t_end - t0), 1),
+        "ttft_ms": {"p50": round(_pct(ttft, 0.5), 1), "p90": round(_pct(ttft, 0.9), 1),
+                    "max": round(max(ttft), 1)},
+        "e2e_ms": {"p50": round(_pct(e2e, 0.5), 1), "p90": round(_pct(e2e, 0.9), 1),
+                   "max": round(max(e2e), 1)},
+        "tpot_ms": {"p50": round(_pct(tpot, 0.5), 3), "p90": round(_pct(tpot, 0.9), 3)},
+        "prefill_ms_p50": round(_pct([f["prefill_ms"] for f in firsts.values()], 0.5), 1),
+        "load_ms_p50": round(_pct([results[r]["load_ms"] for r in results], 0.5), 2),
+        "occupancy_p50": _pct([results[r]["occupancy"] for r in results], 0.5),
+        "producers": args.producers, "batch_width": args.batch,
+        # Where the time to first token goes: waiting for a producer (its
+        # earlier prompts) and the prefill itself.
+        "ttft_parts_ms": {
+            "queued_p50": round(_pct(queued, 0.5), 1), "queued_p90": round(_pct(queued, 0.9), 1),
+            "prefill_p50": round(_pct([f["prefill_ms"] for f in firsts.values()], 0.5), 1),
+            "prefill_p90": round(_pct([f["prefill_ms"] for f in firsts.values()], 0.9), 1)},
+        "decode_step_ms": {"steps": len(step_ms), "p50": round(_pct(step_ms, 0.5), 3),
+                           "p90": round(_pct(step_ms, 0.9), 3),
+                           "p99": round(_pct(step_ms, 0.99), 3), "max": round(max(step_ms), 3)}
+        if step_ms else {},
+        "decode_steps_by_overlapping_prefills": contention(
+            steps, [(f["t0"], f["t"]) for f in firsts.values()], t0, t_end),
+    }
+    return summary, {r: results[r]["tokens"] for r in results}
+
+
 def run(args):
-    """Start the children, feed the workload at its arrival times, collect results."""
+    """Start the children, feed the workload at its arrival times (``repeats``
+    passes, each with request ids of its own), collect results."""
     root = tempfile.mkdtemp(prefix="pd1gpu-", dir="/dev/shm" if os.path.isdir("/dev/shm") else None)
     env = dict(os.environ, PD_SHM_ROOT=root, PD_KV_PULL_TIMEOUT=str(args.timeout),
                PYTHONPATH=os.path.dirname(os.path.dirname(os.path.dirname(
@@ -254,7 +366,7 @@ def run(args):
              for n in names}
     for n, p in procs.items():
         threading.Thread(target=_pump, args=(n, p, events), daemon=True).start()
-    results, firsts, failed = {}, {}, []
+    passes, tokens = [], {}
     try:
         ready = set()
         deadline = time.monotonic() + args.timeout * 4
@@ -265,38 +377,12 @@ def run(args):
                 _log(f"{n} ready")
             elif ev["ev"] == "eof":
                 raise RuntimeError(f"{n} exited before it was ready")
-        work = workload(args)
-        t0 = time.monotonic()
-        arrivals = {r["req"]: t0 + r["arrival"] for r in work}
-        nxt = 0
-        while len(results) + len(failed) < len(work):
-            now = time.monotonic()
-            while nxt < len(work) and arrivals[work[nxt]["req"]] <= now:
-                r = work[nxt]
-                p = procs[names[1 + nxt % args.producers]]
-                p.stdin.write(json.dumps({"cmd": "prefill", "req": r["req"],
-                                          "tokens": r["tokens"]}) + "\n")
-                p.stdin.flush()
-                nxt += 1
-            wait = (arrivals[work[nxt]["req"]] - time.monotonic()) if nxt < len(work) else 1.0
-            try:
-                n, ev = events.get(timeout=max(0.0005, min(wait, 1.0)))
-            except queue.Empty:
-                continue
-            if ev["ev"] == "prefilled":
-                firsts[ev["req"]] = ev
-                procs["consumer"].stdin.write(json.dumps({
-                    "cmd": "decode", "req": ev["req"], "first": ev["first"], "P": ev["P"],
-                    "max_new": args.max_new}) + "\n")
-                procs["consumer"].stdin.flush()
-            elif ev["ev"] == "done":
-                results[ev["req"]] = ev
-            elif ev["ev"] == "failed":
-                failed.append(ev)
-                _log(f"failed: {ev}")
-            elif ev["ev"] == "eof":
-                raise RuntimeError(f"{n} exited during the run")
-        t_end = time.monotonic()
+        for rep in range(args.repeats):
+            summary, toks = _pass(args, rep, procs, names, events)
+            passes.append(summary)
+            tokens.update(toks)
+            _log(f"pass {rep}: {summary['output_tokens_per_s']} tok/s, TTFT p50 "
+                 f"{summary['ttft_ms']['p50']} ms, TPOT p50 {summary['tpot_ms']['p50']} ms")
     finally:
         for p in procs.values():
             try:
@@ -314,26 +400,16 @@ def run(args):
     bad = [n for n, p in procs.items() if p.returncode != 0]
     if bad:
         raise RuntimeError(f"children exited with errors: {bad}")
-    ttft = sorted((firsts[r]["t"] - arrivals[r]) * 1e3 for r in results)
-    e2e = sorted((results[r]["t"] - arrivals[r]) * 1e3 for r in results)
-    tpot = sorted(results[r]["tpot_ms"] for r in results)
-    pct = lambda xs, q: xs[min(len(xs) - 1, int(q * len(xs)))] if xs else None   # noqa: E731
-    n_tok = sum(len(results[r]["tokens"]) for r in results)
-    summary = {
-        "requests": len(work), "completed": len(results), "failed": len(failed),
-        "output_tokens": n_tok, "makespan_s": round(t_end - t0, 3),
-        "output_tokens_per_s": round(n_tok / (t_end - t0), 1),
-        "ttft_ms": {"p50": round(pct(ttft, 0.5), 1), "p90": round(pct(ttft, 0.9), 1),
-                    "max": round(ttft[-1], 1)},
-        "e2e_ms": {"p50": round(pct(e2e, 0.5), 1), "p90": round(pct(e2e, 0.9), 1),
-                   "max": round(e2e[-1], 1)},
-        "tpot_ms": {"p50": round(pct(tpot, 0.5), 3), "p90": round(pct(tpot, 0.9), 3)},
-        "prefill_ms_p50": round(pct(sorted(f["prefill_ms"] for f in firsts.values()), 0.5), 1),
-        "load_ms_p50": round(pct(sorted(results[r]["load_ms"] for r in results), 0.5), 2),
-        "occupancy_p50": pct(sorted(results[r]["occupancy"] for r in results), 0.5),
-        "producers": args.producers, "batch_width": args.batch,
-    }
-    return summary, {r: results[r]["tokens"] for r in results}
+    summary = dict(passes[0])
+    if len(passes) > 1:
+        spread = lambda f: [f(x) for x in passes]   # noqa: E731
+        summary["passes"] = passes
+        summary["across_passes"] = {
+            "output_tokens_per_s": spread(lambda x: x["output_tokens_per_s"]),
+            "ttft_p50_ms": spread(lambda x: x["ttft_ms"]["p50"]),
+            "tpot_p50_ms": spread(lambda x: x["tpot_ms"]["p50"]),
+            "tpot_p90_ms": spread(lambda x: x["tpot_ms"]["p90"])}
+    return summary, tokens
 
 
 def parse(argv=None):
@@ -354,6 +430,8 @@ def parse(argv=None):
     ap.add_argument("--eager", action="store_true", help="decode without HIP graphs")
     ap.add_argument("--timeout", type=float, default=120.0)
     ap.add_argument("--tokens-out", default=None, help="write each request's tokens (JSON)")
+    ap.add_argument("--repeats", type=int, default=1,
+                    help="passes of the same workload in one run (children stay up)")
     ap.add_argument("--plan-batch", type=int, default=16,
                     help="batch size the decode attention plans its context split for (the "
                          "consumer and the control use max(--batch, this)): equal values give "

@@ -66,6 +66,10 @@ class ContinuousScheduler:
         self.starved_lane_steps = 0
         self.held_lane_steps = 0
         self.admit_stall_ms = 0.0
+        # (start on the monotonic clock, duration ms, streams) of each step
+        # since the last take_step_log(): what a serving run correlates with
+        # other processes' work on the same GPU.
+        self.step_log = []
         # Step inputs: one pinned host block and its device copy, as int32
         # [tokens B | ctx B | tables B x max_blocks]; the step reads views of
         # the device copy, so a captured graph sees each step's values.
@@ -142,6 +146,11 @@ class ContinuousScheduler:
             self.cv.notify()
         self._thread.join(timeout=10)
         self._loader.shutdown(wait=True)
+
+    def take_step_log(self):
+        """The steps since the last call: [(start s, duration ms, streams)]."""
+        log, self.step_log = self.step_log, []
+        return log
 
     def _active(self):
         return [s for s in self.slots if s]
@@ -283,12 +292,15 @@ class ContinuousScheduler:
                 live = [i for i, s in enumerate(self.slots) if s]
                 if not live:
                     continue
+                t_mono = time.monotonic()
                 t1 = time.perf_counter()
                 with self._on_stream():
                     nxt = self._step(live)
                 dt = (time.perf_counter() - t1) * 1e3
                 self.lane_steps += len(live)
                 self.steps += 1
+                if len(self.step_log) < 1_000_000:
+                    self.step_log.append((t_mono, dt, len(live)))
                 for row, i in enumerate(live):
                     s = self.slots[i]
                     s["steps"].append(dt)

@@ -98,6 +98,31 @@ def test_two_producers_one_consumer_match_control(tmp_path):
         assert got == want, f"batch {batch}: tokens differ from the one-process control"
 
 
+def test_repeated_passes_give_the_same_tokens(tmp_path):
+    """Passes of one run replay the workload on the same processes: every
+    pass's tokens equal the control's, and each pass reports its decode steps
+    grouped by overlapping prefills (the config-5 spread diagnosis)."""
+    out = _run(["control"] + COMMON)
+    want = {}
+    for line in out.splitlines():
+        if line.startswith("{"):
+            ev = json.loads(line)
+            want[ev["req"]] = ev["tokens"]
+    tok_file = tmp_path / "tokens.json"
+    out = _run(["run", "--batch", "4", "--repeats", "2", "--tokens-out", str(tok_file)] + COMMON)
+    summary = json.loads([ln for ln in out.splitlines() if ln.startswith("{")][-1])
+    assert len(summary["passes"]) == 2
+    for p in summary["passes"]:
+        assert p["completed"] == 6 and p["failed"] == 0
+        groups = p["decode_steps_by_overlapping_prefills"]
+        assert sum(g["steps"] for g in groups.values()) == p["decode_step_ms"]["steps"] > 0
+        assert p["ttft_parts_ms"]["queued_p50"] >= 0
+    got = json.loads(tok_file.read_text())
+    assert len(got) == 12
+    for req, toks in want.items():
+        assert got[req] == toks and got["r1" + req] == toks, req
+
+
 def test_llama8b_two_producers_one_consumer_match_control(tmp_path):
     """The serving workload's shape: Llama-3.1-8B, two prefill producer processes
     and one decode consumer at width 16 on this GPU, Poisson arrivals, prompts

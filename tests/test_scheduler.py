@@ -171,3 +171,39 @@ def test_prefetch_cap_ttl_and_join():
     p.ttl_s = 0.0                                             # everything left is stale
     assert p.prefetch("d")["prefetch"] == "started"           # "b" reclaimed, not counted
     assert p.outstanding() == ["d"]
+
+
+def test_contention_groups_steps_by_overlapping_prefills():
+    """Config-5 diagnosis: each decode step is counted with the number of
+    prefills whose [start, end) overlaps it, inside the pass window only."""
+    from rngd_pd_amd.serving.pd_one_gpu import contention
+    prefills = [(10.0, 10.1), (10.05, 10.2)]
+    steps = [
+        (9.0, 5.0, 4),        # before the pass window: ignored
+        (10.0, 4.0, 4),       # [10.000, 10.004): overlaps the first prefill
+        (10.06, 6.0, 4),      # [10.060, 10.066): both
+        (10.15, 5.0, 4),      # [10.150, 10.155): the second
+        (10.3, 3.0, 4),       # after both
+        (10.31, 3.5, 4),
+    ]
+    got = contention(steps, prefills, 9.5, 11.0)
+    assert got["0_prefills"] == {"steps": 2, "step_ms_p50": 3.5, "step_ms_p90": 3.5}
+    assert got["1_prefills"]["steps"] == 2
+    assert got["2_prefills"] == {"steps": 1, "step_ms_p50": 6.0, "step_ms_p90": 6.0}
+
+
+def test_step_log_is_taken_and_cleared():
+    from rngd_pd_amd.serving.scheduler import ContinuousScheduler
+    sched = ContinuousScheduler.__new__(ContinuousScheduler)
+    sched.step_log = [(1.0, 2.0, 3)]
+    assert sched.take_step_log() == [(1.0, 2.0, 3)]
+    assert sched.take_step_log() == []
+
+
+def test_each_pass_replays_the_workload_under_its_own_ids():
+    from rngd_pd_amd.serving.pd_one_gpu import parse, workload
+    args = parse(["run", "--requests", "5", "--small"])
+    a, b = workload(args, 0), workload(args, 2)
+    assert [r["req"] for r in a] == [f"q{i}" for i in range(5)]
+    assert [r["req"] for r in b] == [f"r2q{i}" for i in range(5)]
+    assert [(r["arrival"], r["tokens"]) for r in a] == [(r["arrival"], r["tokens"]) for r in b]
