@@ -352,6 +352,32 @@ int pdk_linear_argmax_tiled(const uint16_t* x, const uint16_t* wt, int B, int K,
                             int N, uint16_t* logits, uint64_t* keys,
                             int32_t* tokens, uintptr_t stream);
 
+/* The post-attention RMSNorm folded into its neighbours (rms_dsl,
+ * kernels/dsl_batch.py:22-41, between the o and gate/up matmuls of
+ * kernels/decode_batch.py:73-91):
+ * pdk_linear_ssq is pdk_linear with a residual (y = residual + x.w^T, residual
+ *   may alias y) that also writes ssq [N/16][B] fp32: ssq[t][b] = the sum over
+ *   columns 16t..16t+15 of y[b][.]^2, y as rounded to bf16. N % 16 == 0.
+ * pdk_linear_swiglu_rms is pdk_linear_swiglu on the un-normalised x with the
+ *   norm's gain folded into the weights (w_gate_up[n][k] = bf16(w[n][k] g[k]),
+ *   made once at weight load): row b's two sums are scaled by
+ *   r_b = rsqrt(sum_t ssq[t][b] / K + eps) (t in a fixed order) before silu,
+ *   i.e. silu(r x.wg^T) * (r x.wu^T) = the gate/up of rmsnorm(x) g, with one
+ *   bf16 rounding (of the weights' product with g) in place of the rounding of
+ *   the normalised activations. n_ssq = K / 16 (the tiles of the producing
+ *   pdk_linear_ssq call, with the same B). No launch between the two GEMMs. */
+int pdk_linear_ssq(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                   const uint16_t* residual, uint16_t* y, float* ssq, uintptr_t stream);
+int pdk_linear_ssq_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                         const uint16_t* residual, uint16_t* y, float* ssq,
+                         uintptr_t stream);
+int pdk_linear_swiglu_rms(const uint16_t* x, const uint16_t* w_gate_up, int B, int K,
+                          int M, const float* ssq, int n_ssq, float eps, uint16_t* y,
+                          uintptr_t stream);
+int pdk_linear_swiglu_rms_tiled(const uint16_t* x, const uint16_t* wt_gate_up, int B,
+                                int K, int M, const float* ssq, int n_ssq, float eps,
+                                uint16_t* y, uintptr_t stream);
+
 /* ---- KONI token blocks (second frame format) --------------------------------
  * The Furiosa native connector's KV payload (native_v4/kv.py:1-20): units of
  * one token of one tensor (t = 2*layer + 0 for K, 1 for V), each [Hkv][D] bf16,

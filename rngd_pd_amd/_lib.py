@@ -61,6 +61,7 @@ _I = ctypes.c_int
 _I64 = ctypes.c_int64
 _U = ctypes.c_uintptr_t if hasattr(ctypes, "c_uintptr_t") else ctypes.c_size_t
 _SZ = ctypes.c_size_t
+_F = ctypes.c_float
 
 # name -> (restype, argtypes); every declaration of include/rngdpd.h.
 SIGNATURES = {
@@ -100,6 +101,10 @@ SIGNATURES = {
     "pdk_linear_swiglu_tiled": (_I, [_P, _P, _I, _I, _I, _P, _U]),
     "pdk_linear_splitk_tiled": (_I, [_P, _P, _I, _I, _I, _I, _P, _U]),
     "pdk_linear_argmax_tiled": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _U]),
+    "pdk_linear_ssq": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _U]),
+    "pdk_linear_ssq_tiled": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _U]),
+    "pdk_linear_swiglu_rms": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _U]),
+    "pdk_linear_swiglu_rms_tiled": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _U]),
     "pdk_scatter_koni": (_I, [_P, _I64, _P, _I, _I, _P, _I, _P, _P, _I64, _I, _I, _I, _U]),
     "pdk_host_alloc": (_I, [_SZ, ctypes.POINTER(_P)]),
     "pdk_host_free": (_I, [_P]),

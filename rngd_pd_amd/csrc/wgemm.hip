@@ -52,7 +52,14 @@ __device__ __forceinline__ f32x4 mfma(const v8& a, const v8& b, f32x4 c) {
 constexpr int kStepK = 128;        // k per wave step: 4 MFMA of 32
 constexpr int kWaves = 8;
 
-enum Epilogue { kPlain = 0, kResidual = 1, kSwiGLU = 2, kArgmax = 3, kPartial = 4 };
+// kResidualSsq: kResidual that also writes, per 16-column tile and row, the
+// sum of squares of the bf16 outputs (ssq[tile][row]): the raw material of the
+// next RMSNorm. kSwiGLURms: kSwiGLU on weights with that norm's gain folded
+// into their columns, whose input x is the un-normalised residual: each row's
+// two sums are scaled by r = rsqrt(sum(ssq[.][row]) / K + eps) before SwiGLU,
+// so rmsnorm(x) . W^T = r * (x . (W diag g)^T) takes no launch of its own.
+enum Epilogue { kPlain = 0, kResidual = 1, kSwiGLU = 2, kArgmax = 3, kPartial = 4,
+                kResidualSsq = 5, kSwiGLURms = 6 };
 
 // Greedy-token key of one bf16 logit: the value in an order-preserving code
 // above the complement of the column, so the unsigned maximum is the largest
@@ -83,11 +90,14 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ w, int B,
                                                             int K, int N,
                                                             const uint16_t* r, uint16_t* y,
-                                                            uint64_t* keys, float* part) {
-  constexpr int kPairs = kEpi == kSwiGLU ? 2 : 1;
+                                                            uint64_t* keys, float* part,
+                                                            float* ssq, int n_ssq, float eps) {
+  constexpr bool kGLU = kEpi == kSwiGLU || kEpi == kSwiGLURms;
+  constexpr int kPairs = kGLU ? 2 : 1;
   constexpr int kW = kPairs * kCols;                 // W tiles per step
   constexpr int kDepth = depth_for(kTiles + kW);
   __shared__ float red[kWaves][kW][256];
+  __shared__ float rms[kEpi == kSwiGLURms ? 64 : 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
   const int n0 = blockIdx.x * 16 * kCols;
@@ -144,8 +154,47 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
 #pragma unroll
       for (int c = 0; c < 4; ++c) xv[slot][t][c] = pdk::ld16(xp[t] + k + 32 * c);
   };
+  // Row scales of kSwiGLURms: 32 lanes per row (16 rows per pass over the
+  // workgroup, kTiles passes), each adding every 32nd tile's sum of squares,
+  // then a fixed butterfly: a row's scale depends neither on B nor on timing.
+  // A lane's loads are issued before the first steps' weight loads
+  // (unconditional, from clamped addresses), so waiting for them costs no
+  // more than waiting for those.
+  constexpr int kTpr = 32, kPer = 8;                 // 32 lanes x 8 tiles per pass
+  const int srow = threadIdx.x / kTpr, ssub = threadIdx.x % kTpr;
+  float sq_part[kTiles];
+  if constexpr (kEpi == kSwiGLURms) {
 #pragma unroll
-  for (int d = 0; d < kDepth; ++d) load(d, d);
+    for (int t = 0; t < kTiles; ++t) sq_part[t] = 0.f;
+    for (int base = 0; base < n_ssq; base += kTpr * kPer) {
+      float v[kTiles][kPer];
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+        const float* sp = ssq + min(t * 16 + srow, B - 1);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+          v[t][i] = sp[(int64_t)min(base + ssub + i * kTpr, n_ssq - 1) * B];
+      }
+      if (base + kTpr * kPer >= n_ssq) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) load(d, d);
+      }
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+          sq_part[t] += base + ssub + i * kTpr < n_ssq ? v[t][i] : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+      for (int o = 1; o < kTpr; o <<= 1) sq_part[t] += __shfl_xor(sq_part[t], o);
+      if (ssub == 0) rms[t * 16 + srow] = rsqrtf(sq_part[t] / (float)K + eps);
+    }
+  } else {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) load(d, d);
+  }
   for (int j0 = 0; j0 < n_mine; j0 += kDepth) {
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
@@ -193,10 +242,23 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
         continue;
       }
       float out = v[0];
-      if (kEpi == kResidual && ok) out += pdk::bf16_to_f32(r[at]);
+      if ((kEpi == kResidual || kEpi == kResidualSsq) && ok) out += pdk::bf16_to_f32(r[at]);
       if (kEpi == kSwiGLU) out = v[0] / (1.f + expf(-v[0])) * v[kPairs - 1];
+      if (kEpi == kSwiGLURms) {
+        const float s = rms[m < 64 ? m : 63];
+        const float a = v[0] * s, b = v[kPairs - 1] * s;
+        out = a / (1.f + expf(-a)) * b;
+      }
       const uint32_t h = pdk::f32_to_bf16_rne(out);
       if (ok && y) y[at] = (uint16_t)h;
+      if (kEpi == kResidualSsq) {
+        // Lanes e .. e|15 hold one row's 16 columns of this tile.
+        const float hv = pdk::bf16_to_f32(h);
+        float sq = ok ? hv * hv : 0.f;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o);
+        if ((e & 15) == 0 && m < B) ssq[((int64_t)blockIdx.x * kCols + c) * B + m] = sq;
+      }
       if (kEpi == kArgmax) {
         // The 16 lanes e .. e|15 hold one row's 16 columns of this tile: the
         // best of them goes to keys[m] (an atomic only when it beats the
@@ -229,10 +291,10 @@ __global__ void argmax_finish_kernel(uint64_t* keys, int B, int32_t* tokens) {
 template <int kCols, int kEpi, bool kTiled>
 int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
                 uint16_t* y, uint64_t* keys, hipStream_t st, float* part = nullptr,
-                int splits = 1) {
+                int splits = 1, float* ssq = nullptr, int n_ssq = 0, float eps = 0.f) {
   const dim3 grid((N + 16 * kCols - 1) / (16 * kCols), splits), block(kWaves * 64);
 #define PDK_WGEMM(T) \
-  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part)
+  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part, ssq, n_ssq, eps)
   switch ((B + 15) / 16) {
     case 1: PDK_WGEMM(1); break;
     case 2: PDK_WGEMM(2); break;
@@ -250,14 +312,17 @@ int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const
 // with 4 tiles; N = 4096 and 6144 need every workgroup one tile gives.
 template <int kEpi, bool kTiled>
 int launch(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
-           uint16_t* y, uint64_t* keys, hipStream_t st) {
+           uint16_t* y, uint64_t* keys, hipStream_t st, float* ssq = nullptr, int n_ssq = 0,
+           float eps = 0.f) {
   const int64_t wide = (N + 63) / 64;                // workgroups with 4 tiles
   // Wide SwiGLU tiles hold 8 weight tiles per step in registers: beyond 32
   // streams they would spill, and one tile is used instead. The lm_head with
   // tiled weights runs 4 tiles wide at every B (B = 4: 181 -> 178 us).
-  const bool four = kEpi == kSwiGLU ? (wide >= 192 && B <= 32) : ((B > 8 || kTiled) && wide >= 1024);
-  if (four) return launch_cols<4, kEpi, kTiled>(x, w, B, K, N, r, y, keys, st);
-  return launch_cols<1, kEpi, kTiled>(x, w, B, K, N, r, y, keys, st);
+  constexpr bool kGLU = kEpi == kSwiGLU || kEpi == kSwiGLURms;
+  const bool four = kGLU ? (wide >= 192 && B <= 32) : ((B > 8 || kTiled) && wide >= 1024);
+  if (four) return launch_cols<4, kEpi, kTiled>(x, w, B, K, N, r, y, keys, st, nullptr, 1, ssq,
+                                                n_ssq, eps);
+  return launch_cols<1, kEpi, kTiled>(x, w, B, K, N, r, y, keys, st, nullptr, 1, ssq, n_ssq, eps);
 }
 
 // Tiled copy of W [N][K]: one thread per 16-byte group of the copy.
@@ -307,6 +372,30 @@ int linear_swiglu(const uint16_t* x, const uint16_t* w_gate_up, int B, int K, in
   PDK_REQUIRE(!kTiled || M % 16 == 0, "tiled gate|up weights need M %% 16 == 0 (got %d)", M);
   return launch<kSwiGLU, kTiled>(x, w_gate_up, B, K, M, nullptr, y, nullptr,
                                  pdk::as_stream(stream));
+}
+
+template <bool kTiled>
+int linear_ssq(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* residual,
+               uint16_t* y, float* ssq, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_shape(x, w, y, B, K, N)) return rc;
+  PDK_REQUIRE(residual && ssq, "null pointer argument");
+  PDK_REQUIRE(N % 16 == 0, "N must be a multiple of 16 (got %d)", N);
+  return launch<kResidualSsq, kTiled>(x, w, B, K, N, residual, y, nullptr, pdk::as_stream(stream),
+                                      ssq);
+}
+
+template <bool kTiled>
+int linear_swiglu_rms(const uint16_t* x, const uint16_t* w_gate_up, int B, int K, int M,
+                      const float* ssq, int n_ssq, float eps, uint16_t* y, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_shape(x, w_gate_up, y, B, K, M)) return rc;
+  PDK_REQUIRE(ssq, "null pointer argument");
+  PDK_REQUIRE(n_ssq >= 1 && n_ssq * 16 == K, "n_ssq must be K / 16 = %d (got %d)", K / 16, n_ssq);
+  PDK_REQUIRE(eps > 0.f, "eps must be positive");
+  PDK_REQUIRE(!kTiled || M % 16 == 0, "tiled gate|up weights need M %% 16 == 0 (got %d)", M);
+  return launch<kSwiGLURms, kTiled>(x, w_gate_up, B, K, M, nullptr, y, nullptr,
+                                    pdk::as_stream(stream), const_cast<float*>(ssq), n_ssq, eps);
 }
 
 template <bool kTiled>
@@ -397,6 +486,29 @@ extern "C" int pdk_linear_argmax_tiled(const uint16_t* x, const uint16_t* wt, in
                                        uint16_t* logits, uint64_t* keys, int32_t* tokens,
                                        uintptr_t stream) {
   return linear_argmax<true>(x, wt, B, K, N, logits, keys, tokens, stream);
+}
+
+extern "C" int pdk_linear_ssq(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                              const uint16_t* residual, uint16_t* y, float* ssq, uintptr_t stream) {
+  return linear_ssq<false>(x, w, B, K, N, residual, y, ssq, stream);
+}
+
+extern "C" int pdk_linear_ssq_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                                    const uint16_t* residual, uint16_t* y, float* ssq,
+                                    uintptr_t stream) {
+  return linear_ssq<true>(x, wt, B, K, N, residual, y, ssq, stream);
+}
+
+extern "C" int pdk_linear_swiglu_rms(const uint16_t* x, const uint16_t* w_gate_up, int B, int K,
+                                     int M, const float* ssq, int n_ssq, float eps, uint16_t* y,
+                                     uintptr_t stream) {
+  return linear_swiglu_rms<false>(x, w_gate_up, B, K, M, ssq, n_ssq, eps, y, stream);
+}
+
+extern "C" int pdk_linear_swiglu_rms_tiled(const uint16_t* x, const uint16_t* wt_gate_up, int B,
+                                           int K, int M, const float* ssq, int n_ssq, float eps,
+                                           uint16_t* y, uintptr_t stream) {
+  return linear_swiglu_rms<true>(x, wt_gate_up, B, K, M, ssq, n_ssq, eps, y, stream);
 }
 
 extern "C" int pdk_linear_splitk_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,

@@ -9,9 +9,10 @@ Replaces the reference's BatchDecodeEngine.step / step_logits
   qkv = h . Wqkv^T                                 pdk_linear_splitk (fp32 halves of K; one part when K < 4096)
   RoPE(q, k); new k, v into the paged cache;
   ao = attention over slots 0..pos                 pdk_decode_attn_rope (+ its merge when split)
-  x = x + ao . Wo^T                                pdk_linear, residual fused
-  h = rmsnorm(x)                                   pdk_rmsnorm
-  a = silu(h . Wg^T) * (h . Wu^T)                  pdk_linear_swiglu
+  x = x + ao . Wo^T; ssq = row sums of x^2         pdk_linear_ssq, residual fused
+  a = silu(r h) * (r u), [h; u] = x . (W diag g)^T pdk_linear_swiglu_rms: the norm's gain folded
+      with r = rsqrt(sum ssq / H + eps)            into the gate|up weights, its scale r into
+                                                   the epilogue (rmsnorm(x) . W^T, no launch)
   partials = a . Wd^T split over K                 pdk_linear_splitk (fp32, joins x in the next norm)
 
 then the final norm (which adds the last layer's partials) and the lm_head
@@ -30,7 +31,7 @@ import torch
 
 from .. import _lib
 from ..kernels import attention as _attn
-from ..kernels.decode_step import tile_weight
+from ..kernels.decode_step import fold_norm, tile_weight
 from ..kernels.handoff import stream_handle
 
 BF16 = torch.bfloat16
@@ -155,6 +156,9 @@ class LlamaDecoder:
         self.qkv_splits = 2 if H // 128 >= 32 else 1
         self.part_qkv = torch.empty((self.qkv_splits, B, cfg.qkv_dim), dtype=torch.float32,
                                     device=dev)
+        # Per 16-column tile and row, the sums of squares the O projection
+        # leaves for the post-attention norm (fused into gate|up).
+        self.ssq = torch.zeros((H // 16, B), dtype=torch.float32, device=dev)
         self.inv = cfg.inv_freq().to(dev)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
         self._ws = None
@@ -166,8 +170,10 @@ class LlamaDecoder:
         # GEMMs themselves do).
         self.tiled = bool(tiled) and cfg.inter % 16 == 0
         prep = tile_weight if self.tiled else (lambda t: t)
-        self._wt = [tuple(prep(t) for t in (w.wqkv[i], w.wo[i], w.wgu[i], w.wd[i]))
-                    for i in range(cfg.n_layers)]
+        # gate|up with the post-attention norm's gain folded into its columns
+        # (a copy in either layout; the originals stay as they are).
+        self._wt = [(prep(w.wqkv[i]), prep(w.wo[i]), prep(fold_norm(w.wgu[i], w.norm2[i])),
+                     prep(w.wd[i])) for i in range(cfg.n_layers)]
         self._lm_head = prep(w.lm_head)
         if self.tiled:
             # The copies are written on the current stream; a step may run on
@@ -175,7 +181,9 @@ class LlamaDecoder:
             torch.cuda.current_stream(dev).synchronize()
         self._gemm = {n: n + "_tiled" if self.tiled else n for n in
                       ("pdk_linear", "pdk_linear_splitk", "pdk_linear_swiglu",
-                       "pdk_linear_argmax")}
+                       "pdk_linear_argmax", "pdk_linear_ssq", "pdk_linear_swiglu_rms")}
+        if cfg.hidden % 16:
+            raise ValueError("the fused post-attention norm needs hidden % 16 == 0")
         self._layers = [tuple(t.data_ptr() for t in (w.norm1[i], wt[0], wt[1], w.norm2[i], wt[2],
                                                      wt[3], cache.k[i], cache.v[i]))
                         for i, wt in enumerate(self._wt)]
@@ -234,8 +242,9 @@ class LlamaDecoder:
         aop, actp, inv = self.ao.data_ptr(), self.act.data_ptr(), self.inv.data_ptr()
         call = _lib.call
         g = self._gemm
-        lin, lin_sk, lin_sw, lin_am = (g["pdk_linear"], g["pdk_linear_splitk"],
-                                       g["pdk_linear_swiglu"], g["pdk_linear_argmax"])
+        lin_sk, lin_am = g["pdk_linear_splitk"], g["pdk_linear_argmax"]
+        lin_ssq, lin_swr = g["pdk_linear_ssq"], g["pdk_linear_swiglu_rms"]
+        ssqp = self.ssq.data_ptr()
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
             torch.index_select(w.embed, 0, tokens.long(), out=x)
             partp, sp = self.part.data_ptr(), self.down_splits
@@ -248,9 +257,8 @@ class LlamaDecoder:
                 call(lin_sk, hp, wqkv, B, H, QKV, qs, pqp, st)
                 call("pdk_decode_attn_rope", pqp, qs, inv, ck, cv, nb, tp, mb, cp, int(max_ctx),
                      B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, self.plan_batch, st)
-                call(lin, aop, wo, B, NH * HD, H, xp, xp, st)
-                call("pdk_rmsnorm", xp, None, n2, B, H, eps, hp, st)
-                call(lin_sw, hp, wgu, B, H, M, actp, st)
+                call(lin_ssq, aop, wo, B, NH * HD, H, xp, xp, ssqp, st)
+                call(lin_swr, xp, wgu, B, H, M, ssqp, H // 16, eps, actp, st)
                 call(lin_sk, actp, wd, B, M, H, sp, partp, st)
             call("pdk_rmsnorm_partials", xp, partp, sp, w.norm_f.data_ptr(), B, H, eps, hp, st)
             call(lin_am, hp, self._lm_head.data_ptr(), B, H, cfg.vocab,

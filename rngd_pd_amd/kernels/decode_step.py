@@ -194,6 +194,56 @@ def linear_swiglu(x, w_gate_up, out=None, stream=None):
     return out
 
 
+def linear_ssq(x, w, residual, ssq, out=None, stream=None):
+    """residual + x . w^T -> [B, N] (``out`` may be ``residual``), and ssq
+    float32 [N/16, B]: per 16-column tile and row, the sum of squares of the
+    bf16 outputs (the raw material of the next RMSNorm)."""
+    B, K, N = _check_linear(x, w)
+    _need(residual, "residual")
+    if tuple(residual.shape) != (B, N) or not residual.is_contiguous():
+        raise ValueError(f"residual must be contiguous [{B}, {N}]")
+    if N % 16:
+        raise ValueError(f"N must be a multiple of 16 (got {N})")
+    if ssq.dtype != torch.float32 or not ssq.is_cuda or not ssq.is_contiguous() \
+            or ssq.numel() < (N // 16) * B:
+        raise ValueError(f"ssq must be contiguous float32 holding {N // 16}x{B}")
+    if out is None:
+        out = torch.empty((B, N), dtype=x.dtype, device=x.device)
+    elif tuple(out.shape) != (B, N) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{B}, {N}]")
+    _lib.call(_entry("pdk_linear_ssq", w), x.data_ptr(), w.data_ptr(), B, K, N,
+              residual.data_ptr(), out.data_ptr(), ssq.data_ptr(), stream_handle(stream))
+    return out
+
+
+def fold_norm(w, g):
+    """w [N, K] with the RMSNorm gain g [K] folded into its columns:
+    bf16(w * g), the weight linear_swiglu_rms takes."""
+    _need(w, "w")
+    _need(g, "g")
+    if w.dim() != 2 or g.shape != (w.shape[1],):
+        raise ValueError(f"g must be [{w.shape[1]}] for w {tuple(w.shape)}")
+    return (w.float() * g.float()[None, :]).to(w.dtype).contiguous()
+
+
+def linear_swiglu_rms(x, w_gate_up_folded, ssq, eps, out=None, stream=None):
+    """silu(r x . wg'^T) * (r x . wu'^T) -> [B, M], r_b = rsqrt(sum_t ssq[t, b]
+    / K + eps): the gate|up of rmsnorm(x) * g for weights folded with g
+    (fold_norm), ssq from the linear_ssq that produced x."""
+    B, K, M = _check_linear(x, w_gate_up_folded, rows_per_col=2)
+    if ssq.dtype != torch.float32 or not ssq.is_cuda or not ssq.is_contiguous() \
+            or ssq.numel() < (K // 16) * B:
+        raise ValueError(f"ssq must be contiguous float32 holding {K // 16}x{B}")
+    if out is None:
+        out = torch.empty((B, M), dtype=x.dtype, device=x.device)
+    elif tuple(out.shape) != (B, M) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{B}, {M}]")
+    _lib.call(_entry("pdk_linear_swiglu_rms", w_gate_up_folded), x.data_ptr(),
+              w_gate_up_folded.data_ptr(), B, K, M, ssq.data_ptr(), K // 16, float(eps),
+              out.data_ptr(), stream_handle(stream))
+    return out
+
+
 def linear_argmax(x, w, keys, tokens=None, logits=None, stream=None):
     """Greedy tokens of x . w^T (the lm_head): the first-maximum argmax of each
     row of the bf16 logits, computed in the GEMM's epilogue. ``keys`` is an

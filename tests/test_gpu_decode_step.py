@@ -267,6 +267,69 @@ def test_linear_swiglu(cuda, B, K, M):
     np.testing.assert_allclose(_f32(to_host(y)), want, rtol=HALF_ULP, atol=tol)
 
 
+@pytest.mark.parametrize("B,K,N", [(16, 4096, 4096), (4, 4096, 4096), (3, 256, 1024),
+                                   (64, 128, 256), (1, 128, 16), (33, 512, 2048)])
+def test_linear_ssq(cuda, B, K, N):
+    """The O projection with the norm's raw material: y bit-identical to
+    pdk_linear with the residual, ssq[t][b] the sum of y[b, 16t:16t+16]^2
+    (as bf16 values), tiled and untiled weights alike."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B * 7 + K + N)
+    x, w, r = rand_bf16(rng, (B, K)), rand_bf16(rng, (N, K), 0.05), rand_bf16(rng, (B, N), 4.0)
+    xd, wd = to_dev(x), to_dev(w)
+    print(f"linear_ssq B={B} K={K} N={N}", flush=True)
+    want_y = K_.linear(xd, wd, residual=to_dev(r))
+    outs = []
+    for wgt in (wd, K_.tile_weight(wd)):
+        rd = to_dev(r)
+        ssq = torch.full((N // 16, B), float("nan"), dtype=torch.float32, device=cuda)
+        y = K_.linear_ssq(xd, wgt, rd, ssq, out=rd)            # in place, as the decoder runs it
+        outs.append((y, ssq))
+    torch.cuda.synchronize()
+    for y, ssq in outs:
+        assert torch.equal(y.view(torch.int16), want_y.view(torch.int16))
+        yf = _f32(to_host(y)).astype(np.float64)
+        want = (yf.reshape(B, N // 16, 16) ** 2).sum(-1).T
+        np.testing.assert_allclose(ssq.cpu().numpy(), want, rtol=1e-6, atol=1e-30)
+    assert torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("B,K,M", [(16, 4096, 14336), (4, 4096, 14336), (3, 256, 64),
+                                   (40, 512, 64), (1, 128, 16)])
+def test_linear_swiglu_rms(cuda, B, K, M):
+    """gate|up of rmsnorm(x) * g from the un-normalised x, the gain folded into
+    the weights and the row scale taken from per-tile sums of squares: within
+    half an ulp of the same products in fp64 (the folded bf16 weights, the
+    exact row scale), within 1 % of the unfused norm -> gate|up, and the
+    same bits on tiled weights."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B * 13 + K + M)
+    x = rand_bf16(rng, (B, K), 2.0)
+    w = rand_bf16(rng, (2 * M, K), 0.05)
+    g = _bf16_bits_rne(1.0 + 0.1 * rng.standard_normal(K).astype(np.float32))
+    eps = 1e-5
+    xd, wd, gd = to_dev(x), to_dev(w), to_dev(g)
+    xf = _f32(x).astype(np.float64)
+    ssq = torch.from_numpy((xf.reshape(B, K // 16, 16) ** 2).sum(-1).T.astype(np.float32))
+    ssq = ssq.contiguous().to(cuda)
+    print(f"linear_swiglu_rms B={B} K={K} M={M}", flush=True)
+    wf = K_.fold_norm(wd, gd)
+    y = K_.linear_swiglu_rms(xd, wf, ssq, eps)
+    y_t = K_.linear_swiglu_rms(xd, K_.tile_weight(wf), ssq, eps)
+    # the unfused path: pdk_rmsnorm then pdk_linear_swiglu on the raw weights
+    h = K_.rmsnorm(xd, gd, eps)
+    y_ref = K_.linear_swiglu(h, wd)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y_t.view(torch.int16))
+    r = 1.0 / np.sqrt(ssq.cpu().numpy().astype(np.float64).sum(0) / K + eps)     # [B]
+    gu = (xf @ _f32(to_host(wf)).astype(np.float64).T) * r[:, None]
+    want = od.swiglu(gu)
+    tol = 1e-5 * np.abs(gu).max() ** 2
+    np.testing.assert_allclose(_f32(to_host(y)), want, rtol=HALF_ULP, atol=tol)
+    a, b = _f32(to_host(y)).astype(np.float64), _f32(to_host(y_ref)).astype(np.float64)
+    assert np.linalg.norm(a - b) <= 0.01 * np.linalg.norm(b)
+
+
 @pytest.mark.parametrize("B,K,N", [(16, 4096, 128256), (4, 4096, 128256), (3, 256, 1000),
                                    (1, 128, 7)])
 def test_linear_argmax(cuda, B, K, N):
