@@ -161,7 +161,7 @@ __device__ __forceinline__ void span_pv(Span& r, const float* p, uint32_t pmask,
   v8 pv;
 #pragma unroll
   for (int w = 0; w < 4; ++w)
-    pv.w[w] = (pdk::f32_to_bf16_rne(p[2 * w]) | (pdk::f32_to_bf16_rne(p[2 * w + 1]) << 16)) & pmask;
+    pv.w[w] = pdk::pack_bf16x2_rne(p[2 * w], p[2 * w + 1]) & pmask;   // p in [0, 1]: finite
 #pragma unroll
   for (int n = 0; n < 8; ++n) o[n] = mfma(pv, r.vf[n], o[n]);
 }
