@@ -221,6 +221,24 @@ int pdk_decode_attn_rope(const float* qkv_partials, int splits,
                          float scale, void* workspace, size_t workspace_bytes,
                          uint16_t* out, int plan_batch, uintptr_t stream);
 
+/* pdk_decode_attn_rope for a q|k|v projection whose input was the
+ * un-normalised residual and whose weights carry the pre-attention RMSNorm's
+ * gain (rms_dsl, kernels/dsl_batch.py:22-41, folded): each stream's summed
+ * partials are scaled by r_b = rsqrt(sum_t ssq[b][t] / (16 n_ssq) + eps)
+ * before the one rounding, ssq [B][n_ssq] fp32 holding the residual's per
+ * 16-column tile sums of squares (pdk_linear_splitk_final, pdk_row_ssq). The
+ * row scale is summed in a fixed order, so a stream's value does not depend
+ * on B. head_dim 128. */
+int pdk_decode_attn_rope_rms(const float* qkv_partials, int splits,
+                             const float* ssq, int n_ssq, float eps,
+                             const float* inv_freq, uint16_t* cache_k,
+                             uint16_t* cache_v, int num_blocks,
+                             const int32_t* block_tables, int max_blocks,
+                             const int32_t* ctx_lens, int max_ctx, int B,
+                             int n_q_heads, int n_kv_heads, int head_dim,
+                             float scale, void* workspace, size_t workspace_bytes,
+                             uint16_t* out, int plan_batch, uintptr_t stream);
+
 /* Write one new token's k and v per stream at slot ctx[b]-1 of the paged
  * cache: the one-hot cache injection Kf = Kp + k*oh, Vf = Vp + v*oh
  * (kernels/decode_batch.py:81-82), done as a store.
@@ -286,6 +304,24 @@ int pdk_rope_cache_append_partials(const float* partials, int splits, int N,
                                    int num_blocks, int B, int n_q_heads,
                                    int n_kv_heads, int head_dim,
                                    uintptr_t stream);
+
+/* The same with the folded pre-attention norm's row scale (as
+ * pdk_decode_attn_rope_rms; head_dim >= 64): the two calls' outputs and cache
+ * contents are bit-identical to pdk_decode_attn_rope_rms's. */
+int pdk_rope_cache_append_partials_rms(const float* partials, int splits, int N,
+                                       const float* ssq, int n_ssq, float eps,
+                                       uint16_t* q_out, const float* inv_freq,
+                                       const int32_t* ctx_lens,
+                                       const int32_t* block_tables, int max_blocks,
+                                       uint16_t* cache_k, uint16_t* cache_v,
+                                       int num_blocks, int B, int n_q_heads,
+                                       int n_kv_heads, int head_dim,
+                                       uintptr_t stream);
+
+/* ssq [B][H/16] fp32: per 16-column tile t, the sum of x[b][16t..16t+15]^2
+ * (bf16 x [B][H], H % 16 == 0): the row-scale input of the folded norms when
+ * no GEMM produced x (the embedding rows before the first layer). */
+int pdk_row_ssq(const uint16_t* x, int B, int H, float* ssq, uintptr_t stream);
 
 /* out [B][M] = silu(g) * u for gate_up [B][2M] = [g | u] (swiglu_dsl,
  * kernels/dsl_batch.py:55-71). M % 8 == 0. */
@@ -356,12 +392,12 @@ int pdk_linear_argmax_tiled(const uint16_t* x, const uint16_t* wt, int B, int K,
  * kernels/dsl_batch.py:22-41, between the o and gate/up matmuls of
  * kernels/decode_batch.py:73-91):
  * pdk_linear_ssq is pdk_linear with a residual (y = residual + x.w^T, residual
- *   may alias y) that also writes ssq [N/16][B] fp32: ssq[t][b] = the sum over
+ *   may alias y) that also writes ssq [B][N/16] fp32: ssq[b][t] = the sum over
  *   columns 16t..16t+15 of y[b][.]^2, y as rounded to bf16. N % 16 == 0.
  * pdk_linear_swiglu_rms is pdk_linear_swiglu on the un-normalised x with the
  *   norm's gain folded into the weights (w_gate_up[n][k] = bf16(w[n][k] g[k]),
  *   made once at weight load): row b's two sums are scaled by
- *   r_b = rsqrt(sum_t ssq[t][b] / K + eps) (t in a fixed order) before silu,
+ *   r_b = rsqrt(sum_t ssq[b][t] / K + eps) (t in a fixed order) before silu,
  *   i.e. silu(r x.wg^T) * (r x.wu^T) = the gate/up of rmsnorm(x) g, with one
  *   bf16 rounding (of the weights' product with g) in place of the rounding of
  *   the normalised activations. n_ssq = K / 16 (the tiles of the producing
@@ -377,6 +413,33 @@ int pdk_linear_swiglu_rms(const uint16_t* x, const uint16_t* w_gate_up, int B, i
 int pdk_linear_swiglu_rms_tiled(const uint16_t* x, const uint16_t* wt_gate_up, int B,
                                 int K, int M, const float* ssq, int n_ssq, float eps,
                                 uint16_t* y, uintptr_t stream);
+
+/* The down projection and the next RMSNorm's residual add in one launch:
+ * pdk_linear_splitk whose last split to finish, per group of columns, adds the
+ * splits' partials in split order to `residual` in place (residual =
+ * bf16(residual + sum), the update pdk_rmsnorm_partials makes) and writes
+ * ssq [B][N/16] as pdk_linear_ssq does. Workgroups never wait for each other:
+ * each counts itself in on counters (int32, >= N/16 of them, zero before the
+ * first call; every call leaves them zero) after its partials are stored, and
+ * the one that completes a group finishes it. Calls sharing counters must not
+ * overlap. N % 16 == 0, 1 <= splits <= 16. */
+int pdk_linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                            int splits, float* partials, uint16_t* residual, float* ssq,
+                            int* counters, uintptr_t stream);
+int pdk_linear_splitk_final_tiled(const uint16_t* x, const uint16_t* wt, int B, int K,
+                                  int N, int splits, float* partials, uint16_t* residual,
+                                  float* ssq, int* counters, uintptr_t stream);
+
+/* The lm_head with greedy sampling (pdk_linear_argmax) on weights carrying
+ * the final norm's gain, x the un-normalised residual: each row's logits are
+ * scaled by its r (ssq [B][K/16], as pdk_linear_swiglu_rms) before the bf16
+ * rounding the argmax ranks. */
+int pdk_linear_argmax_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                          const float* ssq, int n_ssq, float eps, uint16_t* logits,
+                          uint64_t* keys, int32_t* tokens, uintptr_t stream);
+int pdk_linear_argmax_rms_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                                const float* ssq, int n_ssq, float eps, uint16_t* logits,
+                                uint64_t* keys, int32_t* tokens, uintptr_t stream);
 
 /* ---- KONI token blocks (second frame format) --------------------------------
  * The Furiosa native connector's KV payload (native_v4/kv.py:1-20): units of

@@ -82,6 +82,9 @@ SIGNATURES = {
                                      ctypes.c_float, _P, _U]),
     "pdk_decode_attn_rope": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I,
                                   ctypes.c_float, _P, _SZ, _P, _I, _U]),
+    "pdk_decode_attn_rope_rms": (_I, [_P, _I, _P, _I, ctypes.c_float, _P, _P, _P, _I, _P, _I,
+                                      _P, _I, _I, _I, _I, _I, ctypes.c_float, _P, _SZ, _P, _I,
+                                      _U]),
     "pdk_cache_append": (_I, [_P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _U]),
     "pdk_greedy_argmax": (_I, [_P, _I, _I, _I64, _P, _U]),
     "pdk_rmsnorm": (_I, [_P, _P, _P, _I, _I, ctypes.c_float, _P, _U]),
@@ -89,6 +92,8 @@ SIGNATURES = {
                                    _U]),
     "pdk_rope_cache_append_partials": (_I, [_P, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I,
                                             _I, _I, _U]),
+    "pdk_rope_cache_append_partials_rms": (_I, [_P, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P,
+                                                _P, _I, _P, _P, _I, _I, _I, _I, _I, _U]),
     "pdk_swiglu": (_I, [_P, _I, _I, _P, _U]),
     "pdk_linear": (_I, [_P, _P, _I, _I, _I, _P, _P, _U]),
     "pdk_linear_swiglu": (_I, [_P, _P, _I, _I, _I, _P, _U]),
@@ -105,6 +110,11 @@ SIGNATURES = {
     "pdk_linear_ssq_tiled": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _U]),
     "pdk_linear_swiglu_rms": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _U]),
     "pdk_linear_swiglu_rms_tiled": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _U]),
+    "pdk_linear_splitk_final": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _U]),
+    "pdk_linear_splitk_final_tiled": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _U]),
+    "pdk_linear_argmax_rms": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _P, _P, _U]),
+    "pdk_linear_argmax_rms_tiled": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _P, _P, _U]),
+    "pdk_row_ssq": (_I, [_P, _I, _I, _P, _U]),
     "pdk_scatter_koni": (_I, [_P, _I64, _P, _I, _I, _P, _I, _P, _P, _I64, _I, _I, _I, _U]),
     "pdk_host_alloc": (_I, [_SZ, ctypes.POINTER(_P)]),
     "pdk_host_free": (_I, [_P]),

@@ -315,7 +315,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int32_t* ctx_lens, uint32_t hgw, int max_blocks, int num_blocks, int split_tokens,
     int nsplit, float scale_log2, uint16_t* out, float* ws_ml, float* ws_o,
     const float* part, int64_t part_stride, const float* inv_freq, uint16_t* ck_w,
-    uint16_t* cv_w) {
+    uint16_t* cv_w, const float* ssq, int n_ssq, float eps) {
   __shared__ float sm_m[kMaxWaves][kMaxG];
   __shared__ float sm_l[kMaxWaves][kMaxG];
   __shared__ __align__(16) uint16_t q_rot[kRope ? kMaxG : 1][kD];   // rotated q of the group
@@ -380,7 +380,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   float raw[kPre][2][kParts];
   float ifreq = 0.f;
+  // The row scale's loads go out with the partial sums', before any K/V load;
+  // it is finished after those are issued (loads complete in order).
+  pdk::RowRms rr{};
   if constexpr (kRope > 0) {
+    if (ssq) rr = pdk::row_rms_load(ssq, b, n_ssq, lane);
     ifreq = inv_freq[lane];
 #pragma unroll
     for (int k = 0; k < kPre; ++k) {
@@ -435,7 +439,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // the new k and v into LDS.
     float sn, cs;
     sincosf((float)max(pos, 0) * ifreq, &sn, &cs);
-    auto rnd = [](float x) { return pdk::bf16_to_f32(pdk::f32_to_bf16_rne(x)); };
+    const float rb = ssq ? pdk::row_rms_finish(rr, ssq, b, n_ssq, 16 * n_ssq, eps, lane)
+                         : 1.f;
+    auto rnd = [&](float x) {
+      return pdk::bf16_to_f32(pdk::f32_to_bf16_rne(ssq ? x * rb : x));
+    };
     auto put = [&](int r, float x0, float x1) {
       if (r <= G) {
         uint16_t* dst = r < G ? q_rot[r] : kv_new[0];
@@ -685,6 +693,9 @@ struct RopeIn {
   const float* inv_freq;
   uint16_t* ck_w;
   uint16_t* cv_w;
+  const float* ssq = nullptr;    // folded-norm row scale (pdk::row_rms), or none
+  int n_ssq = 0;
+  float eps = 0.f;
 };
 
 int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
@@ -747,7 +758,7 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   hipLaunchKernelGGL(decode_attn_kernel<R>, grid, block, lds, st, a.q, a.ck, a.cv, a.tables,   \
                      a.ctx, hgw, a.max_blocks, a.num_blocks, a.split_tokens, a.nsplit,         \
                      a.scale_log2, a.out, a.ws_ml, a.ws_o, rope.part, pstride, rope.inv_freq,  \
-                     rope.ck_w, rope.cv_w)
+                     rope.ck_w, rope.cv_w, rope.ssq, rope.n_ssq, rope.eps)
   switch (rope.part ? rope.splits : 0) {
     case 0: PDK_ATTN_LAUNCH(0); break;
     case 1: PDK_ATTN_LAUNCH(1); break;
@@ -826,6 +837,29 @@ extern "C" int pdk_decode_attn_rope(const float* qkv_partials, int splits, const
                      workspace_bytes, out, stream,
                      RopeIn{qkv_partials, splits, inv_freq, cache_k, cache_v},
                      plan_batch > 0 ? plan_batch : B);
+}
+
+extern "C" int pdk_decode_attn_rope_rms(const float* qkv_partials, int splits,
+                                        const float* ssq, int n_ssq, float eps,
+                                        const float* inv_freq, uint16_t* cache_k,
+                                        uint16_t* cache_v, int num_blocks,
+                                        const int32_t* block_tables, int max_blocks,
+                                        const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads,
+                                        int n_kv_heads, int head_dim, float scale, void* workspace,
+                                        size_t workspace_bytes, uint16_t* out, int plan_batch,
+                                        uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(qkv_partials && inv_freq && ssq, "null pointer argument");
+  PDK_REQUIRE(splits == 1 || splits == 2 || splits == 4, "splits must be 1, 2 or 4 (got %d)",
+              splits);
+  PDK_REQUIRE(n_ssq >= 1 && eps > 0.f, "n_ssq must be >= 1 and eps positive");
+  RopeIn rope{qkv_partials, splits, inv_freq, cache_k, cache_v};
+  rope.ssq = ssq;
+  rope.n_ssq = n_ssq;
+  rope.eps = eps;
+  return launch_attn(nullptr, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens,
+                     max_ctx, B, n_q_heads, n_kv_heads, head_dim, scale, workspace,
+                     workspace_bytes, out, stream, rope, plan_batch > 0 ? plan_batch : B);
 }
 
 extern "C" int pdk_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* cache_k,

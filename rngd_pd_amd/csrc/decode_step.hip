@@ -129,13 +129,24 @@ __device__ __forceinline__ uint16_t to_bf(float f) { return (uint16_t)pdk::f32_t
 // With kSplits > 0 the row comes as kSplits fp32 partial sums of the q|k|v
 // projection (split-K, [split][B][ld]): they are added in split order and
 // rounded to bf16 once, the value the unsplit projection would have written.
+//
+// With ssq (kSplits > 0 only) the projection's input was the un-normalised
+// residual and its weights carry the norm's gain: the summed row is scaled by
+// the row's r (pdk::row_rms over ssq [B][n_ssq], K = 16 n_ssq) before the one
+// rounding, the value pdk_decode_attn_rope_rms uses.
 template <int kSplits>
 __global__ void rope_append_kernel(const void* src_, int64_t ld, int64_t split_stride,
                                    uint16_t* q_out, const float* inv_freq, const int32_t* ctx,
                                    const int32_t* tables, int max_blocks, uint16_t* ck,
-                                   uint16_t* cv, int num_blocks, int NH, int NKV, int HD) {
+                                   uint16_t* cv, int num_blocks, int NH, int NKV, int HD,
+                                   const float* ssq, int n_ssq, float eps) {
   const int head = blockIdx.x, b = blockIdx.y, i = threadIdx.x, half = HD >> 1;
   const int pos = ctx[b] - 1;
+  float rb = 1.f;
+  if (kSplits > 0 && ssq) {
+    const pdk::RowRms rr = pdk::row_rms_load(ssq, b, n_ssq, i);
+    rb = pdk::row_rms_finish(rr, ssq, b, n_ssq, 16 * n_ssq, eps, i);
+  }
   // Element c of row b, already rounded to bf16.
   auto val = [&](int64_t c) -> uint16_t {
     if constexpr (kSplits == 0) {
@@ -145,7 +156,7 @@ __global__ void rope_append_kernel(const void* src_, int64_t ld, int64_t split_s
       float sum = p[0];
 #pragma unroll
       for (int s = 1; s < kSplits; ++s) sum += p[s * split_stride];
-      return to_bf(sum);
+      return to_bf(ssq ? sum * rb : sum);
     }
   };
   int blk = -1;
@@ -199,7 +210,36 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* gu, int M, 
   pdk::st16(out + b * M + 8 * c, o);
 }
 
+// ssq[b][t] = the sum over x[b][16t .. 16t+15] (bf16) of x^2, in index order:
+// the per-tile sums of squares a folded RMSNorm's consumer scales rows by.
+__global__ __launch_bounds__(256) void row_ssq_kernel(const uint16_t* x, int B, int H, float* ssq) {
+  const int b = blockIdx.x;
+  for (int t = threadIdx.x; t < H / 16; t += 256) {
+    const uint16_t* p = x + (int64_t)b * H + 16 * t;
+    const v8 lo = pdk::ld16(p), hi = pdk::ld16(p + 8);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const v8& v = k < 4 ? lo : hi;
+      const float a = pdk::bf16_to_f32(v.w[k & 3] & 0xffffu), c = pdk::bf16_to_f32(v.w[k & 3] >> 16);
+      s += a * a;
+      s += c * c;
+    }
+    ssq[(int64_t)b * (H / 16) + t] = s;
+  }
+}
+
 }  // namespace
+
+extern "C" int pdk_row_ssq(const uint16_t* x, int B, int H, float* ssq, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(x && ssq, "null pointer argument");
+  PDK_REQUIRE(B >= 1 && B <= 65535, "B must be in [1, 65535] (got %d)", B);
+  PDK_REQUIRE(H >= 16 && H % 16 == 0, "H must be a positive multiple of 16 (got %d)", H);
+  PDK_REQUIRE(pdk::aligned16(x), "x must be 16-byte aligned");
+  hipLaunchKernelGGL(row_ssq_kernel, dim3(B), dim3(256), 0, pdk::as_stream(stream), x, B, H, ssq);
+  return pdk::check_launch("row_ssq_kernel");
+}
 
 static int check_norm(const void* x, const void* weight, const void* out, int B, int H) {
   PDK_REQUIRE(x && weight && out, "null pointer argument");
@@ -270,7 +310,35 @@ extern "C" int pdk_rope_cache_append(const uint16_t* qkv, int64_t qkv_ld, uint16
   hipLaunchKernelGGL(rope_append_kernel<0>, dim3(n_q_heads + 2 * n_kv_heads, B),
                      dim3(head_dim / 2), 0, pdk::as_stream(stream), qkv, qkv_ld, (int64_t)0,
                      q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v,
-                     num_blocks, n_q_heads, n_kv_heads, head_dim);
+                     num_blocks, n_q_heads, n_kv_heads, head_dim, nullptr, 0, 0.f);
+  return pdk::check_launch("rope_append_kernel");
+}
+
+static int rope_partials(const float* partials, int splits, int N, uint16_t* q_out,
+                         const float* inv_freq, const int32_t* ctx_lens,
+                         const int32_t* block_tables, int max_blocks, uint16_t* cache_k,
+                         uint16_t* cache_v, int num_blocks, int B, int n_q_heads, int n_kv_heads,
+                         int head_dim, const float* ssq, int n_ssq, float eps,
+                         uintptr_t stream) {
+  if (int rc = check_rope(partials, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k,
+                          cache_v, num_blocks, B, n_q_heads, n_kv_heads, head_dim, N))
+    return rc;
+  if (ssq) {
+    PDK_REQUIRE(n_ssq >= 1, "n_ssq must be >= 1 (got %d)", n_ssq);
+    PDK_REQUIRE(eps > 0.f, "eps must be positive");
+    PDK_REQUIRE(head_dim >= 64, "the row scale needs head_dim >= 64 (got %d)", head_dim);
+  }
+  const dim3 grid(n_q_heads + 2 * n_kv_heads, B), block(head_dim / 2);
+  const int64_t stride = (int64_t)B * N;
+  hipStream_t st = pdk::as_stream(stream);
+  switch (splits) {
+    case 1: hipLaunchKernelGGL(rope_append_kernel<1>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim, ssq, n_ssq, eps); break;
+    case 2: hipLaunchKernelGGL(rope_append_kernel<2>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim, ssq, n_ssq, eps); break;
+    case 4: hipLaunchKernelGGL(rope_append_kernel<4>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim, ssq, n_ssq, eps); break;
+    default:
+      pdk::set_error("splits must be 1, 2 or 4 (got %d)", splits);
+      return PDK_EINVAL;
+  }
   return pdk::check_launch("rope_append_kernel");
 }
 
@@ -282,21 +350,21 @@ extern "C" int pdk_rope_cache_append_partials(const float* partials, int splits,
                                               int num_blocks, int B, int n_q_heads,
                                               int n_kv_heads, int head_dim, uintptr_t stream) {
   pdk::clear_error();
-  if (int rc = check_rope(partials, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k,
-                          cache_v, num_blocks, B, n_q_heads, n_kv_heads, head_dim, N))
-    return rc;
-  const dim3 grid(n_q_heads + 2 * n_kv_heads, B), block(head_dim / 2);
-  const int64_t stride = (int64_t)B * N;
-  hipStream_t st = pdk::as_stream(stream);
-  switch (splits) {
-    case 1: hipLaunchKernelGGL(rope_append_kernel<1>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim); break;
-    case 2: hipLaunchKernelGGL(rope_append_kernel<2>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim); break;
-    case 4: hipLaunchKernelGGL(rope_append_kernel<4>, grid, block, 0, st, partials, (int64_t)N, stride, q_out, inv_freq, ctx_lens, block_tables, max_blocks, cache_k, cache_v, num_blocks, n_q_heads, n_kv_heads, head_dim); break;
-    default:
-      pdk::set_error("splits must be 1, 2 or 4 (got %d)", splits);
-      return PDK_EINVAL;
-  }
-  return pdk::check_launch("rope_append_kernel");
+  return rope_partials(partials, splits, N, q_out, inv_freq, ctx_lens, block_tables, max_blocks,
+                       cache_k, cache_v, num_blocks, B, n_q_heads, n_kv_heads, head_dim, nullptr,
+                       0, 0.f, stream);
+}
+
+extern "C" int pdk_rope_cache_append_partials_rms(
+    const float* partials, int splits, int N, const float* ssq, int n_ssq, float eps,
+    uint16_t* q_out, const float* inv_freq, const int32_t* ctx_lens, const int32_t* block_tables,
+    int max_blocks, uint16_t* cache_k, uint16_t* cache_v, int num_blocks, int B, int n_q_heads,
+    int n_kv_heads, int head_dim, uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(ssq, "null pointer argument");
+  return rope_partials(partials, splits, N, q_out, inv_freq, ctx_lens, block_tables, max_blocks,
+                       cache_k, cache_v, num_blocks, B, n_q_heads, n_kv_heads, head_dim, ssq,
+                       n_ssq, eps, stream);
 }
 
 extern "C" int pdk_swiglu(const uint16_t* gate_up, int B, int M, uint16_t* out,

@@ -124,6 +124,42 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// Row scale of an RMSNorm whose gain is folded into the next weights:
+// rsqrt(sum_t ssq[row * n_tiles + t] / K + eps), t < n_tiles, ssq [rows]
+// [n_tiles] holding each 16-column tile's sum of squares of the row. Lane l
+// (l = lane & 31) of a 32-lane group adds tiles l, l + 32, ... in increasing
+// order, then a fixed xor butterfly (every lane of the group ends with the
+// same bits), so the value depends on nothing but the row's data. The 32
+// lanes of the group must all be active. row_rms_load issues the first 256
+// tiles' loads (unconditional, from clamped addresses; one 128-byte line per
+// instruction) and returns at once, so a caller can issue other loads before
+// row_rms_finish waits for these.
+struct RowRms {
+  float v[8];
+};
+
+__device__ __forceinline__ RowRms row_rms_load(const float* ssq, int row, int n_tiles, int lane) {
+  const int l = lane & 31;
+  const float* p = ssq + (int64_t)row * n_tiles;
+  RowRms r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r.v[i] = p[min(l + 32 * i, n_tiles - 1)];
+  return r;
+}
+
+__device__ __forceinline__ float row_rms_finish(const RowRms& r, const float* ssq, int row,
+                                                int n_tiles, int K, float eps, int lane) {
+  const int l = lane & 31;
+  const float* p = ssq + (int64_t)row * n_tiles;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += l + 32 * i < n_tiles ? r.v[i] : 0.f;
+  for (int t = l + 256; t < n_tiles; t += 32) s += p[t];
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o);
+  return rsqrtf(s / (float)K + eps);
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }

@@ -53,13 +53,20 @@ constexpr int kStepK = 128;        // k per wave step: 4 MFMA of 32
 constexpr int kWaves = 8;
 
 // kResidualSsq: kResidual that also writes, per 16-column tile and row, the
-// sum of squares of the bf16 outputs (ssq[tile][row]): the raw material of the
+// sum of squares of the bf16 outputs (ssq[row][tile]): the raw material of the
 // next RMSNorm. kSwiGLURms: kSwiGLU on weights with that norm's gain folded
 // into their columns, whose input x is the un-normalised residual: each row's
-// two sums are scaled by r = rsqrt(sum(ssq[.][row]) / K + eps) before SwiGLU,
+// two sums are scaled by r = rsqrt(sum(ssq[row][.]) / K + eps) before SwiGLU,
 // so rmsnorm(x) . W^T = r * (x . (W diag g)^T) takes no launch of its own.
+//
+// kPartialFinal: kPartial whose last-arriving split of each column group adds
+// the splits' partials in split order to the residual (y = bf16(r + sum), r
+// may alias y: the update pdk_rmsnorm_partials makes) and writes that
+// group's sums of squares as kResidualSsq does, so the next RMSNorm needs no
+// launch. kArgmaxRms: kArgmax on weights with the final norm's gain folded in,
+// each row's logits scaled by its r (from ssq) before rounding.
 enum Epilogue { kPlain = 0, kResidual = 1, kSwiGLU = 2, kArgmax = 3, kPartial = 4,
-                kResidualSsq = 5, kSwiGLURms = 6 };
+                kResidualSsq = 5, kSwiGLURms = 6, kPartialFinal = 7, kArgmaxRms = 8 };
 
 // Greedy-token key of one bf16 logit: the value in an order-preserving code
 // above the complement of the column, so the unsigned maximum is the largest
@@ -91,13 +98,17 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
                                                             int K, int N,
                                                             const uint16_t* r, uint16_t* y,
                                                             uint64_t* keys, float* part,
-                                                            float* ssq, int n_ssq, float eps) {
+                                                            float* ssq, int n_ssq, float eps,
+                                                            int* counters) {
   constexpr bool kGLU = kEpi == kSwiGLU || kEpi == kSwiGLURms;
+  constexpr bool kRowScale = kEpi == kSwiGLURms || kEpi == kArgmaxRms;
+  constexpr bool kArg = kEpi == kArgmax || kEpi == kArgmaxRms;
   constexpr int kPairs = kGLU ? 2 : 1;
   constexpr int kW = kPairs * kCols;                 // W tiles per step
   constexpr int kDepth = depth_for(kTiles + kW);
   __shared__ float red[kWaves][kW][256];
-  __shared__ float rms[kEpi == kSwiGLURms ? 64 : 1];
+  __shared__ float rms[kRowScale ? 64 : 1];
+  __shared__ int is_last;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
   const int n0 = blockIdx.x * 16 * kCols;
@@ -163,17 +174,16 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   constexpr int kTpr = 32, kPer = 8;                 // 32 lanes x 8 tiles per pass
   const int srow = threadIdx.x / kTpr, ssub = threadIdx.x % kTpr;
   float sq_part[kTiles];
-  if constexpr (kEpi == kSwiGLURms) {
+  if constexpr (kRowScale) {
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) sq_part[t] = 0.f;
     for (int base = 0; base < n_ssq; base += kTpr * kPer) {
       float v[kTiles][kPer];
 #pragma unroll
       for (int t = 0; t < kTiles; ++t) {
-        const float* sp = ssq + min(t * 16 + srow, B - 1);
+        const float* sp = ssq + (int64_t)min(t * 16 + srow, B - 1) * n_ssq;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i)
-          v[t][i] = sp[(int64_t)min(base + ssub + i * kTpr, n_ssq - 1) * B];
+        for (int i = 0; i < kPer; ++i) v[t][i] = sp[min(base + ssub + i * kTpr, n_ssq - 1)];
       }
       if (base + kTpr * kPer >= n_ssq) {
 #pragma unroll
@@ -241,6 +251,14 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
         if (ok) part[((int64_t)blockIdx.y * B + m) * N + n] = v[0];
         continue;
       }
+      if (kEpi == kPartialFinal) {
+        // Device-coherent stores: the split that finishes last reads them
+        // from another workgroup, possibly on another XCD.
+        if (ok)
+          __hip_atomic_store(&part[((int64_t)blockIdx.y * B + m) * N + n], v[0], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        continue;
+      }
       float out = v[0];
       if ((kEpi == kResidual || kEpi == kResidualSsq) && ok) out += pdk::bf16_to_f32(r[at]);
       if (kEpi == kSwiGLU) out = v[0] / (1.f + expf(-v[0])) * v[kPairs - 1];
@@ -249,6 +267,7 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
         const float a = v[0] * s, b = v[kPairs - 1] * s;
         out = a / (1.f + expf(-a)) * b;
       }
+      if (kEpi == kArgmaxRms) out = v[0] * rms[m < 64 ? m : 63];
       const uint32_t h = pdk::f32_to_bf16_rne(out);
       if (ok && y) y[at] = (uint16_t)h;
       if (kEpi == kResidualSsq) {
@@ -257,9 +276,9 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
         float sq = ok ? hv * hv : 0.f;
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o);
-        if ((e & 15) == 0 && m < B) ssq[((int64_t)blockIdx.x * kCols + c) * B + m] = sq;
+        if ((e & 15) == 0 && m < B) ssq[(int64_t)m * (N >> 4) + blockIdx.x * kCols + c] = sq;
       }
-      if (kEpi == kArgmax) {
+      if (kArg) {
         // The 16 lanes e .. e|15 hold one row's 16 columns of this tile: the
         // best of them goes to keys[m] (an atomic only when it beats the
         // value already there, so few of the workgroups write).
@@ -277,6 +296,49 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
       }
     }
   }
+  if constexpr (kEpi == kPartialFinal) {
+    // This split's partial stores are complete before it counts itself in
+    // (counters[blockIdx.x] counts the splits of this column group that are
+    // done); the last one resets the count for the next call and finishes the
+    // group. No workgroup waits for another.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int* cnt = counters + blockIdx.x;
+      const int done = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = done == (int)gridDim.y - 1;
+      if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = last;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    const int S = gridDim.y;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+      for (int e = threadIdx.x; e < 256 * kCols; e += kWaves * 64) {
+        const int c = e >> 8, m = t * 16 + ((e >> 4) & 15), n = n0 + 16 * c + (e & 15);
+        const bool ok = m < B && n < N;
+        const int64_t at = (int64_t)min(m, B - 1) * N + min(n, N - 1);
+        float pv[16];
+#pragma unroll
+        for (int sp = 0; sp < 16; ++sp)
+          if (sp < S)
+            pv[sp] = __hip_atomic_load(&part[(int64_t)sp * B * N + at], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        float acc = 0.f;                         // in split order, as pdk_rmsnorm_partials adds
+#pragma unroll
+        for (int sp = 0; sp < 16; ++sp)
+          if (sp < S) acc += pv[sp];
+        const uint32_t h = pdk::f32_to_bf16_rne(pdk::bf16_to_f32(r[at]) + acc);
+        if (ok) y[at] = (uint16_t)h;
+        const float hv = pdk::bf16_to_f32(h);
+        float sq = ok ? hv * hv : 0.f;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o);
+        if ((e & 15) == 0 && m < B) ssq[(int64_t)m * (N >> 4) + blockIdx.x * kCols + c] = sq;
+      }
+    }
+  }
 }
 
 // tokens[b] = the column of keys[b]; keys[b] back to 0 for the next call.
@@ -291,10 +353,11 @@ __global__ void argmax_finish_kernel(uint64_t* keys, int B, int32_t* tokens) {
 template <int kCols, int kEpi, bool kTiled>
 int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
                 uint16_t* y, uint64_t* keys, hipStream_t st, float* part = nullptr,
-                int splits = 1, float* ssq = nullptr, int n_ssq = 0, float eps = 0.f) {
+                int splits = 1, float* ssq = nullptr, int n_ssq = 0, float eps = 0.f,
+                int* counters = nullptr) {
   const dim3 grid((N + 16 * kCols - 1) / (16 * kCols), splits), block(kWaves * 64);
 #define PDK_WGEMM(T) \
-  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part, ssq, n_ssq, eps)
+  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part, ssq, n_ssq, eps, counters)
   switch ((B + 15) / 16) {
     case 1: PDK_WGEMM(1); break;
     case 2: PDK_WGEMM(2); break;
@@ -413,6 +476,42 @@ int linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N, uin
 }
 
 template <bool kTiled>
+int linear_argmax_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N, const float* ssq,
+                      int n_ssq, float eps, uint16_t* logits, uint64_t* keys, int32_t* tokens,
+                      uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_shape(x, w, keys, B, K, N)) return rc;
+  PDK_REQUIRE(tokens && ssq, "null pointer argument");
+  PDK_REQUIRE(((uintptr_t)keys & 7u) == 0, "keys must be 8-byte aligned");
+  PDK_REQUIRE(n_ssq >= 1 && n_ssq * 16 == K, "n_ssq must be K / 16 = %d (got %d)", K / 16, n_ssq);
+  PDK_REQUIRE(eps > 0.f, "eps must be positive");
+  hipStream_t st = pdk::as_stream(stream);
+  if (int rc = launch<kArgmaxRms, kTiled>(x, w, B, K, N, nullptr, logits, keys, st,
+                                          const_cast<float*>(ssq), n_ssq, eps))
+    return rc;
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, keys, B, tokens);
+  return pdk::check_launch("argmax_finish_kernel");
+}
+
+template <bool kTiled>
+int linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int N, int splits,
+                        float* partials, uint16_t* residual, float* ssq, int* counters,
+                        uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_shape(x, w, partials, B, K, N)) return rc;
+  PDK_REQUIRE(residual && ssq && counters, "null pointer argument");
+  PDK_REQUIRE(N % 16 == 0, "N must be a multiple of 16 (got %d)", N);
+  PDK_REQUIRE(splits >= 1 && splits <= 16 && splits <= K / kStepK,
+              "splits must be in [1, min(16, K/%d)] (got %d)", kStepK, splits);
+  hipStream_t st = pdk::as_stream(stream);
+  if (N >= 1024)
+    return launch_cols<4, kPartialFinal, kTiled>(x, w, B, K, N, residual, residual, nullptr, st,
+                                                 partials, splits, ssq, 0, 0.f, counters);
+  return launch_cols<1, kPartialFinal, kTiled>(x, w, B, K, N, residual, residual, nullptr, st,
+                                               partials, splits, ssq, 0, 0.f, counters);
+}
+
+template <bool kTiled>
 int linear_splitk(const uint16_t* x, const uint16_t* w, int B, int K, int N, int splits,
                   float* partials, uintptr_t stream) {
   pdk::clear_error();
@@ -509,6 +608,34 @@ extern "C" int pdk_linear_swiglu_rms_tiled(const uint16_t* x, const uint16_t* wt
                                            int K, int M, const float* ssq, int n_ssq, float eps,
                                            uint16_t* y, uintptr_t stream) {
   return linear_swiglu_rms<true>(x, wt_gate_up, B, K, M, ssq, n_ssq, eps, y, stream);
+}
+
+extern "C" int pdk_linear_argmax_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                                     const float* ssq, int n_ssq, float eps, uint16_t* logits,
+                                     uint64_t* keys, int32_t* tokens, uintptr_t stream) {
+  return linear_argmax_rms<false>(x, w, B, K, N, ssq, n_ssq, eps, logits, keys, tokens, stream);
+}
+
+extern "C" int pdk_linear_argmax_rms_tiled(const uint16_t* x, const uint16_t* wt, int B, int K,
+                                           int N, const float* ssq, int n_ssq, float eps,
+                                           uint16_t* logits, uint64_t* keys, int32_t* tokens,
+                                           uintptr_t stream) {
+  return linear_argmax_rms<true>(x, wt, B, K, N, ssq, n_ssq, eps, logits, keys, tokens, stream);
+}
+
+extern "C" int pdk_linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                                       int splits, float* partials, uint16_t* residual,
+                                       float* ssq, int* counters, uintptr_t stream) {
+  return linear_splitk_final<false>(x, w, B, K, N, splits, partials, residual, ssq, counters,
+                                    stream);
+}
+
+extern "C" int pdk_linear_splitk_final_tiled(const uint16_t* x, const uint16_t* wt, int B, int K,
+                                             int N, int splits, float* partials,
+                                             uint16_t* residual, float* ssq, int* counters,
+                                             uintptr_t stream) {
+  return linear_splitk_final<true>(x, wt, B, K, N, splits, partials, residual, ssq, counters,
+                                   stream);
 }
 
 extern "C" int pdk_linear_splitk_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,

@@ -3,20 +3,27 @@
 Replaces the reference's BatchDecodeEngine.step / step_logits
 (engines/decode_batch.py:422-442) and its compiled DecodeLayer
 (kernels/decode_batch.py:56-91) plus the batched lm_head and greedy argmax
-(engines/decode_batch.py:162-171). Per layer, one launch per line:
+(engines/decode_batch.py:162-171). The two RMSNorms of a layer and the final
+one have no launch of their own: rmsnorm(x) . W^T = r * (x . (W diag g)^T)
+with r = rsqrt(mean(x^2) + eps) per row, so each norm's gain g is folded into
+the columns of the weights that follow it (once, when the decoder is built),
+the kernel that produces x also writes its per-16-column sums of squares
+(ssq), and the kernel that consumes the projection scales each row by r. Per
+layer, one launch per line:
 
-  x = x + sum(partials); h = rmsnorm(x)           pdk_rmsnorm_partials (pdk_rmsnorm at layer 0)
-  qkv = h . Wqkv^T                                 pdk_linear_splitk (fp32 halves of K; one part when K < 4096)
-  RoPE(q, k); new k, v into the paged cache;
-  ao = attention over slots 0..pos                 pdk_decode_attn_rope (+ its merge when split)
-  x = x + ao . Wo^T; ssq = row sums of x^2         pdk_linear_ssq, residual fused
-  a = silu(r h) * (r u), [h; u] = x . (W diag g)^T pdk_linear_swiglu_rms: the norm's gain folded
-      with r = rsqrt(sum ssq / H + eps)            into the gate|up weights, its scale r into
-                                                   the epilogue (rmsnorm(x) . W^T, no launch)
-  partials = a . Wd^T split over K                 pdk_linear_splitk (fp32, joins x in the next norm)
+  qkv = x . (Wqkv diag g1)^T                        pdk_linear_splitk (fp32 halves of K)
+  q, k, v = bf16(r qkv); RoPE(q, k); new k, v
+  into the paged cache; ao = attention over 0..pos  pdk_decode_attn_rope_rms (+ its merge when split)
+  x = x + ao . Wo^T; ssq                            pdk_linear_ssq, residual fused
+  a = silu(r g) * (r u), [g; u] = x . (Wgu diag g2)^T  pdk_linear_swiglu_rms
+  x = x + a . Wd^T; ssq                             pdk_linear_splitk_final: split over K, the last
+                                                    split of each column group adds the partials
+                                                    to x in split order and writes that group's ssq
 
-then the final norm (which adds the last layer's partials) and the lm_head
-GEMM with the first-maximum argmax in its epilogue (pdk_linear_argmax).
+before the first layer pdk_row_ssq gives the embedding rows' ssq, and after
+the last the lm_head GEMM (weights folded with the final norm's gain) scales
+each row's logits by r and takes the first-maximum argmax in its epilogue
+(pdk_linear_argmax_rms).
 Weights are [out, in] contiguous (torch Linear layout) with q|k|v and gate|up
 stacked, so each projection is one pass over its weights. By default the
 decoder streams tiled copies of them (pdk_weight_tile, made once at
@@ -138,7 +145,7 @@ class LlamaDecoder:
             raise ValueError(f"plan_batch={plan_batch} below max_batch={max_batch}")
         self._captured = False
         e = lambda *s: torch.empty(s, dtype=BF16, device=dev)   # noqa: E731
-        self.x, self.h = e(B, H), e(B, H)
+        self.x = e(B, H)
         self.ao = e(B, cfg.n_heads, cfg.head_dim)
         self.act = e(B, cfg.inter)
         self.logits = e(B, cfg.vocab)
@@ -156,9 +163,15 @@ class LlamaDecoder:
         self.qkv_splits = 2 if H // 128 >= 32 else 1
         self.part_qkv = torch.empty((self.qkv_splits, B, cfg.qkv_dim), dtype=torch.float32,
                                     device=dev)
-        # Per 16-column tile and row, the sums of squares the O projection
-        # leaves for the post-attention norm (fused into gate|up).
-        self.ssq = torch.zeros((H // 16, B), dtype=torch.float32, device=dev)
+        # Per 16-column tile and row, the residual's sums of squares: left by
+        # the O projection for the post-attention norm (fused into gate|up),
+        # and by the down projection (pdk_row_ssq before layer 0) for the
+        # pre-attention norm (fused into attention) and the final one (into
+        # the lm_head). The down projection's split counters start at zero
+        # and every call leaves them so.
+        self.ssq = torch.zeros((B, H // 16), dtype=torch.float32, device=dev)
+        self.ssq_a = torch.zeros((B, H // 16), dtype=torch.float32, device=dev)
+        self.counters = torch.zeros(max(1, H // 16), dtype=torch.int32, device=dev)
         self.inv = cfg.inv_freq().to(dev)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
         self._ws = None
@@ -170,22 +183,24 @@ class LlamaDecoder:
         # GEMMs themselves do).
         self.tiled = bool(tiled) and cfg.inter % 16 == 0
         prep = tile_weight if self.tiled else (lambda t: t)
-        # gate|up with the post-attention norm's gain folded into its columns
-        # (a copy in either layout; the originals stay as they are).
-        self._wt = [(prep(w.wqkv[i]), prep(w.wo[i]), prep(fold_norm(w.wgu[i], w.norm2[i])),
-                     prep(w.wd[i])) for i in range(cfg.n_layers)]
-        self._lm_head = prep(w.lm_head)
+        # q|k|v, gate|up and the lm_head with their norms' gains folded into
+        # their columns (copies in either layout; the originals stay as they
+        # are).
+        self._wt = [(prep(fold_norm(w.wqkv[i], w.norm1[i])), prep(w.wo[i]),
+                     prep(fold_norm(w.wgu[i], w.norm2[i])), prep(w.wd[i]))
+                    for i in range(cfg.n_layers)]
+        self._lm_head = prep(fold_norm(w.lm_head, w.norm_f))
         if self.tiled:
             # The copies are written on the current stream; a step may run on
             # another one, so they are complete before the constructor returns.
             torch.cuda.current_stream(dev).synchronize()
         self._gemm = {n: n + "_tiled" if self.tiled else n for n in
-                      ("pdk_linear", "pdk_linear_splitk", "pdk_linear_swiglu",
-                       "pdk_linear_argmax", "pdk_linear_ssq", "pdk_linear_swiglu_rms")}
-        if cfg.hidden % 16:
-            raise ValueError("the fused post-attention norm needs hidden % 16 == 0")
-        self._layers = [tuple(t.data_ptr() for t in (w.norm1[i], wt[0], wt[1], w.norm2[i], wt[2],
-                                                     wt[3], cache.k[i], cache.v[i]))
+                      ("pdk_linear_splitk", "pdk_linear_ssq", "pdk_linear_swiglu_rms",
+                       "pdk_linear_splitk_final", "pdk_linear_argmax_rms")}
+        if cfg.hidden % 16 or cfg.head_dim != 128:
+            raise ValueError("the fused norms need hidden % 16 == 0 and head_dim 128")
+        self._layers = [tuple(t.data_ptr() for t in (wt[0], wt[1], wt[2], wt[3], cache.k[i],
+                                                     cache.v[i]))
                         for i, wt in enumerate(self._wt)]
 
     def reserve(self, max_ctx):
@@ -238,30 +253,29 @@ class LlamaDecoder:
         ws_bytes = ws.numel() * 4 if ws is not None else 0
         mb, nb = tables.shape[1], cache.num_blocks
         tp, cp = tables.data_ptr(), ctx_lens.data_ptr()
-        xp, hp = x.data_ptr(), self.h.data_ptr()
+        xp = x.data_ptr()
         aop, actp, inv = self.ao.data_ptr(), self.act.data_ptr(), self.inv.data_ptr()
         call = _lib.call
         g = self._gemm
-        lin_sk, lin_am = g["pdk_linear_splitk"], g["pdk_linear_argmax"]
-        lin_ssq, lin_swr = g["pdk_linear_ssq"], g["pdk_linear_swiglu_rms"]
-        ssqp = self.ssq.data_ptr()
+        lin_sk, lin_skf = g["pdk_linear_splitk"], g["pdk_linear_splitk_final"]
+        lin_ssq, lin_swr, lin_amr = (g["pdk_linear_ssq"], g["pdk_linear_swiglu_rms"],
+                                     g["pdk_linear_argmax_rms"])
+        ssqp, ssqa, cntp, n_ssq = (self.ssq.data_ptr(), self.ssq_a.data_ptr(),
+                                   self.counters.data_ptr(), H // 16)
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
             torch.index_select(w.embed, 0, tokens.long(), out=x)
+            call("pdk_row_ssq", xp, B, H, ssqa, st)
             partp, sp = self.part.data_ptr(), self.down_splits
             pqp, qs = self.part_qkv.data_ptr(), self.qkv_splits
-            for li, (n1, wqkv, wo, n2, wgu, wd, ck, cv) in enumerate(self._layers):
-                if li:      # the previous layer's down projection joins the residual here
-                    call("pdk_rmsnorm_partials", xp, partp, sp, n1, B, H, eps, hp, st)
-                else:
-                    call("pdk_rmsnorm", xp, None, n1, B, H, eps, hp, st)
-                call(lin_sk, hp, wqkv, B, H, QKV, qs, pqp, st)
-                call("pdk_decode_attn_rope", pqp, qs, inv, ck, cv, nb, tp, mb, cp, int(max_ctx),
-                     B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, self.plan_batch, st)
+            for wqkv, wo, wgu, wd, ck, cv in self._layers:
+                call(lin_sk, xp, wqkv, B, H, QKV, qs, pqp, st)
+                call("pdk_decode_attn_rope_rms", pqp, qs, ssqa, n_ssq, eps, inv, ck, cv, nb, tp,
+                     mb, cp, int(max_ctx), B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop,
+                     self.plan_batch, st)
                 call(lin_ssq, aop, wo, B, NH * HD, H, xp, xp, ssqp, st)
-                call(lin_swr, xp, wgu, B, H, M, ssqp, H // 16, eps, actp, st)
-                call(lin_sk, actp, wd, B, M, H, sp, partp, st)
-            call("pdk_rmsnorm_partials", xp, partp, sp, w.norm_f.data_ptr(), B, H, eps, hp, st)
-            call(lin_am, hp, self._lm_head.data_ptr(), B, H, cfg.vocab,
+                call(lin_swr, xp, wgu, B, H, M, ssqp, n_ssq, eps, actp, st)
+                call(lin_skf, actp, wd, B, M, H, sp, partp, xp, ssqa, cntp, st)
+            call(lin_amr, xp, self._lm_head.data_ptr(), B, H, cfg.vocab, ssqa, n_ssq, eps,
                  self.logits.data_ptr(), self.keys.data_ptr(), self.tokens.data_ptr(), st)
         return self.tokens[:B]
 

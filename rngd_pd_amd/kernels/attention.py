@@ -86,7 +86,7 @@ def decode_attention(q, cache_k, cache_v, block_tables, ctx_lens, max_ctx, scale
 
 def decode_attention_rope(qkv_partials, inv_freq, cache_k, cache_v, block_tables, ctx_lens,
                           max_ctx, n_q_heads, scale=1.0, out=None, workspace=None, stream=None,
-                          plan_batch=0):
+                          plan_batch=0, ssq=None, eps=None):
     """RoPE, the new token's cache write and attention for one layer in one launch.
 
     qkv_partials float32 [splits, B, (n_q + 2 n_kv) D] (split-K partial sums of
@@ -121,6 +121,18 @@ def decode_attention_rope(qkv_partials, inv_freq, cache_k, cache_v, block_tables
             ws = workspace
         else:
             ws = get_workspace(need, cache_k.device)
+    if ssq is not None:
+        _need(ssq, "ssq", torch.float32)
+        if ssq.dim() != 2 or ssq.shape[0] != B or not ssq.is_contiguous():
+            raise ValueError(f"ssq must be contiguous float32 [{B}, H/16]")
+        _lib.call("pdk_decode_attn_rope_rms", qkv_partials.data_ptr(), splits, ssq.data_ptr(),
+                  ssq.shape[1], float(eps), inv_freq.data_ptr(), cache_k.data_ptr(),
+                  cache_v.data_ptr(), nb, block_tables.data_ptr(), block_tables.shape[1],
+                  ctx_lens.data_ptr(), int(max_ctx), B, n_q_heads, H, D, float(scale),
+                  ws.data_ptr() if ws is not None else None,
+                  ws.numel() * ws.element_size() if ws is not None else 0, out.data_ptr(),
+                  int(plan_batch), stream_handle(stream))
+        return out
     _lib.call("pdk_decode_attn_rope", qkv_partials.data_ptr(), splits, inv_freq.data_ptr(),
               cache_k.data_ptr(), cache_v.data_ptr(), nb, block_tables.data_ptr(),
               block_tables.shape[1], ctx_lens.data_ptr(), int(max_ctx), B, n_q_heads, H, D,

@@ -68,11 +68,14 @@ def rope_cache_append(qkv, inv_freq, ctx_lens, block_tables, cache_k, cache_v, n
 
 
 def rope_cache_append_partials(partials, inv_freq, ctx_lens, block_tables, cache_k, cache_v,
-                               n_q_heads, q_out=None, stream=None):
+                               n_q_heads, q_out=None, stream=None, ssq=None, eps=None):
     """rope_cache_append from split-K partial sums of the q|k|v projection.
 
     partials float32 [splits, B, N] (linear_splitk's output, N = (n_q + 2 n_kv)
-    * D), added in split order and rounded to bf16 per element first."""
+    * D), added in split order and rounded to bf16 per element first. With
+    ``ssq`` float32 [B, H/16] (the projection's input was the un-normalised
+    residual, its weights folded with the norm's gain) each row's sum is
+    scaled by r = rsqrt(sum ssq / H + eps) before the rounding."""
     _need(partials, "partials", torch.float32)
     _need(inv_freq, "inv_freq", torch.float32)
     _need(ctx_lens, "ctx_lens", torch.int32)
@@ -90,11 +93,34 @@ def rope_cache_append_partials(partials, inv_freq, ctx_lens, block_tables, cache
         raise ValueError("ctx_lens [B] and contiguous block_tables [B, max_blocks] expected")
     if q_out is None:
         q_out = torch.empty((B, n_q_heads, D), dtype=cache_k.dtype, device=partials.device)
+    if ssq is not None:
+        _need(ssq, "ssq", torch.float32)
+        if ssq.dim() != 2 or ssq.shape[0] != B or not ssq.is_contiguous():
+            raise ValueError(f"ssq must be contiguous float32 [{B}, H/16]")
+        _lib.call("pdk_rope_cache_append_partials_rms", partials.data_ptr(), splits, N,
+                  ssq.data_ptr(), ssq.shape[1], float(eps), q_out.data_ptr(),
+                  inv_freq.data_ptr(), ctx_lens.data_ptr(), block_tables.data_ptr(),
+                  block_tables.shape[1], cache_k.data_ptr(), cache_v.data_ptr(), nb, B,
+                  n_q_heads, Hkv, D, stream_handle(stream))
+        return q_out
     _lib.call("pdk_rope_cache_append_partials", partials.data_ptr(), splits, N, q_out.data_ptr(),
               inv_freq.data_ptr(), ctx_lens.data_ptr(), block_tables.data_ptr(),
               block_tables.shape[1], cache_k.data_ptr(), cache_v.data_ptr(), nb, B, n_q_heads,
               Hkv, D, stream_handle(stream))
     return q_out
+
+
+def row_ssq(x, ssq=None, stream=None):
+    """float32 [B, H/16]: per 16-column tile, the sum of squares of each row
+    of the bf16 x [B, H]."""
+    _need(x, "x")
+    if x.dim() != 2 or not x.is_contiguous() or x.shape[1] % 16:
+        raise ValueError("x must be contiguous [B, H] with H % 16 == 0")
+    B, H = x.shape
+    if ssq is None:
+        ssq = torch.empty((B, H // 16), dtype=torch.float32, device=x.device)
+    _lib.call("pdk_row_ssq", x.data_ptr(), B, H, ssq.data_ptr(), stream_handle(stream))
+    return ssq
 
 
 def swiglu(gate_up, out=None, stream=None):
@@ -196,7 +222,7 @@ def linear_swiglu(x, w_gate_up, out=None, stream=None):
 
 def linear_ssq(x, w, residual, ssq, out=None, stream=None):
     """residual + x . w^T -> [B, N] (``out`` may be ``residual``), and ssq
-    float32 [N/16, B]: per 16-column tile and row, the sum of squares of the
+    float32 [B, N/16]: per row and 16-column tile, the sum of squares of the
     bf16 outputs (the raw material of the next RMSNorm)."""
     B, K, N = _check_linear(x, w)
     _need(residual, "residual")
@@ -227,7 +253,7 @@ def fold_norm(w, g):
 
 
 def linear_swiglu_rms(x, w_gate_up_folded, ssq, eps, out=None, stream=None):
-    """silu(r x . wg'^T) * (r x . wu'^T) -> [B, M], r_b = rsqrt(sum_t ssq[t, b]
+    """silu(r x . wg'^T) * (r x . wu'^T) -> [B, M], r_b = rsqrt(sum_t ssq[b, t]
     / K + eps): the gate|up of rmsnorm(x) * g for weights folded with g
     (fold_norm), ssq from the linear_ssq that produced x."""
     B, K, M = _check_linear(x, w_gate_up_folded, rows_per_col=2)
@@ -242,6 +268,42 @@ def linear_swiglu_rms(x, w_gate_up_folded, ssq, eps, out=None, stream=None):
               w_gate_up_folded.data_ptr(), B, K, M, ssq.data_ptr(), K // 16, float(eps),
               out.data_ptr(), stream_handle(stream))
     return out
+
+
+def linear_splitk_final(x, w, splits, residual, ssq, counters, partials=None, stream=None):
+    """residual += x . w^T in place (bf16(residual + sum of split-K partials in
+    split order), added by the last split of each column group) and ssq
+    float32 [B, N/16] of the result; counters: int32 device zeros (>= N/16),
+    left zero."""
+    B, K, N = _check_linear(x, w)
+    _need(residual, "residual")
+    if tuple(residual.shape) != (B, N) or not residual.is_contiguous():
+        raise ValueError(f"residual must be contiguous [{B}, {N}]")
+    if ssq.dtype != torch.float32 or ssq.numel() < (N // 16) * B or not ssq.is_contiguous():
+        raise ValueError(f"ssq must be contiguous float32 holding {N // 16}x{B}")
+    if counters.dtype != torch.int32 or counters.numel() < N // 16:
+        raise ValueError(f"counters must be int32 holding >= {N // 16} zeros")
+    if partials is None:
+        partials = torch.empty((splits, B, N), dtype=torch.float32, device=x.device)
+    _lib.call(_entry("pdk_linear_splitk_final", w), x.data_ptr(), w.data_ptr(), B, K, N,
+              int(splits), partials.data_ptr(), residual.data_ptr(), ssq.data_ptr(),
+              counters.data_ptr(), stream_handle(stream))
+    return residual
+
+
+def linear_argmax_rms(x, w_folded, ssq, eps, keys, tokens=None, logits=None, stream=None):
+    """linear_argmax of rmsnorm(x) * g for weights folded with g (fold_norm):
+    each row's logits scaled by r from ssq [B, K/16] before rounding."""
+    B, K, N = _check_linear(x, w_folded)
+    if ssq.dtype != torch.float32 or ssq.numel() < (K // 16) * B or not ssq.is_contiguous():
+        raise ValueError(f"ssq must be contiguous float32 holding {K // 16}x{B}")
+    if tokens is None:
+        tokens = torch.empty(B, dtype=torch.int32, device=x.device)
+    _lib.call(_entry("pdk_linear_argmax_rms", w_folded), x.data_ptr(), w_folded.data_ptr(), B, K,
+              N, ssq.data_ptr(), K // 16, float(eps),
+              logits.data_ptr() if logits is not None else None, keys.data_ptr(),
+              tokens.data_ptr(), stream_handle(stream))
+    return tokens
 
 
 def linear_argmax(x, w, keys, tokens=None, logits=None, stream=None):

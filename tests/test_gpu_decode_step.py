@@ -186,6 +186,156 @@ def test_fused_rope_attention_equals_two_calls(cuda, B, splits, NH, NKV):
     np.testing.assert_array_equal(to_host(cv_b), to_host(cv_a))
 
 
+def _rand_ssq(rng, n_tiles, B):
+    """[B, n_tiles] per-tile sums of squares of plausible residual rows."""
+    return (rng.chisquare(16, (B, n_tiles)) * rng.uniform(0.1, 3.0, (B, 1))).astype(np.float32)
+
+
+def _host_rms(ssq, K, eps):
+    """The row scale in fp64 (the kernels sum in fp32 in a fixed order)."""
+    return 1.0 / np.sqrt(ssq.astype(np.float64).sum(1) / K + eps)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_rope_from_partials_with_row_scale(cuda, splits):
+    """With the pre-attention norm folded, each row's summed partials are
+    scaled by the row's r before the one rounding: q, the cache's new k and v
+    equal rope_cache_append on bf16(r * sum) rows, within the fp32 rounding of
+    r (compared exactly on the rows the kernel's r reproduces)."""
+    from rngd_pd_amd import kernels as K
+    NH, NKV, D, H = 8, 2, 128, 4096
+    positions = [0, 17, 511, 4000]
+    B = len(positions)
+    rng = np.random.default_rng(700 + splits)
+    max_blocks = max(positions) // 16 + 1
+    nb = 2 * B + 1
+    tables = np.zeros((B, max_blocks), np.int32)
+    own = rng.permutation(np.arange(1, nb))[:B]
+    for b, p in enumerate(positions):
+        tables[b, p // 16] = own[b]
+    N = (NH + 2 * NKV) * D
+    part = (rng.standard_normal((splits, B, N)) * 3).astype(np.float32)
+    ssq = _rand_ssq(rng, H // 16, B)
+    eps = 1e-5
+    total = part[0].copy()
+    for s in range(1, splits):
+        total = total + part[s]
+    r = _host_rms(ssq, H, eps).astype(np.float32)
+    ck0, cv0 = rand_bf16(rng, (nb, NKV, 16, D)), rand_bf16(rng, (nb, NKV, D, 16))
+    inv = torch.from_numpy(od.inv_freq(D, 500000.0, LLAMA3)).to(cuda)
+    ctx = torch.tensor([p + 1 for p in positions], dtype=torch.int32, device=cuda)
+    tab = torch.from_numpy(tables).to(cuda)
+    print(f"rope partials with row scale, splits={splits}", flush=True)
+    ck_a, cv_a = to_dev(ck0), to_dev(cv0)
+    K.rope_cache_append_partials(torch.from_numpy(part).to(cuda), inv, ctx, tab, ck_a, cv_a, NH,
+                                 ssq=torch.from_numpy(ssq).to(cuda), eps=eps)
+    torch.cuda.synchronize()
+    got_v = _f32(to_host(cv_a))
+    for b, p in enumerate(positions):
+        want = (total[b, (NH + NKV) * D:] * r[b]).reshape(NKV, D)
+        np.testing.assert_allclose(got_v[own[b], :, :, p % 16], want, rtol=2 * HALF_ULP, atol=0)
+
+
+@pytest.mark.parametrize("B,splits,H", [(16, 2, 4096), (4, 2, 4096), (5, 4, 512), (1, 1, 8192)])
+def test_fused_rope_attention_with_row_scale_equals_two_calls(cuda, B, splits, H):
+    """pdk_decode_attn_rope_rms against pdk_rope_cache_append_partials_rms
+    followed by pdk_decode_attn: bit-identical outputs and cache contents (the
+    two compute each row's scale in the same fixed order)."""
+    from rngd_pd_amd import kernels as K
+    NH, NKV, D = 32, 8, 128
+    ctx = [1, 16, 17, 512, 511, 300, 1000, 33, 64, 129, 700, 2, 48, 250, 999, 15][:B]
+    rng = np.random.default_rng(900 + B + splits + H)
+    max_blocks = (max(ctx) + 15) // 16
+    nb = B * max_blocks + 3
+    tables = rng.permutation(nb)[:B * max_blocks].astype(np.int32).reshape(B, max_blocks)
+    N = (NH + 2 * NKV) * D
+    part_d = torch.from_numpy((rng.standard_normal((splits, B, N)) * 2).astype(np.float32)).to(cuda)
+    ssq = torch.from_numpy(_rand_ssq(rng, H // 16, B)).to(cuda)
+    ck0, cv0 = rand_bf16(rng, (nb, NKV, 16, D)), rand_bf16(rng, (nb, NKV, D, 16))
+    inv = torch.from_numpy(od.inv_freq(D, 500000.0, LLAMA3)).to(cuda)
+    ctx_t = torch.tensor(ctx, dtype=torch.int32, device=cuda)
+    tab = torch.from_numpy(tables).to(cuda)
+    scale = 1.0 / math.sqrt(D)
+    print(f"fused rope+attention with row scale B={B} splits={splits} H={H}", flush=True)
+    ck_a, cv_a = to_dev(ck0), to_dev(cv0)
+    q = K.rope_cache_append_partials(part_d, inv, ctx_t, tab, ck_a, cv_a, NH, ssq=ssq, eps=1e-5)
+    out_a = K.decode_attention(q, ck_a, cv_a, tab, ctx_t, max(ctx), scale=scale)
+    ck_b, cv_b = to_dev(ck0), to_dev(cv0)
+    out_b = K.decode_attention_rope(part_d, inv, ck_b, cv_b, tab, ctx_t, max(ctx), NH,
+                                    scale=scale, ssq=ssq, eps=1e-5)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(out_b), to_host(out_a))
+    np.testing.assert_array_equal(to_host(ck_b), to_host(ck_a))
+    np.testing.assert_array_equal(to_host(cv_b), to_host(cv_a))
+
+
+@pytest.mark.parametrize("B,H", [(16, 4096), (3, 512), (64, 8192), (1, 16)])
+def test_row_ssq(cuda, B, H):
+    from rngd_pd_amd import kernels as K
+    rng = np.random.default_rng(B + H)
+    x = rand_bf16(rng, (B, H), 3.0)
+    print(f"row_ssq B={B} H={H}", flush=True)
+    got = K.row_ssq(to_dev(x)).cpu().numpy()
+    want = (_f32(x).astype(np.float64).reshape(B, H // 16, 16) ** 2).sum(-1)
+    np.testing.assert_allclose(got, want, rtol=1e-6)
+
+
+@pytest.mark.parametrize("B,K,N,splits", [(16, 14336, 4096, 4), (4, 14336, 4096, 4),
+                                          (3, 1024, 512, 8), (33, 512, 2048, 2), (1, 128, 16, 1)])
+def test_linear_splitk_final(cuda, B, K, N, splits):
+    """The down projection with the residual add of the next norm: residual
+    bit-identical to linear_splitk + rmsnorm_partials' update, ssq the sums
+    of squares of the result, the counters back at zero, and the same on a
+    second call and on tiled weights."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B * 5 + K + N + splits)
+    w = rand_bf16(rng, (N, K), 0.05)
+    wd = to_dev(w)
+    counters = torch.zeros(N // 16, dtype=torch.int32, device=cuda)
+    ones = torch.ones(N, dtype=BF16, device=cuda)
+    print(f"linear_splitk_final B={B} K={K} N={N} splits={splits}", flush=True)
+    for call, wgt in enumerate((wd, K_.tile_weight(wd), wd)):
+        x, r = rand_bf16(rng, (B, K)), rand_bf16(rng, (B, N), 4.0)
+        xd = to_dev(x)
+        want = to_dev(r)
+        parts = K_.linear_splitk(xd, wd, splits)
+        K_.rmsnorm_partials(want, parts, splits, ones, 1e-5)
+        got = to_dev(r)
+        ssq = torch.full((B, N // 16), float("nan"), dtype=torch.float32, device=cuda)
+        K_.linear_splitk_final(xd, wgt, splits, got, ssq, counters)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), call
+        gf = _f32(to_host(got)).astype(np.float64)
+        np.testing.assert_allclose(ssq.cpu().numpy(), (gf.reshape(B, N // 16, 16) ** 2).sum(-1),
+                                   rtol=1e-6, atol=1e-30)
+        assert int(counters.abs().sum()) == 0, call
+
+
+@pytest.mark.parametrize("B,K,N", [(16, 4096, 128256), (4, 4096, 128256), (3, 256, 1000)])
+def test_linear_argmax_rms(cuda, B, K, N):
+    """The lm_head on weights folded with the final norm's gain: logits within
+    half an ulp of r * (x . w'^T) in fp64, tokens the first maximum of those
+    bf16 logits (pdk_greedy_argmax on the same logits)."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B + K + N + 1)
+    x, w = rand_bf16(rng, (B, K), 2.0), rand_bf16(rng, (N, K), 0.05)
+    ssq = _rand_ssq(rng, K // 16, B)
+    eps = 1e-5
+    wd = to_dev(w)
+    keys = torch.zeros(B, dtype=torch.int64, device=cuda)
+    logits = torch.empty((B, N), dtype=BF16, device=cuda)
+    print(f"linear_argmax_rms B={B} K={K} N={N}", flush=True)
+    tok = K_.linear_argmax_rms(to_dev(x), K_.tile_weight(wd), torch.from_numpy(ssq).to(cuda), eps,
+                               keys, logits=logits)
+    want_tok = K_.greedy_argmax(logits)
+    torch.cuda.synchronize()
+    assert torch.equal(tok.cpu(), want_tok.cpu().to(torch.int32))
+    assert int(keys.abs().sum()) == 0
+    r = _host_rms(ssq, K, eps)
+    ref = (_f32(x).astype(np.float64) @ _f32(w).astype(np.float64).T) * r[:, None]
+    np.testing.assert_allclose(_f32(to_host(logits)), ref, rtol=HALF_ULP, atol=1e-3 * np.abs(ref).max())
+
+
 @pytest.mark.parametrize("B,M", [(3, 14336), (1, 8), (16, 1024)])
 def test_swiglu(cuda, B, M):
     from rngd_pd_amd import kernels as K
@@ -282,14 +432,14 @@ def test_linear_ssq(cuda, B, K, N):
     outs = []
     for wgt in (wd, K_.tile_weight(wd)):
         rd = to_dev(r)
-        ssq = torch.full((N // 16, B), float("nan"), dtype=torch.float32, device=cuda)
+        ssq = torch.full((B, N // 16), float("nan"), dtype=torch.float32, device=cuda)
         y = K_.linear_ssq(xd, wgt, rd, ssq, out=rd)            # in place, as the decoder runs it
         outs.append((y, ssq))
     torch.cuda.synchronize()
     for y, ssq in outs:
         assert torch.equal(y.view(torch.int16), want_y.view(torch.int16))
         yf = _f32(to_host(y)).astype(np.float64)
-        want = (yf.reshape(B, N // 16, 16) ** 2).sum(-1).T
+        want = (yf.reshape(B, N // 16, 16) ** 2).sum(-1)
         np.testing.assert_allclose(ssq.cpu().numpy(), want, rtol=1e-6, atol=1e-30)
     assert torch.equal(outs[0][1], outs[1][1])
 
@@ -310,7 +460,7 @@ def test_linear_swiglu_rms(cuda, B, K, M):
     eps = 1e-5
     xd, wd, gd = to_dev(x), to_dev(w), to_dev(g)
     xf = _f32(x).astype(np.float64)
-    ssq = torch.from_numpy((xf.reshape(B, K // 16, 16) ** 2).sum(-1).T.astype(np.float32))
+    ssq = torch.from_numpy((xf.reshape(B, K // 16, 16) ** 2).sum(-1).astype(np.float32))
     ssq = ssq.contiguous().to(cuda)
     print(f"linear_swiglu_rms B={B} K={K} M={M}", flush=True)
     wf = K_.fold_norm(wd, gd)
@@ -321,7 +471,7 @@ def test_linear_swiglu_rms(cuda, B, K, M):
     y_ref = K_.linear_swiglu(h, wd)
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int16), y_t.view(torch.int16))
-    r = 1.0 / np.sqrt(ssq.cpu().numpy().astype(np.float64).sum(0) / K + eps)     # [B]
+    r = 1.0 / np.sqrt(ssq.cpu().numpy().astype(np.float64).sum(1) / K + eps)     # [B]
     gu = (xf @ _f32(to_host(wf)).astype(np.float64).T) * r[:, None]
     want = od.swiglu(gu)
     tol = 1e-5 * np.abs(gu).max() ** 2
