@@ -414,6 +414,18 @@ int pdk_linear_swiglu_rms_tiled(const uint16_t* x, const uint16_t* wt_gate_up, i
                                 int K, int M, const float* ssq, int n_ssq, float eps,
                                 uint16_t* y, uintptr_t stream);
 
+/* pdk_linear_splitk on weights carrying an RMSNorm's gain, x the
+ * un-normalised residual: each row's partials are scaled by its r (ssq
+ * [B][K/16], as pdk_linear_swiglu_rms), so the splits' sum is the projection
+ * of the normalised row (the q|k|v projection after the pre-attention norm,
+ * kernels/decode_batch.py:73-80 with rms_dsl folded). */
+int pdk_linear_splitk_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                          int splits, const float* ssq, int n_ssq, float eps,
+                          float* partials, uintptr_t stream);
+int pdk_linear_splitk_rms_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                                int splits, const float* ssq, int n_ssq, float eps,
+                                float* partials, uintptr_t stream);
+
 /* The down projection and the next RMSNorm's residual add in one launch:
  * pdk_linear_splitk whose last split to finish, per group of columns, adds the
  * splits' partials in split order to `residual` in place (residual =

@@ -110,6 +110,8 @@ SIGNATURES = {
     "pdk_linear_ssq_tiled": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _U]),
     "pdk_linear_swiglu_rms": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _U]),
     "pdk_linear_swiglu_rms_tiled": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _U]),
+    "pdk_linear_splitk_rms": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _F, _P, _U]),
+    "pdk_linear_splitk_rms_tiled": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _F, _P, _U]),
     "pdk_linear_splitk_final": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _U]),
     "pdk_linear_splitk_final_tiled": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _U]),
     "pdk_linear_argmax_rms": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _P, _P, _U]),

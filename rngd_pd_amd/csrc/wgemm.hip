@@ -64,9 +64,12 @@ constexpr int kWaves = 8;
 // may alias y: the update pdk_rmsnorm_partials makes) and writes that
 // group's sums of squares as kResidualSsq does, so the next RMSNorm needs no
 // launch. kArgmaxRms: kArgmax on weights with the final norm's gain folded in,
-// each row's logits scaled by its r (from ssq) before rounding.
+// each row's logits scaled by its r (from ssq) before rounding. kPartialRms:
+// kPartial on weights with a norm's gain folded in, each row's partial scaled
+// by its r (the q|k|v projection: its consumer adds the scaled halves).
 enum Epilogue { kPlain = 0, kResidual = 1, kSwiGLU = 2, kArgmax = 3, kPartial = 4,
-                kResidualSsq = 5, kSwiGLURms = 6, kPartialFinal = 7, kArgmaxRms = 8 };
+                kResidualSsq = 5, kSwiGLURms = 6, kPartialFinal = 7, kArgmaxRms = 8,
+                kPartialRms = 9 };
 
 // Greedy-token key of one bf16 logit: the value in an order-preserving code
 // above the complement of the column, so the unsigned maximum is the largest
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
                                                             float* ssq, int n_ssq, float eps,
                                                             int* counters) {
   constexpr bool kGLU = kEpi == kSwiGLU || kEpi == kSwiGLURms;
-  constexpr bool kRowScale = kEpi == kSwiGLURms || kEpi == kArgmaxRms;
+  constexpr bool kRowScale = kEpi == kSwiGLURms || kEpi == kArgmaxRms || kEpi == kPartialRms;
   constexpr bool kArg = kEpi == kArgmax || kEpi == kArgmaxRms;
   constexpr int kPairs = kGLU ? 2 : 1;
   constexpr int kW = kPairs * kCols;                 // W tiles per step
@@ -247,8 +250,9 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
         v[p] = sum;
       }
       const int64_t at = (int64_t)m * N + n;
-      if (kEpi == kPartial) {
-        if (ok) part[((int64_t)blockIdx.y * B + m) * N + n] = v[0];
+      if (kEpi == kPartial || kEpi == kPartialRms) {
+        const float pv = kEpi == kPartialRms ? v[0] * rms[m < 64 ? m : 63] : v[0];
+        if (ok) part[((int64_t)blockIdx.y * B + m) * N + n] = pv;
         continue;
       }
       if (kEpi == kPartialFinal) {
@@ -494,6 +498,25 @@ int linear_argmax_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N,
 }
 
 template <bool kTiled>
+int linear_splitk_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N, int splits,
+                      const float* ssq, int n_ssq, float eps, float* partials, uintptr_t stream) {
+  pdk::clear_error();
+  if (int rc = check_shape(x, w, partials, B, K, N)) return rc;
+  PDK_REQUIRE(ssq, "null pointer argument");
+  PDK_REQUIRE(n_ssq >= 1 && n_ssq * 16 == K, "n_ssq must be K / 16 = %d (got %d)", K / 16, n_ssq);
+  PDK_REQUIRE(eps > 0.f, "eps must be positive");
+  PDK_REQUIRE(splits >= 1 && splits <= 16 && splits <= K / kStepK,
+              "splits must be in [1, min(16, K/%d)] (got %d)", kStepK, splits);
+  hipStream_t st = pdk::as_stream(stream);
+  float* q = const_cast<float*>(ssq);
+  if (N >= 1024)
+    return launch_cols<4, kPartialRms, kTiled>(x, w, B, K, N, nullptr, nullptr, nullptr, st,
+                                               partials, splits, q, n_ssq, eps);
+  return launch_cols<1, kPartialRms, kTiled>(x, w, B, K, N, nullptr, nullptr, nullptr, st,
+                                             partials, splits, q, n_ssq, eps);
+}
+
+template <bool kTiled>
 int linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int N, int splits,
                         float* partials, uint16_t* residual, float* ssq, int* counters,
                         uintptr_t stream) {
@@ -621,6 +644,18 @@ extern "C" int pdk_linear_argmax_rms_tiled(const uint16_t* x, const uint16_t* wt
                                            uint16_t* logits, uint64_t* keys, int32_t* tokens,
                                            uintptr_t stream) {
   return linear_argmax_rms<true>(x, wt, B, K, N, ssq, n_ssq, eps, logits, keys, tokens, stream);
+}
+
+extern "C" int pdk_linear_splitk_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N,
+                                     int splits, const float* ssq, int n_ssq, float eps,
+                                     float* partials, uintptr_t stream) {
+  return linear_splitk_rms<false>(x, w, B, K, N, splits, ssq, n_ssq, eps, partials, stream);
+}
+
+extern "C" int pdk_linear_splitk_rms_tiled(const uint16_t* x, const uint16_t* wt, int B, int K,
+                                           int N, int splits, const float* ssq, int n_ssq,
+                                           float eps, float* partials, uintptr_t stream) {
+  return linear_splitk_rms<true>(x, wt, B, K, N, splits, ssq, n_ssq, eps, partials, stream);
 }
 
 extern "C" int pdk_linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int N,

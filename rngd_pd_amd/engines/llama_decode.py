@@ -11,9 +11,9 @@ the kernel that produces x also writes its per-16-column sums of squares
 (ssq), and the kernel that consumes the projection scales each row by r. Per
 layer, one launch per line:
 
-  qkv = x . (Wqkv diag g1)^T                        pdk_linear_splitk (fp32 halves of K)
-  q, k, v = bf16(r qkv); RoPE(q, k); new k, v
-  into the paged cache; ao = attention over 0..pos  pdk_decode_attn_rope_rms (+ its merge when split)
+  qkv halves = r x . (Wqkv diag g1)^T              pdk_linear_splitk_rms (fp32 halves of K, rows scaled)
+  q, k, v = bf16(sum of halves); RoPE(q, k); new
+  k, v into the paged cache; ao = attention        pdk_decode_attn_rope (+ its merge when split)
   x = x + ao . Wo^T; ssq                            pdk_linear_ssq, residual fused
   a = silu(r g) * (r u), [g; u] = x . (Wgu diag g2)^T  pdk_linear_swiglu_rms
   x = x + a . Wd^T; ssq                             pdk_linear_splitk_final: split over K, the last
@@ -195,7 +195,7 @@ class LlamaDecoder:
             # another one, so they are complete before the constructor returns.
             torch.cuda.current_stream(dev).synchronize()
         self._gemm = {n: n + "_tiled" if self.tiled else n for n in
-                      ("pdk_linear_splitk", "pdk_linear_ssq", "pdk_linear_swiglu_rms",
+                      ("pdk_linear_splitk_rms", "pdk_linear_ssq", "pdk_linear_swiglu_rms",
                        "pdk_linear_splitk_final", "pdk_linear_argmax_rms")}
         if cfg.hidden % 16 or cfg.head_dim != 128:
             raise ValueError("the fused norms need hidden % 16 == 0 and head_dim 128")
@@ -257,7 +257,7 @@ class LlamaDecoder:
         aop, actp, inv = self.ao.data_ptr(), self.act.data_ptr(), self.inv.data_ptr()
         call = _lib.call
         g = self._gemm
-        lin_sk, lin_skf = g["pdk_linear_splitk"], g["pdk_linear_splitk_final"]
+        lin_skr, lin_skf = g["pdk_linear_splitk_rms"], g["pdk_linear_splitk_final"]
         lin_ssq, lin_swr, lin_amr = (g["pdk_linear_ssq"], g["pdk_linear_swiglu_rms"],
                                      g["pdk_linear_argmax_rms"])
         ssqp, ssqa, cntp, n_ssq = (self.ssq.data_ptr(), self.ssq_a.data_ptr(),
@@ -268,10 +268,9 @@ class LlamaDecoder:
             partp, sp = self.part.data_ptr(), self.down_splits
             pqp, qs = self.part_qkv.data_ptr(), self.qkv_splits
             for wqkv, wo, wgu, wd, ck, cv in self._layers:
-                call(lin_sk, xp, wqkv, B, H, QKV, qs, pqp, st)
-                call("pdk_decode_attn_rope_rms", pqp, qs, ssqa, n_ssq, eps, inv, ck, cv, nb, tp,
-                     mb, cp, int(max_ctx), B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop,
-                     self.plan_batch, st)
+                call(lin_skr, xp, wqkv, B, H, QKV, qs, ssqa, n_ssq, eps, pqp, st)
+                call("pdk_decode_attn_rope", pqp, qs, inv, ck, cv, nb, tp, mb, cp, int(max_ctx),
+                     B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, self.plan_batch, st)
                 call(lin_ssq, aop, wo, B, NH * HD, H, xp, xp, ssqp, st)
                 call(lin_swr, xp, wgu, B, H, M, ssqp, n_ssq, eps, actp, st)
                 call(lin_skf, actp, wd, B, M, H, sp, partp, xp, ssqa, cntp, st)

@@ -270,6 +270,20 @@ def linear_swiglu_rms(x, w_gate_up_folded, ssq, eps, out=None, stream=None):
     return out
 
 
+def linear_splitk_rms(x, w_folded, splits, ssq, eps, partials=None, stream=None):
+    """linear_splitk of rmsnorm(x) * g for weights folded with g (fold_norm):
+    each row's partials scaled by r from ssq [B, K/16]."""
+    B, K, N = _check_linear(x, w_folded)
+    if ssq.dtype != torch.float32 or ssq.numel() < (K // 16) * B or not ssq.is_contiguous():
+        raise ValueError(f"ssq must be contiguous float32 holding {B}x{K // 16}")
+    if partials is None:
+        partials = torch.empty((splits, B, N), dtype=torch.float32, device=x.device)
+    _lib.call(_entry("pdk_linear_splitk_rms", w_folded), x.data_ptr(), w_folded.data_ptr(), B, K,
+              N, int(splits), ssq.data_ptr(), K // 16, float(eps), partials.data_ptr(),
+              stream_handle(stream))
+    return partials
+
+
 def linear_splitk_final(x, w, splits, residual, ssq, counters, partials=None, stream=None):
     """residual += x . w^T in place (bf16(residual + sum of split-K partials in
     split order), added by the last split of each column group) and ssq

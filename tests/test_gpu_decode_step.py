@@ -269,6 +269,29 @@ def test_fused_rope_attention_with_row_scale_equals_two_calls(cuda, B, splits, H
     np.testing.assert_array_equal(to_host(cv_b), to_host(cv_a))
 
 
+@pytest.mark.parametrize("B,K,N,splits", [(16, 4096, 6144, 2), (4, 4096, 6144, 2),
+                                          (3, 512, 1536, 1), (40, 1024, 512, 4)])
+def test_linear_splitk_rms(cuda, B, K, N, splits):
+    """The q|k|v projection after the folded pre-attention norm: each row's
+    partials are the plain split-K partials times the row's r (the same fp32
+    sums, one more product), tiled and untiled alike."""
+    from rngd_pd_amd import kernels as K_
+    rng = np.random.default_rng(B * 3 + K + N + splits)
+    x, w = rand_bf16(rng, (B, K), 2.0), rand_bf16(rng, (N, K), 0.05)
+    ssq = _rand_ssq(rng, K // 16, B)
+    eps = 1e-5
+    xd, wd, sd = to_dev(x), to_dev(w), torch.from_numpy(ssq).to(cuda)
+    print(f"linear_splitk_rms B={B} K={K} N={N} splits={splits}", flush=True)
+    plain = K_.linear_splitk(xd, wd, splits)
+    got = K_.linear_splitk_rms(xd, wd, splits, sd, eps)
+    got_t = K_.linear_splitk_rms(xd, K_.tile_weight(wd), splits, sd, eps)
+    torch.cuda.synchronize()
+    assert torch.equal(got, got_t)
+    r = _host_rms(ssq, K, eps)
+    np.testing.assert_allclose(got.cpu().numpy(), plain.cpu().numpy() * r[None, :, None],
+                               rtol=2e-6, atol=1e-30)
+
+
 @pytest.mark.parametrize("B,H", [(16, 4096), (3, 512), (64, 8192), (1, 16)])
 def test_row_ssq(cuda, B, H):
     from rngd_pd_amd import kernels as K
