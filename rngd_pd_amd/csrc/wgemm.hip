@@ -168,41 +168,57 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
 #pragma unroll
       for (int c = 0; c < 4; ++c) xv[slot][t][c] = pdk::ld16(xp[t] + k + 32 * c);
   };
-  // Row scales of kSwiGLURms: 32 lanes per row (16 rows per pass over the
+  // Row scales (kRowScale): 32 lanes per row (16 rows per pass over the
   // workgroup, kTiles passes), each adding every 32nd tile's sum of squares,
   // then a fixed butterfly: a row's scale depends neither on B nor on timing.
   // A lane's loads are issued before the first steps' weight loads
-  // (unconditional, from clamped addresses), so waiting for them costs no
-  // more than waiting for those.
+  // (unconditional, from clamped addresses). With at most 256 tiles and one row
+  // tile (two, but for the register-heavy SwiGLU epilogue) the values stay in registers and are summed in the epilogue, so
+  // nothing waits for them before the main loop; otherwise they are summed
+  // right after the first weight loads are issued.
   constexpr int kTpr = 32, kPer = 8;                 // 32 lanes x 8 tiles per pass
+  constexpr bool kLate = kRowScale && (kTiles == 1 || (kTiles == 2 && kEpi != kSwiGLURms));
   const int srow = threadIdx.x / kTpr, ssub = threadIdx.x % kTpr;
-  float sq_part[kTiles];
+  const bool late = kLate && n_ssq <= kTpr * kPer;
+  float sv[kLate ? kTiles : 1][kPer];
   if constexpr (kRowScale) {
+    if (late) {
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) sq_part[t] = 0.f;
-    for (int base = 0; base < n_ssq; base += kTpr * kPer) {
-      float v[kTiles][kPer];
-#pragma unroll
-      for (int t = 0; t < kTiles; ++t) {
+      for (int t = 0; t < (kLate ? kTiles : 1); ++t) {
         const float* sp = ssq + (int64_t)min(t * 16 + srow, B - 1) * n_ssq;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) v[t][i] = sp[min(base + ssub + i * kTpr, n_ssq - 1)];
-      }
-      if (base + kTpr * kPer >= n_ssq) {
-#pragma unroll
-        for (int d = 0; d < kDepth; ++d) load(d, d);
+        for (int i = 0; i < kPer; ++i) sv[t][i] = sp[min(ssub + i * kTpr, n_ssq - 1)];
       }
 #pragma unroll
-      for (int t = 0; t < kTiles; ++t)
+      for (int d = 0; d < kDepth; ++d) load(d, d);
+    } else {
+      float sq_part[kTiles];
 #pragma unroll
-        for (int i = 0; i < kPer; ++i)
-          sq_part[t] += base + ssub + i * kTpr < n_ssq ? v[t][i] : 0.f;
-    }
+      for (int t = 0; t < kTiles; ++t) sq_part[t] = 0.f;
+      for (int base = 0; base < n_ssq; base += kTpr * kPer) {
+        float v[kTiles][kPer];
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
+        for (int t = 0; t < kTiles; ++t) {
+          const float* sp = ssq + (int64_t)min(t * 16 + srow, B - 1) * n_ssq;
 #pragma unroll
-      for (int o = 1; o < kTpr; o <<= 1) sq_part[t] += __shfl_xor(sq_part[t], o);
-      if (ssub == 0) rms[t * 16 + srow] = rsqrtf(sq_part[t] / (float)K + eps);
+          for (int i = 0; i < kPer; ++i) v[t][i] = sp[min(base + ssub + i * kTpr, n_ssq - 1)];
+        }
+        if (base + kTpr * kPer >= n_ssq) {
+#pragma unroll
+          for (int d = 0; d < kDepth; ++d) load(d, d);
+        }
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+          for (int i = 0; i < kPer; ++i)
+            sq_part[t] += base + ssub + i * kTpr < n_ssq ? v[t][i] : 0.f;
+      }
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+        for (int o = 1; o < kTpr; o <<= 1) sq_part[t] += __shfl_xor(sq_part[t], o);
+        if (ssub == 0) rms[t * 16 + srow] = rsqrtf(sq_part[t] / (float)K + eps);
+      }
     }
   } else {
 #pragma unroll
@@ -228,6 +244,19 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
     }
   }
 
+  if constexpr (kLate) {
+    if (late) {                              // the same sums in the same order, now
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+        float sq = 0.f;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) sq += ssub + i * kTpr < n_ssq ? sv[t][i] : 0.f;
+#pragma unroll
+        for (int o = 1; o < kTpr; o <<= 1) sq += __shfl_xor(sq, o);
+        if (ssub == 0) rms[t * 16 + srow] = rsqrtf(sq / (float)K + eps);
+      }
+    }
+  }
   // acc[q][t][i] = partial Y[t*16 + 4*kg + i][column tile q, column col]; one
   // row tile at a time through LDS, summed over the waves.
 #pragma unroll
