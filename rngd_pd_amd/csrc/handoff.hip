@@ -44,12 +44,17 @@ constexpr int64_t kStreamBytes = 256ll << 20;   // the MI355X last-level (Infini
 
 // Requests of a batched launch are laid end to end over grid.x: request r owns
 // wavefront tiles off[r] .. off[r+1]-1, so a launch holds only tiles with
-// work, however different the requests' lengths are.
+// work, however different the requests' lengths are. Pack lays out the
+// tiles that move tokens first (off[]), for all requests, and the zero-fill
+// chunks of the frames' tails after them (zoff[], counted from off[n_req]): on
+// the 8-request Llama-3.1-8B batch that is 2-5 us faster (of about 145) than
+// each request's zero chunks right after its own tiles.
 struct PackArgs {
   pdk_pack_req req[PDK_MAX_BATCH];
   int64_t off[PDK_MAX_BATCH + 1];
+  int64_t zoff[PDK_MAX_BATCH + 1];
   int32_t nT[PDK_MAX_BATCH];     // 64-token tiles of request r holding valid tokens
-  int32_t nvalid[PDK_MAX_BATCH]; // its units that move tokens (the rest fill zeros)
+  int32_t nvalid[PDK_MAX_BATCH]; // its units that move tokens
   int32_t Pz[PDK_MAX_BATCH];     // first column of its all-zero tail: min(64 nT, S)
   int32_t nZ[PDK_MAX_BATCH];     // zero-fill chunks per (layer, head)
   uint32_t magic[PDK_MAX_BATCH]; // ceil(2^32 / ((S - Pz) / 8)): row of a K tail group
@@ -113,15 +118,18 @@ __device__ __forceinline__ int64_t wave_unit() {
 template <bool kStream>
 __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
   const int64_t unit = wave_unit();
-  if (unit >= a.off[a.n_req]) return;
-  const int r = request_of(a.off, a.n_req, unit);
-  const pdk_pack_req& R = a.req[r];
+  const int64_t n_moving = a.off[a.n_req];
   const int lane = threadIdx.x & 63;
-  uint32_t u = (uint32_t)(unit - a.off[r]);   // units of one request fit 32 bits
-  if (u >= (uint32_t)a.nvalid[r]) {           // uniform across the wavefront
-    pack_zero_chunk<kStream>(a, r, u - (uint32_t)a.nvalid[r], lane);
+  if (unit >= n_moving) {                     // uniform across the wavefront
+    const int64_t z = unit - n_moving;
+    if (z >= a.zoff[a.n_req]) return;
+    const int rz = request_of(a.zoff, a.n_req, z);
+    pack_zero_chunk<kStream>(a, rz, (uint32_t)(z - a.zoff[rz]), lane);
     return;
   }
+  const int r = request_of(a.off, a.n_req, unit);
+  const pdk_pack_req& R = a.req[r];
+  uint32_t u = (uint32_t)(unit - a.off[r]);   // units of one request fit 32 bits
   const int dt = (int)(u % (uint32_t)a.nD); u /= (uint32_t)a.nD;
   const int tt = (int)(u % (uint32_t)a.nT[r]); u /= (uint32_t)a.nT[r];
   const int h = (int)(u % (uint32_t)a.Hkv); u /= (uint32_t)a.Hkv;
@@ -399,6 +407,7 @@ extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_lay
   a.D = head_dim;
   a.nD = head_dim / kTileD;
   a.off[0] = 0;
+  a.zoff[0] = 0;
   for (int i = 0; i < n_reqs; ++i) {
     // Tiles that hold valid tokens move them (and zero their own columns >= P);
     // a full-width frame's tail past them is zero-filled by separate chunks.
@@ -411,10 +420,12 @@ extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_lay
     a.nZ[i] = narrow ? 0 : (int)((tail + kZeroElems - 1) / kZeroElems);
     const uint32_t g_row = (uint32_t)(S - a.Pz[i]) / 8;
     a.magic[i] = g_row ? (uint32_t)((((uint64_t)1 << 32) + g_row - 1) / g_row) : 0;
-    a.off[i + 1] = a.off[i] + a.nvalid[i] + (int64_t)n_layers * n_kv_heads * a.nZ[i];
+    a.off[i + 1] = a.off[i] + a.nvalid[i];
+    a.zoff[i + 1] = a.zoff[i] + (int64_t)n_layers * n_kv_heads * a.nZ[i];
   }
-  if (a.off[n_reqs] == 0) return PDK_OK;
-  const int64_t gx = grid_x(a.off[n_reqs]);
+  const int64_t units = a.off[n_reqs] + a.zoff[n_reqs];
+  if (units == 0) return PDK_OK;
+  const int64_t gx = grid_x(units);
   PDK_REQUIRE(gx < (1ll << 31), "launch too large");
   // Bytes the launch moves: valid tokens read, frame columns written.
   int64_t moved = 0;
