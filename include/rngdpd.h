@@ -530,25 +530,31 @@ int pdk_copy_layers(void* dst, const void* src, size_t layer_bytes,
                     const uintptr_t* done_events, uintptr_t stream);
 
 /* The valid columns of frame layers [layer0, layer0 + n_layers) -- K rows'
- * columns [0, min(round64(P), S)) and V rows [0, P) -- copied by the DMA
+ * columns [0, min(round16(P), S)) and V rows [0, P) -- copied by the DMA
  * engines between a device frame and a pinned host frame (dst and src are
- * frame bases, layer 0), two rectangular copies in all; direction PDK_COPY_D2H
- * or PDK_COPY_H2D. The device->host and host->device legs of the reference's
+ * frame bases, layer 0): one rectangular copy for each part in `parts`
+ * (PDK_FRAME_K, PDK_FRAME_V or both); direction PDK_COPY_D2H or
+ * PDK_COPY_H2D. The device->host and host->device legs of the reference's
  * download / upload (engines/prefill_full.py:378-384, engines/decode_batch.py:
  * 305-351) for the bytes that are not padding. P = 0 copies nothing. */
+#define PDK_FRAME_K 1
+#define PDK_FRAME_V 2
+#define PDK_FRAME_KV 3
 int pdk_copy_frame_valid(void* dst, const void* src, int layer0, int n_layers,
                          int n_kv_heads, int head_dim, int S, int P,
-                         int direction, uintptr_t stream);
+                         int direction, int parts, uintptr_t stream);
 
-/* Host side of a frame packed narrow (PDK_PACK_NARROW) into pinned memory:
- * zero what the narrow pack leaves unwritten -- per layer, K rows' columns
- * [round64(P), S) and V rows [P, S) -- with `threads` host threads (1..64), so
- * the frame becomes the S-wide wire payload while the host link carries only
- * the valid columns. Host memory only; no stream, no device work. Replaces
- * the device-side zero padding of engines/prefill_full.py:378-379 for frames
- * staged through the host. */
+/* Host side of a pinned frame whose valid columns the device wrote: zero what
+ * it left unwritten -- per layer, K rows' columns [round_k(P), S) and V rows
+ * [P, S) -- with `threads` host threads (1..64), so the frame becomes the
+ * S-wide wire payload while the host link carries only the valid columns.
+ * k_round: 64 after a PDK_PACK_NARROW pack into the frame (whole 64-token
+ * tiles of K), 16 after pdk_copy_frame_valid. Host memory only; no stream, no
+ * device work. Replaces the device-side zero padding of
+ * engines/prefill_full.py:378-379 for frames staged through the host. */
 int pdk_host_zero_frame_tail(uint16_t* frame, int n_layers, int n_kv_heads,
-                             int head_dim, int S, int P, int threads);
+                             int head_dim, int S, int P, int k_round,
+                             int threads);
 
 /* Per layer l: wait wait_events[l], then one scatter launch of frame slice l
  * of all n_reqs requests (1..16) into cache layer l. */

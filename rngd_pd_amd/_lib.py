@@ -49,6 +49,7 @@ class PackReq(ctypes.Structure):
 
 
 PDK_PACK_NARROW = 1
+PDK_FRAME_K, PDK_FRAME_V, PDK_FRAME_KV = 1, 2, 3
 
 
 class ScatterReq(ctypes.Structure):
@@ -144,8 +145,8 @@ SIGNATURES = {
     "pdk_ipc_open_event": (_I, [_P, ctypes.POINTER(_U)]),
     "pdk_pack_kv_layerwise": (_I, [ctypes.POINTER(PackReq), _I, _I, _I, _I, _I, _P, _U]),
     "pdk_copy_layers": (_I, [_P, _P, _SZ, _I, _I, _P, _P, _U]),
-    "pdk_host_zero_frame_tail": (_I, [_P, _I, _I, _I, _I, _I, _I]),
-    "pdk_copy_frame_valid": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _U]),
+    "pdk_host_zero_frame_tail": (_I, [_P, _I, _I, _I, _I, _I, _I, _I]),
+    "pdk_copy_frame_valid": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _U]),
     "pdk_scatter_paged_layerwise": (_I, [ctypes.POINTER(ScatterReq), _I, _I, _I, _I, _I, _P, _P,
                                          _I64, _I, _P, _U]),
 }

@@ -115,7 +115,7 @@ class FrameSaver:
                     self.events.sync(slot)
                     base = slot * self.slot_bytes
                     _lib.call("pdk_host_zero_frame_tail", self.pinned.ptr + base, 1, self.H,
-                              self.D, self.S, P, 1)
+                              self.D, self.S, P, 64, 1)
                     half = self.F * 2
                     kmv = self.pinned.memoryview(base, half)
                     vmv = self.pinned.memoryview(base + half, half)

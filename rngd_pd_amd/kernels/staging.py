@@ -25,15 +25,16 @@ over layers and requests, with nothing synchronising the host between them:
     current stream  per request, one narrow pack into a device frame (all
                     layers), then an event;
     save stream     per request, after its pack: the DMA engine copies the
-                    valid columns down into the pinned frame, a few layers
-                    per copy (two rectangular copies each: K rows, V runs),
-                    an event after each;
-    load stream     after each of those copies, the same layers' valid
-                    columns back up into a second device frame (the other
-                    DMA engine);
+                    valid columns (K rows up to the 16-token block past P, V
+                    rows < P) down into the pinned frame, a few layers per
+                    copy, as two rectangular copies (K rows, then V runs)
+                    with an event after each;
+    load stream     after each of those copies, the same part back up into a
+                    second device frame (the other DMA engine);
     current stream  per request, after its last upload: one scatter launch
                     (all layers) into the paged cache;
-    host threads    the frames' zero tails, as in "kernel" mode.
+    host threads    the frames' zero tails (K columns >= round16(P), V rows
+                    >= P).
     This is the reference's download / upload shape with copy engines, minus
     the padding: each direction has an engine of its own and no CU is used.
 
@@ -51,7 +52,10 @@ with a kernel on either side. On 8 Llama-3.1-8B requests (P uniform in
 traffic) and "kernel" mode, whose pack and scatter kernels overlap layer by
 layer, 9.5 ms (50 GB/s). Each DMA copy costs about 10 us besides its bytes,
 so "dma" mode copies several layers per command (``copy_bytes`` of valid
-columns, 16 MiB by default).
+columns, 16 MiB by default). An upload can start only once its download is
+done, so a run takes about the download stream's time plus the longest single
+copy: the K and V parts of a chunk are separate copies with an event each,
+which halves that copy against one event per chunk.
 """
 import ctypes
 import os
@@ -61,7 +65,8 @@ import numpy as np
 import torch
 
 from .. import _lib
-from .._lib import PDK_COPY_D2H, PDK_COPY_H2D, PDK_PACK_NARROW, PDK_EVENT_SYNC, PackReq, ScatterReq
+from .._lib import (PDK_COPY_D2H, PDK_COPY_H2D, PDK_EVENT_SYNC, PDK_FRAME_K, PDK_FRAME_V,
+                    PDK_PACK_NARROW, PackReq, ScatterReq)
 from ..hip import EventArray, PinnedBuffer
 from .handoff import _as_layers, _check_cache, _need
 
@@ -92,10 +97,11 @@ class HostStagedHandoff:
             self.ev_layer = EventArray(n_layers)
             self.ev_read = EventArray(1, PDK_EVENT_SYNC)
         else:
-            # Per request: its pack, each of its down copies (at most one per
-            # layer), its last up copy; and the run's last up copy.
+            # Per request: its pack, each of its down copies (at most one K
+            # and one V copy per layer), its last up copy; and the run's last
+            # up copy.
             self.ev_pack = EventArray(max_requests)
-            self.ev_down = EventArray(max_requests * n_layers)
+            self.ev_down = EventArray(2 * max_requests * n_layers)
             self.ev_up = EventArray(max_requests)
             self.ev_read = EventArray(1, PDK_EVENT_SYNC)
             shape = (max_requests, n_layers, 2, self.F)
@@ -178,7 +184,7 @@ class HostStagedHandoff:
                     self.ev_read.sync(0)
                 for r, P in enumerate(lengths):
                     ok(lib.pdk_host_zero_frame_tail(ctypes.c_void_p(self.host_ptr(r)), L, H, D, S,
-                                                    P, self.host_threads),
+                                                    P, 64 if kernel else 16, self.host_threads),
                        "pdk_host_zero_frame_tail")
             except BaseException as e:      # re-raised on the calling thread
                 errors.append(e)
@@ -215,33 +221,19 @@ class HostStagedHandoff:
         ok(lib.pdk_event_record(self.ev_read[0], self.load_stream.cuda_stream),
            "pdk_event_record")
 
-    def layer_chunks(self, P, ramp_up=False, ramp_down=False):
+    def layer_chunks(self, P):
         """(first layer, layers) of each DMA copy of a request of P tokens:
-        about ``copy_bytes`` of valid columns per copy. With ``ramp_up`` the
-        copies start at 1, 2 and 4 layers (the first request of a run: its
-        first upload can start sooner); with ``ramp_down`` they end at 4, 2
-        and 1 (the last request: less upload left once the last download is
-        done)."""
-        k1 = min((P + 63) // 64 * 64, self.S)
+        about ``copy_bytes`` of valid columns per copy, the layers spread
+        evenly over the copies. (Copies that start and end a run at one, two
+        and four layers do not help: a run takes about the download stream's
+        time plus its longest single copy, and they only add copies.)"""
+        k1 = min((P + 15) // 16 * 16, self.S)
         per_layer = max(1, (k1 + P) * self.H * self.D * 2)
         n = max(1, min(self.L, self.copy_bytes // per_layer))
-        ramp = [m for m in (1, 2, 4) if m < n]
-        sizes, left = [], self.L
-        head = ramp if ramp_up else []
-        tail = ramp[::-1] if ramp_down else []
-        for m in head:
-            if left - m < sum(tail):
-                break
-            sizes.append(m)
-            left -= m
-        mid = left - sum(tail)
-        if mid < 0:                       # too few layers for both ramps
-            tail, mid = [], left
-        k = -(-mid // n)                  # copies of at most n layers, sizes within one
-        sizes += [mid // k + (1 if i < mid % k else 0) for i in range(k)]
-        sizes += tail
+        k = -(-self.L // n)               # copies of at most n layers, sizes within one
         out, l0 = [], 0
-        for m in sizes:
+        for i in range(k):
+            m = self.L // k + (1 if i < self.L % k else 0)
             out.append((l0, m))
             l0 += m
         return out
@@ -256,15 +248,17 @@ class HostStagedHandoff:
             out_f, in_f, host = (self.out_frames[r].data_ptr(), self.in_frames[r].data_ptr(),
                                  ctypes.c_void_p(self.host_ptr(r)))
             ok(lib.pdk_stream_wait_event(save, self.ev_pack[r]), "pdk_stream_wait_event")
-            chunks = self.layer_chunks(P, ramp_up=r == 0, ramp_down=r == len(lengths) - 1)
-            for c, (l0, nl) in enumerate(chunks):
-                ev = self.ev_down[r * L + c]
-                ok(lib.pdk_copy_frame_valid(host, ctypes.c_void_p(out_f), l0, nl, H, D, S, P,
-                                            PDK_COPY_D2H, save), "pdk_copy_frame_valid (down)")
-                ok(lib.pdk_event_record(ev, save), "pdk_event_record")
-                ok(lib.pdk_stream_wait_event(load, ev), "pdk_stream_wait_event")
-                ok(lib.pdk_copy_frame_valid(ctypes.c_void_p(in_f), host, l0, nl, H, D, S, P,
-                                            PDK_COPY_H2D, load), "pdk_copy_frame_valid (up)")
+            for c, (l0, nl) in enumerate(self.layer_chunks(P)):
+                for i, part in enumerate((PDK_FRAME_K, PDK_FRAME_V)):
+                    ev = self.ev_down[2 * (r * L + c) + i]
+                    ok(lib.pdk_copy_frame_valid(host, ctypes.c_void_p(out_f), l0, nl, H, D, S, P,
+                                                PDK_COPY_D2H, part, save),
+                       "pdk_copy_frame_valid (down)")
+                    ok(lib.pdk_event_record(ev, save), "pdk_event_record")
+                    ok(lib.pdk_stream_wait_event(load, ev), "pdk_stream_wait_event")
+                    ok(lib.pdk_copy_frame_valid(ctypes.c_void_p(in_f), host, l0, nl, H, D, S, P,
+                                                PDK_COPY_H2D, part, load),
+                       "pdk_copy_frame_valid (up)")
             ok(lib.pdk_event_record(self.ev_up[r], load), "pdk_event_record")
         ok(lib.pdk_event_record(self.ev_read[0], load), "pdk_event_record")
         for r, sr in enumerate(scats):
@@ -274,13 +268,14 @@ class HostStagedHandoff:
                "pdk_scatter_paged_batch")
 
     def link_bytes(self, lengths):
-        """Bytes one run() moves over the host link: the valid columns each way
-        (K rows in whole 64-token tiles, V rows < P) in "dma" mode; the same
-        on the way up in "kernel" mode, whose scatter loads only columns < P."""
+        """Bytes one run() moves over the host link. "dma" mode: the valid
+        columns each way (K rows up to the 16-token block past P, V rows < P).
+        "kernel" mode: on the way down the pack's stores (K in whole 64-token
+        tiles, V rows < P); on the way up the scatter's loads (columns < P)."""
         half = self.L * self.H * self.D * 2              # one token of K (or V), all layers
-        down = sum((min((P + 63) // 64 * 64, self.S) + P) * half for P in lengths)
         if self.mode == "dma":
-            return 2 * down
+            return 2 * sum((min((P + 15) // 16 * 16, self.S) + P) * half for P in lengths)
+        down = sum((min((P + 63) // 64 * 64, self.S) + P) * half for P in lengths)
         return down + sum(2 * P * half for P in lengths)
 
     def close(self):

@@ -38,7 +38,8 @@ def test_version_and_constants():
     assert lib.pdk_version() == 100
     text = open(HEADER).read()
     for name in ("PDK_EINVAL", "PDK_ENOTSUP", "PDK_EHIP", "PDK_EAGAIN", "PDK_ENOMEM",
-                 "PDK_MAX_BATCH", "PDK_BLOCK_SIZE", "PDK_PACK_NARROW", "PDK_COPY_H2D"):
+                 "PDK_MAX_BATCH", "PDK_BLOCK_SIZE", "PDK_PACK_NARROW", "PDK_COPY_H2D",
+                 "PDK_FRAME_K", "PDK_FRAME_V", "PDK_FRAME_KV"):
         value = int(re.search(rf"#define {name}\s+\(?(-?\d+)", text).group(1))
         assert getattr(_lib, name) == value, name
 
@@ -115,32 +116,36 @@ def test_net_library_exports_its_header():
 
 
 def test_host_zero_frame_tail_completes_a_narrow_frame():
-    """The host's half of a narrow-packed frame: what the device leaves unwritten
-    (K columns >= round64(P), V rows >= P) becomes zero, nothing else changes,
-    and the frame equals the oracle's S-wide frame. Host memory only."""
+    """The host's half of a frame the device filled narrow: what it leaves
+    unwritten (K columns >= round16(P) or round64(P), V rows >= P) becomes zero,
+    nothing else changes, and the frame equals the oracle's S-wide frame. Host
+    memory only."""
     import ctypes
     import numpy as np
     from oracle import native as orc
     lib = _lib.lib()
     rng = np.random.default_rng(3)
     L, H, D, S = 3, 2, 64, 144
-    for P in (0, 1, 7, 8, 9, 63, 64, 65, 79, 129, 143, 144):
+    for P in (0, 1, 7, 8, 9, 15, 16, 17, 63, 64, 65, 79, 129, 143, 144):
         k = rng.integers(0, 1 << 16, (L, S, H, D), dtype=np.uint16)
         v = rng.integers(0, 1 << 16, (L, S, H, D), dtype=np.uint16)
         want = orc.pack_kv(k, v, P, S)
-        frame = want.copy()
-        F = H * D * S
-        kf = frame[:, 0].reshape(L, H * D, S)
-        vf = frame[:, 1].reshape(L, H, S, D)
-        k0 = min((P + 63) // 64 * 64, S)
-        kf[:, :, k0:] = 0xBEEF                        # what the narrow pack leaves
-        vf[:, :, P:, :] = 0xBEEF
-        for threads in (1, 4):
-            f = frame.copy()
-            rc = lib.pdk_host_zero_frame_tail(f.ctypes.data_as(ctypes.c_void_p), L, H, D, S, P,
-                                              threads)
-            assert rc == 0, lib.pdk_last_error()
-            np.testing.assert_array_equal(f, want, err_msg=f"P={P} threads={threads}")
+        for k_round in (16, 64):
+            frame = want.copy()
+            kf = frame[:, 0].reshape(L, H * D, S)
+            vf = frame[:, 1].reshape(L, H, S, D)
+            k0 = min((P + k_round - 1) // k_round * k_round, S)
+            kf[:, :, k0:] = 0xBEEF                    # what the device leaves unwritten
+            vf[:, :, P:, :] = 0xBEEF
+            for threads in (1, 4):
+                f = frame.copy()
+                rc = lib.pdk_host_zero_frame_tail(f.ctypes.data_as(ctypes.c_void_p), L, H, D, S,
+                                                  P, k_round, threads)
+                assert rc == 0, lib.pdk_last_error()
+                np.testing.assert_array_equal(f, want,
+                                              err_msg=f"P={P} k_round={k_round} threads={threads}")
     bad = np.zeros(16, np.uint16)
-    assert lib.pdk_host_zero_frame_tail(bad.ctypes.data_as(ctypes.c_void_p), 1, 1, 8, 8, 9, 1) \
-        == _lib.PDK_EINVAL
+    assert lib.pdk_host_zero_frame_tail(bad.ctypes.data_as(ctypes.c_void_p), 1, 1, 8, 8, 9, 64,
+                                        1) == _lib.PDK_EINVAL
+    assert lib.pdk_host_zero_frame_tail(bad.ctypes.data_as(ctypes.c_void_p), 1, 1, 8, 8, 4, 32,
+                                        1) == _lib.PDK_EINVAL
