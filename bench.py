@@ -538,11 +538,14 @@ def bench_attn_floor(args, torch, K, dev, out, batches=(4, 8, 16), ctx=512):
 
 def bench_step(args, torch, dev, out, batches=(4, 16), ctx=512):
     """Full Llama-3.1-8B decode step (32 layers, random-init bf16 weights, no
-    checkpoint): embed -> per layer RMSNorm, q|k|v GEMM split over K, RoPE +
+    checkpoint): embed + the rows' sums of squares -> per layer q|k|v GEMM
+    split over K (rows scaled by the pre-attention RMSNorm's factor), RoPE +
     new-token cache write + paged decode attention in one kernel, o GEMM +
-    residual, RMSNorm, gate|up GEMM with SwiGLU, down GEMM split over K (its
-    residual add in the next norm) -> final norm, lm_head GEMM with the greedy
-    argmax; the GEMMs read the decoder's tiled copies of the weights. Every
+    residual (+ its sums of squares), gate|up GEMM with the post-attention
+    norm's row scale and SwiGLU, down GEMM split over K whose last split adds
+    the residual (+ sums of squares) -> lm_head GEMM with the final norm's row
+    scale and the greedy argmax. The norms' gains are folded into the
+    decoder's tiled copies of the weights, which the GEMMs read. Every
     stream at context ctx (its new token at slot ctx-1; the reference's S=512
     step attends over the whole S). Bytes per step = every weight read once
     (16.06 GB; the embedding contributes B rows) + the K/V of all layers."""
