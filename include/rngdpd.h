@@ -323,6 +323,14 @@ int pdk_rope_cache_append_partials_rms(const float* partials, int splits, int N,
  * no GEMM produced x (the embedding rows before the first layer). */
 int pdk_row_ssq(const uint16_t* x, int B, int H, float* ssq, uintptr_t stream);
 
+/* The decode step's embedding lookup with pdk_row_ssq fused: x [B][H] (bf16)
+ * = table[tokens[b]] (table [vocab][H], the reference's embed_tokens gather of
+ * engines/decode_batch.py:422-442) and ssq [B][H/16] exactly as pdk_row_ssq
+ * computes it from x. tokens are int32 (tok_bytes 4) or int64 (8) on the
+ * device; a token outside [0, vocab) gives a zero row. */
+int pdk_embed_ssq(const uint16_t* table, int64_t vocab, const void* tokens, int tok_bytes,
+                  int B, int H, uint16_t* x, float* ssq, uintptr_t stream);
+
 /* out [B][M] = silu(g) * u for gate_up [B][2M] = [g | u] (swiglu_dsl,
  * kernels/dsl_batch.py:55-71). M % 8 == 0. */
 int pdk_swiglu(const uint16_t* gate_up, int B, int M, uint16_t* out,

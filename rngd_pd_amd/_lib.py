@@ -118,6 +118,7 @@ SIGNATURES = {
     "pdk_linear_argmax_rms": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _P, _P, _U]),
     "pdk_linear_argmax_rms_tiled": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _P, _P, _U]),
     "pdk_row_ssq": (_I, [_P, _I, _I, _P, _U]),
+    "pdk_embed_ssq": (_I, [_P, _I64, _P, _I, _I, _I, _P, _P, _U]),
     "pdk_scatter_koni": (_I, [_P, _I64, _P, _I, _I, _P, _I, _P, _P, _I64, _I, _I, _I, _U]),
     "pdk_host_alloc": (_I, [_SZ, ctypes.POINTER(_P)]),
     "pdk_host_free": (_I, [_P]),

@@ -210,22 +210,48 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* gu, int M, 
   pdk::st16(out + b * M + 8 * c, o);
 }
 
+// The sum of squares of 16 bf16 values (lo: elements 0..7, hi: 8..15), in
+// index order.
+__device__ __forceinline__ float tile_ssq(const v8& lo, const v8& hi) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const v8& v = k < 4 ? lo : hi;
+    const float a = pdk::bf16_to_f32(v.w[k & 3] & 0xffffu), c = pdk::bf16_to_f32(v.w[k & 3] >> 16);
+    s += a * a;
+    s += c * c;
+  }
+  return s;
+}
+
 // ssq[b][t] = the sum over x[b][16t .. 16t+15] (bf16) of x^2, in index order:
 // the per-tile sums of squares a folded RMSNorm's consumer scales rows by.
 __global__ __launch_bounds__(256) void row_ssq_kernel(const uint16_t* x, int B, int H, float* ssq) {
   const int b = blockIdx.x;
   for (int t = threadIdx.x; t < H / 16; t += 256) {
     const uint16_t* p = x + (int64_t)b * H + 16 * t;
-    const v8 lo = pdk::ld16(p), hi = pdk::ld16(p + 8);
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const v8& v = k < 4 ? lo : hi;
-      const float a = pdk::bf16_to_f32(v.w[k & 3] & 0xffffu), c = pdk::bf16_to_f32(v.w[k & 3] >> 16);
-      s += a * a;
-      s += c * c;
-    }
-    ssq[(int64_t)b * (H / 16) + t] = s;
+    ssq[(int64_t)b * (H / 16) + t] = tile_ssq(pdk::ld16(p), pdk::ld16(p + 8));
+  }
+}
+
+// x[b] = table[tokens[b]] and its per-tile sums of squares (row_ssq_kernel's
+// values, bit for bit): the step's embedding lookup and the first layer's
+// folded-norm input in one launch. A token outside [0, vocab) gives a zero row.
+template <typename Tok>
+__global__ __launch_bounds__(256) void embed_ssq_kernel(const uint16_t* table, int64_t vocab,
+                                                        const Tok* tokens, int H, uint16_t* x,
+                                                        float* ssq) {
+  const int b = blockIdx.x;
+  const int64_t tok = (int64_t)tokens[b];
+  const bool ok = tok >= 0 && tok < vocab;
+  const uint16_t* row = table + (ok ? tok : 0) * (int64_t)H;
+  for (int t = threadIdx.x; t < H / 16; t += 256) {
+    v8 lo = pdk::ld16(row + 16 * t), hi = pdk::ld16(row + 16 * t + 8);
+    if (!ok) lo = hi = pdk::zero8();
+    uint16_t* o = x + (int64_t)b * H + 16 * t;
+    pdk::st16(o, lo);
+    pdk::st16(o + 8, hi);
+    ssq[(int64_t)b * (H / 16) + t] = tile_ssq(lo, hi);
   }
 }
 
@@ -239,6 +265,26 @@ extern "C" int pdk_row_ssq(const uint16_t* x, int B, int H, float* ssq, uintptr_
   PDK_REQUIRE(pdk::aligned16(x), "x must be 16-byte aligned");
   hipLaunchKernelGGL(row_ssq_kernel, dim3(B), dim3(256), 0, pdk::as_stream(stream), x, B, H, ssq);
   return pdk::check_launch("row_ssq_kernel");
+}
+
+extern "C" int pdk_embed_ssq(const uint16_t* table, int64_t vocab, const void* tokens,
+                             int tok_bytes, int B, int H, uint16_t* x, float* ssq,
+                             uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(table && tokens && x && ssq, "null pointer argument");
+  PDK_REQUIRE(vocab >= 1, "vocab must be >= 1");
+  PDK_REQUIRE(tok_bytes == 4 || tok_bytes == 8, "tok_bytes must be 4 (int32) or 8 (int64)");
+  PDK_REQUIRE(B >= 1 && B <= 65535, "B must be in [1, 65535] (got %d)", B);
+  PDK_REQUIRE(H >= 16 && H % 16 == 0, "H must be a positive multiple of 16 (got %d)", H);
+  PDK_REQUIRE(pdk::aligned16(table) && pdk::aligned16(x), "table and x must be 16-byte aligned");
+  hipStream_t st = pdk::as_stream(stream);
+  if (tok_bytes == 4)
+    hipLaunchKernelGGL(embed_ssq_kernel<int32_t>, dim3(B), dim3(256), 0, st, table, vocab,
+                       static_cast<const int32_t*>(tokens), H, x, ssq);
+  else
+    hipLaunchKernelGGL(embed_ssq_kernel<int64_t>, dim3(B), dim3(256), 0, st, table, vocab,
+                       static_cast<const int64_t*>(tokens), H, x, ssq);
+  return pdk::check_launch("embed_ssq_kernel");
 }
 
 static int check_norm(const void* x, const void* weight, const void* out, int B, int H) {

@@ -20,10 +20,10 @@ layer, one launch per line:
                                                     split of each column group adds the partials
                                                     to x in split order and writes that group's ssq
 
-before the first layer pdk_row_ssq gives the embedding rows' ssq, and after
-the last the lm_head GEMM (weights folded with the final norm's gain) scales
-each row's logits by r and takes the first-maximum argmax in its epilogue
-(pdk_linear_argmax_rms).
+before the first layer pdk_embed_ssq gathers the embedding rows and writes
+their ssq, and after the last the lm_head GEMM (weights folded with the final
+norm's gain) scales each row's logits by r and takes the first-maximum argmax
+in its epilogue (pdk_linear_argmax_rms).
 Weights are [out, in] contiguous (torch Linear layout) with q|k|v and gate|up
 stacked, so each projection is one pass over its weights. By default the
 decoder streams tiled copies of them (pdk_weight_tile, made once at
@@ -165,7 +165,7 @@ class LlamaDecoder:
                                     device=dev)
         # Per 16-column tile and row, the residual's sums of squares: left by
         # the O projection for the post-attention norm (fused into gate|up),
-        # and by the down projection (pdk_row_ssq before layer 0) for the
+        # and by the down projection (pdk_embed_ssq before layer 0) for the
         # pre-attention norm (fused into attention) and the final one (into
         # the lm_head). The down projection's split counters start at zero
         # and every call leaves them so.
@@ -224,7 +224,7 @@ class LlamaDecoder:
 
     def step(self, tokens, ctx_lens, tables, max_ctx, stream=None):
         """tokens int64/int32 [B] on the device (this step's input token per
-        stream), ctx_lens int32 [B] = position + 1 (the new token's slot is
+        stream; an id outside [0, vocab) embeds as a zero row), ctx_lens int32 [B] = position + 1 (the new token's slot is
         ctx_lens-1, attention covers 0..ctx_lens-1), tables int32 [B, max_blocks]
         holding at least ceil(ctx/16) blocks each; max_ctx (<= max_blocks*16)
         sizes the attention's split plan and should cover every ctx_lens. Returns
@@ -239,6 +239,9 @@ class LlamaDecoder:
         for t, name in ((tokens, "tokens"), (ctx_lens, "ctx_lens"), (tables, "tables")):
             if not t.is_cuda or t.device != self.device:
                 raise ValueError(f"{name} must be on {self.device}")
+        if tokens.dtype not in (torch.int32, torch.int64) or tokens.dim() != 1 \
+                or not tokens.is_contiguous():
+            raise ValueError("tokens must be contiguous int32 or int64 [B]")
         if ctx_lens.dtype != torch.int32 or ctx_lens.numel() != B:
             raise ValueError("ctx_lens must be int32 [B]")
         if tables.dtype != torch.int32 or tables.dim() != 2 or tables.shape[0] != B \
@@ -263,8 +266,8 @@ class LlamaDecoder:
         ssqp, ssqa, cntp, n_ssq = (self.ssq.data_ptr(), self.ssq_a.data_ptr(),
                                    self.counters.data_ptr(), H // 16)
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
-            torch.index_select(w.embed, 0, tokens.long(), out=x)
-            call("pdk_row_ssq", xp, B, H, ssqa, st)
+            call("pdk_embed_ssq", w.embed.data_ptr(), cfg.vocab, tokens.data_ptr(),
+                 tokens.element_size(), B, H, xp, ssqa, st)
             partp, sp = self.part.data_ptr(), self.down_splits
             pqp, qs = self.part_qkv.data_ptr(), self.qkv_splits
             for wqkv, wo, wgu, wd, ck, cv in self._layers:

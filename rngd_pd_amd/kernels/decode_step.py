@@ -110,6 +110,30 @@ def rope_cache_append_partials(partials, inv_freq, ctx_lens, block_tables, cache
     return q_out
 
 
+def embed_ssq(table, tokens, x=None, ssq=None, stream=None):
+    """x = table[tokens] (bf16 [B, H]) and its row_ssq, in one launch; tokens
+    int32 or int64 [B] on the device. A token outside [0, vocab) gives a zero
+    row (torch's index_select would fault instead)."""
+    _need(table, "table")
+    if table.dim() != 2 or not table.is_contiguous() or table.shape[1] % 16:
+        raise ValueError("table must be contiguous [vocab, H] with H % 16 == 0")
+    if tokens.dtype not in (torch.int32, torch.int64) or tokens.dim() != 1 \
+            or not tokens.is_cuda or not tokens.is_contiguous():
+        raise ValueError("tokens must be a contiguous int32 or int64 [B] device tensor")
+    (B,), (V, H) = tokens.shape, table.shape
+    if x is None:
+        x = torch.empty((B, H), dtype=table.dtype, device=table.device)
+    if ssq is None:
+        ssq = torch.empty((B, H // 16), dtype=torch.float32, device=table.device)
+    if tuple(x.shape) != (B, H) or not x.is_contiguous() or x.dtype != table.dtype:
+        raise ValueError(f"x must be contiguous [{B}, {H}] of the table's dtype")
+    if ssq.dtype != torch.float32 or not ssq.is_contiguous() or ssq.numel() < B * (H // 16):
+        raise ValueError(f"ssq must be contiguous float32 holding {B}x{H // 16}")
+    _lib.call("pdk_embed_ssq", table.data_ptr(), V, tokens.data_ptr(), tokens.element_size(), B,
+              H, x.data_ptr(), ssq.data_ptr(), stream_handle(stream))
+    return x, ssq
+
+
 def row_ssq(x, ssq=None, stream=None):
     """float32 [B, H/16]: per 16-column tile, the sum of squares of each row
     of the bf16 x [B, H]."""

@@ -303,6 +303,27 @@ def test_row_ssq(cuda, B, H):
     np.testing.assert_allclose(got, want, rtol=1e-6)
 
 
+@pytest.mark.parametrize("tok_dtype", [torch.int32, torch.int64])
+def test_embed_ssq(cuda, tok_dtype):
+    """The fused lookup: x equal to the table's rows bit for bit (a zero row for
+    ids outside [0, vocab)), ssq bit-identical to row_ssq of that x."""
+    from rngd_pd_amd import kernels as K
+    rng = np.random.default_rng(5)
+    V, H, B = 1000, 4096, 16
+    table = to_dev(rand_bf16(rng, (V, H), 2.0))
+    ids = rng.integers(0, V, B)
+    ids[3], ids[7], ids[11] = -1, V, 0          # out of range both ways, and the first row
+    tok = torch.from_numpy(ids).to(cuda).to(tok_dtype)
+    print(f"embed_ssq tokens {tok_dtype}", flush=True)
+    x, ssq = K.embed_ssq(table, tok)
+    torch.cuda.synchronize()
+    want = to_host(table)[np.clip(ids, 0, V - 1)].copy()
+    want[(ids < 0) | (ids >= V)] = 0
+    np.testing.assert_array_equal(to_host(x), want)
+    ref = K.row_ssq(to_dev(want))
+    assert torch.equal(ssq, ref)
+
+
 @pytest.mark.parametrize("B,K,N,splits", [(16, 14336, 4096, 4), (4, 14336, 4096, 4),
                                           (3, 1024, 512, 8), (33, 512, 2048, 2), (1, 128, 16, 1)])
 def test_linear_splitk_final(cuda, B, K, N, splits):
@@ -348,7 +369,8 @@ def test_linear_argmax_rms(cuda, B, K, N):
     keys = torch.zeros(B, dtype=torch.int64, device=cuda)
     logits = torch.empty((B, N), dtype=BF16, device=cuda)
     print(f"linear_argmax_rms B={B} K={K} N={N}", flush=True)
-    tok = K_.linear_argmax_rms(to_dev(x), K_.tile_weight(wd), torch.from_numpy(ssq).to(cuda), eps,
+    wt = K_.tile_weight(wd)
+    tok = K_.linear_argmax_rms(to_dev(x), wt, torch.from_numpy(ssq).to(cuda), eps,
                                keys, logits=logits)
     want_tok = K_.greedy_argmax(logits)
     torch.cuda.synchronize()

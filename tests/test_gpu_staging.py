@@ -116,3 +116,52 @@ def test_staged_rejects_bad_input(cuda):
             stager.run([(kv[:, 0], kv[:, 1], 1, short)] * 3, ck, cv)
     finally:
         stager.close()
+
+
+def test_copy_frame_valid_parts(cuda):
+    """pdk_copy_frame_valid copies exactly the requested parts: K rows' first
+    min(round16(P), S) columns and V rows < P, for a range of layers, each way;
+    every other byte of the destination keeps what it held."""
+    import ctypes
+    from rngd_pd_amd import _lib
+    from rngd_pd_amd.hip import PinnedBuffer
+    lib = _lib.lib()
+    Lf, Hf, Df, Sf = 5, 2, 64, 144
+    F = Hf * Df * Sf
+    rng = np.random.default_rng(11)
+    src = rng.integers(0, 1 << 16, (Lf, 2, F), dtype=np.uint16)
+    dframe = to_dev(src, cuda)
+    pin = PinnedBuffer(Lf * 2 * F * 2)
+    host = pin.view(np.uint16, 0, Lf * 2 * F).reshape(Lf, 2, F)
+    st = torch.cuda.current_stream(cuda).cuda_stream
+    for P in (1, 15, 16, 17, 100, 129, Sf):
+        k1 = min((P + 15) // 16 * 16, Sf)
+        for parts in (_lib.PDK_FRAME_K, _lib.PDK_FRAME_V, _lib.PDK_FRAME_KV):
+            l0, nl = 1, 3
+            host[:] = 0xBEEF
+            rc = lib.pdk_copy_frame_valid(ctypes.c_void_p(pin.ptr), ctypes.c_void_p(dframe.data_ptr()),
+                                          l0, nl, Hf, Df, Sf, P, _lib.PDK_COPY_D2H, parts, st)
+            assert rc == 0, _lib.last_error()
+            torch.cuda.synchronize()
+            copied = np.zeros(src.shape, bool)
+            if parts & _lib.PDK_FRAME_K:
+                copied[:, 0].reshape(Lf, Hf * Df, Sf)[l0:l0 + nl, :, :k1] = True
+            if parts & _lib.PDK_FRAME_V:
+                copied[:, 1].reshape(Lf, Hf, Sf, Df)[l0:l0 + nl, :, :P] = True
+            want = np.where(copied, src, np.uint16(0xBEEF))
+            np.testing.assert_array_equal(host, want, err_msg=f"down P={P} parts={parts}")
+            # And back up into a device frame holding a pattern.
+            back = to_dev(np.full_like(src, 0x1234), cuda)
+            host[:] = src
+            rc = lib.pdk_copy_frame_valid(ctypes.c_void_p(back.data_ptr()), ctypes.c_void_p(pin.ptr),
+                                          l0, nl, Hf, Df, Sf, P, _lib.PDK_COPY_H2D, parts, st)
+            assert rc == 0, _lib.last_error()
+            torch.cuda.synchronize()
+            want = np.where(copied, src, np.uint16(0x1234))
+            np.testing.assert_array_equal(to_host(back), want, err_msg=f"up P={P} parts={parts}")
+    for bad in (0, 4):
+        assert lib.pdk_copy_frame_valid(ctypes.c_void_p(pin.ptr), ctypes.c_void_p(dframe.data_ptr()),
+                                        0, 1, Hf, Df, Sf, 16, _lib.PDK_COPY_D2H, bad, st) \
+            == _lib.PDK_EINVAL
+    torch.cuda.synchronize()
+    pin.close()
