@@ -48,9 +48,9 @@ Measured on MI355X: one direction alone moves 53-57 GB/s, by a kernel's
 loads or stores through pinned memory or by a DMA engine. Both directions at
 once reach about 98 GB/s in total with one DMA engine each way, 77-87 GB/s
 with a kernel on either side. On 8 Llama-3.1-8B requests (P uniform in
-[64, 512], 486 MB over the link) "dma" mode takes 6.0 ms (80 GB/s of link
-traffic) and "kernel" mode, whose pack and scatter kernels overlap layer by
-layer, 9.5 ms (50 GB/s). Each DMA copy costs about 10 us besides its bytes,
+[64, 512]) "dma" mode takes 6.0 ms (461 MB over the link, 77 GB/s) and
+"kernel" mode, whose pack and scatter kernels overlap layer by layer, 9.7 ms
+(469 MB, 48 GB/s). Each DMA copy costs about 10 us besides its bytes,
 so "dma" mode copies several layers per command (``copy_bytes`` of valid
 columns, 16 MiB by default). An upload can start only once its download is
 done, so a run takes about the download stream's time plus the longest single
