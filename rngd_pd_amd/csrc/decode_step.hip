@@ -277,6 +277,8 @@ extern "C" int pdk_embed_ssq(const uint16_t* table, int64_t vocab, const void* t
   PDK_REQUIRE(B >= 1 && B <= 65535, "B must be in [1, 65535] (got %d)", B);
   PDK_REQUIRE(H >= 16 && H % 16 == 0, "H must be a positive multiple of 16 (got %d)", H);
   PDK_REQUIRE(pdk::aligned16(table) && pdk::aligned16(x), "table and x must be 16-byte aligned");
+  PDK_REQUIRE(reinterpret_cast<uintptr_t>(tokens) % tok_bytes == 0,
+              "tokens must be aligned to their %d-byte size", tok_bytes);
   hipStream_t st = pdk::as_stream(stream);
   if (tok_bytes == 4)
     hipLaunchKernelGGL(embed_ssq_kernel<int32_t>, dim3(B), dim3(256), 0, st, table, vocab,
