@@ -50,6 +50,7 @@ constexpr int kMaxWaves = 8;
 constexpr int kSpan = 32;        // tokens per span
 constexpr int kMaxG = 16;
 constexpr int kMaxSplits = 32;
+constexpr int kMaxCtx = 16384;   // longest context a call accepts
 // LDS row stride of the wavefront merge: kD + 4 puts lane groups g and g+1
 // (rows 4 apart) on different banks.
 constexpr int kOStride = kD + 4;
@@ -723,6 +724,11 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1, "num_blocks and max_blocks must be >= 1");
   PDK_REQUIRE(max_ctx >= 1 && max_ctx <= max_blocks * 16,
               "max_ctx=%d outside [1, max_blocks*16=%d]", max_ctx, max_blocks * 16);
+  // The largest context the tests cover (and the header promises).
+  if (max_ctx > kMaxCtx) {
+    pdk::set_error("max_ctx=%d above the supported %d", max_ctx, kMaxCtx);
+    return PDK_ENOTSUP;
+  }
   PDK_REQUIRE(plan_B >= B && plan_B <= 65535, "plan_batch=%d must be in [B=%d, 65535]", plan_B, B);
   const Plan p = plan_for(plan_B, n_kv_heads, max_ctx);
   AttnArgs a{};

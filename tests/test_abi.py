@@ -149,3 +149,14 @@ def test_host_zero_frame_tail_completes_a_narrow_frame():
                                         1) == _lib.PDK_EINVAL
     assert lib.pdk_host_zero_frame_tail(bad.ctypes.data_as(ctypes.c_void_p), 1, 1, 8, 8, 4, 32,
                                         1) == _lib.PDK_EINVAL
+
+
+def test_decode_attn_refuses_contexts_past_its_limit():
+    """max_ctx above 16384 (the header's limit) is refused before anything is
+    launched; the pointers are never dereferenced, so placeholders do."""
+    lib = _lib.lib()
+    p = 1 << 20                                   # 16-byte aligned placeholder address
+    rc = lib.pdk_decode_attn(p, p, p, 2048, p, 1100, p, 16400, 1, 32, 8, 128, 0.088, p, 1 << 30,
+                             p, 0)
+    assert rc == _lib.PDK_ENOTSUP
+    assert "16384" in _lib.last_error()
