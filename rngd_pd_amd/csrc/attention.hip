@@ -1,18 +1,22 @@
 // GQA decode attention over the paged KV cache, gfx950.
 //
-// Grid (nsplit, Hkv, B); a workgroup of W wavefronts (W <= 8) owns the token
-// range [split*split_tokens, (split+1)*split_tokens) of stream b, KV head h.
-// With B*Hkv >= 128 the host uses one split (no merge at all); smaller batches
+// Grid (nsplit, Hkv, B); a workgroup of 8 wavefronts owns the token range
+// [split*split_tokens, (split+1)*split_tokens) of stream b, KV head h. With
+// B*Hkv >= 128 the host uses one split (no merge at all); smaller batches
 // split the context so the launch still spreads over the CUs, and a second
 // small kernel merges the splits.
 //
-// A wavefront walks 32-token spans, two per iteration (both spans' loads in
-// flight together); per span:
-//   1. the block ids of its tokens (three loads), then all K and V loads;
+// A wavefront walks the 32-token spans wave, wave + 8, ... of its range with
+// two spans' loads in flight: while one span is used the next one's loads
+// are outstanding, and a span's registers are refilled as soon as it has been
+// used. Per span:
+//   1. the block ids of its tokens (scalar loads, one pair of spans ahead),
+//      then all K and V loads;
 //   2. QK^T: two v_mfma_f32_16x16x32_bf16 tiles x 4 k-steps. A = 16 K rows
 //      (tokens), B = the G query heads of the group padded to 16 columns;
-//   3. online softmax in fp32 in the exp2 domain (two lane shuffles per
-//      reduction), rescaling the running output;
+//   3. online softmax in fp32 in the exp2 domain (two lane swaps per column
+//      reduction), rescaling the running output when a maximum grew; spans
+//      whose tokens are all live skip every mask;
 //   4. PV: 8 v_mfma_f32_16x16x32_bf16 (one per 16-dim tile), A = P straight
 //      from the QK accumulators, B = V.
 // MFMA multiplies along the 8 contiguous elements a lane holds, so the cache
@@ -35,6 +39,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "pdk_common.h"
 
@@ -54,6 +59,9 @@ constexpr int kMaxCtx = 16384;   // longest context a call accepts
 // LDS row stride of the wavefront merge: kD + 4 puts lane groups g and g+1
 // (rows 4 apart) on different banks.
 constexpr int kOStride = kD + 4;
+// LDS row of the merge: the 8 wavefronts' O rows of one query head. With
+// kORow = 4 (mod 8), rows 4 apart (lane groups g, g+1) start 16 banks apart.
+constexpr int kORow = 8 * kOStride + 4;
 constexpr int kMergeRows = 8;     // query rows merged per LDS pass
 
 __device__ __forceinline__ bf16x8_t as_bf(const v8& v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -78,14 +86,18 @@ struct AttnArgs {
 // Registers of one span between its loads and its use.
 struct Span {
   v8 ka[4], kb[4], vf[8];
-  bool v_ok;                     // this lane's V block id was valid
 };
+
+__device__ __forceinline__ bool valid_block(int blk, int num_blocks) {
+  return blk >= 0 && blk < num_blocks;
+}
 
 // Issue every load of the 32-token span starting at `span`, whose tokens lie
 // in the blocks blk_lo (tokens span..span+15) and blk_hi (span+16..span+31).
 // Loads are unconditional from in-bounds addresses (an invalid block id reads
-// block 0) so they are all in flight together; V of tokens >= lim is zeroed
-// afterwards, K of such tokens needs nothing (their scores become -inf).
+// block 0) so they are all in flight together; V of tokens >= lim and of
+// invalid blocks is zeroed before use, K of tokens >= lim needs nothing (their
+// scores become -inf).
 __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, int g, int j,
                                           int blk_lo, int blk_hi, Span& r) {
   // QK tile 0 row j is token span + 8(j/4) + j%4 and tile 1 row j that token
@@ -95,9 +107,8 @@ __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, in
   const int tv = span + 8 * g;                   // this lane's 8 V tokens; blk_lo iff g < 2
   const int bk = (j < 8) ? blk_lo : blk_hi;
   const int bv = (g < 2) ? blk_lo : blk_hi;
-  const int cbk = (bk >= 0 && bk < a.num_blocks) ? bk : 0;
-  r.v_ok = bv >= 0 && bv < a.num_blocks;
-  const int cbv = r.v_ok ? bv : 0;
+  const int cbk = valid_block(bk, a.num_blocks) ? bk : 0;
+  const int cbv = valid_block(bv, a.num_blocks) ? bv : 0;
   const uint16_t* pk = a.ck + ((int64_t)cbk * a.Hkv + h) * 16 * kD + (g * 8 + (j & 7)) * 8;
   const uint16_t* pv = a.cv + ((int64_t)cbv * a.Hkv + h) * kD * 16 + (tv & 15) + j * 16;
   // unit(t, s) = ((t * 4 + s) * 4 + g) * 8 + j8 with kD / 32 = 4 dim groups per tile
@@ -115,11 +126,24 @@ __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, in
 // v_permlane32_swap each lane holds {x[i], x[i^32]}, after v_permlane16_swap
 // {y[i], y[i^16]}. Both operands of each step are exchanged symmetrically, so
 // every lane of the column ends with the same bits.
+// Maximum that propagates NaN (v_maximum3_f32 on gfx950): unlike fmaxf it
+// needs no operand canonicalisation.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// n / d for 0 <= n < 2^24 and 1 <= d < 2^24 (wavefront-uniform values):
+// n * rcp(d) in fp32 is within 1 of the quotient, and one step corrects it.
+__device__ __forceinline__ int div_u24(int n, int d) {
+  int q = (int)((float)n * __builtin_amdgcn_rcpf((float)d));
+  const int r = n - q * d;
+  q += (r >= d) - (r < 0);
+  return q;
+}
+
 __device__ __forceinline__ float column_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  x = vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
   const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+  return vmax(__uint_as_float(t[0]), __uint_as_float(t[1]));
 }
 
 __device__ __forceinline__ float column_sum(float x) {
@@ -129,48 +153,11 @@ __device__ __forceinline__ float column_sum(float x) {
   return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
-// QK of one span: lane (g, j) gets query j's scaled scores of tokens tv..tv+7
-// (tv = span + 8g); tokens >= lim get -inf.
-__device__ __forceinline__ void span_scores(const Span& r, const v8 qv[4], float scale_log2,
-                                            int tv, int lim, float* sc) {
-  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    s0 = mfma(r.ka[s], qv[s], s0);
-    s1 = mfma(r.kb[s], qv[s], s1);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    sc[i] = s0[i] * scale_log2;
-    sc[4 + i] = s1[i] * scale_log2;
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    if (tv + e >= lim) sc[e] = -INFINITY;
-}
-
-// PV of one span with probabilities p[0..7] of tokens tv..tv+7.
-__device__ __forceinline__ void span_pv(Span& r, const float* p, uint32_t pmask, int tv, int lim,
-                                        f32x4 o[8]) {
-  if (tv >= lim || !r.v_ok) {
-#pragma unroll
-    for (int n = 0; n < 8; ++n) r.vf[n] = pdk::zero8();
-  } else if (tv + 8 > lim) {
-#pragma unroll
-    for (int n = 0; n < 8; ++n) pdk::mask_tail(r.vf[n], tv, lim);
-  }
-  v8 pv;
-#pragma unroll
-  for (int w = 0; w < 4; ++w)
-    pv.w[w] = pdk::pack_bf16x2_rne(p[2 * w], p[2 * w + 1]) & pmask;   // p in [0, 1]: finite
-#pragma unroll
-  for (int n = 0; n < 8; ++n) o[n] = mfma(pv, r.vf[n], o[n]);
-}
-
 // The new token of the fused RoPE path: its position, its rotated k and its v
 // (bf16, in LDS), and where its cache slot lives.
 struct NewToken {
   int pos, lane, Hkv, h;
+  bool writer;                   // this workgroup writes the token's cache slot
   const uint16_t* k;
   const uint16_t* v;
   uint16_t* ck_w;
@@ -180,7 +167,7 @@ struct NewToken {
 // Block of the new token in the span starting at `span` (its ids lo, hi), or
 // -1 when the span does not hold it or the id is invalid: only a valid block's
 // slot is written, by either path, and V of an invalid block is zeroed by
-// span_pv anyway.
+// attend_span anyway.
 __device__ __forceinline__ int new_token_block(const NewToken& nt, int span, int lo, int hi,
                                                int num_blocks) {
   if (nt.pos < span || nt.pos >= span + kSpan) return -1;   // wavefront-uniform
@@ -208,6 +195,7 @@ __device__ __forceinline__ void patch_k(Span& r, int span, int blk, const NewTok
       r.kb[s].w[w] = in_b ? k.w[w] : r.kb[s].w[w];
     }
   }
+  if (!nt.writer) return;
   const int slot = nt.pos & 15;
   uint16_t* kb = nt.ck_w + ((int64_t)blk * nt.Hkv + nt.h) * 16 * kD;
   uint16_t* vb = nt.cv_w + ((int64_t)blk * nt.Hkv + nt.h) * kD * 16;
@@ -236,70 +224,115 @@ __device__ __forceinline__ void patch_v(Span& r, int span, const NewToken& nt, i
   }
 }
 
-// Fold spans A (and B, when has_b) into the running (m, lsum, o) of query
-// j = lane & 15 with one softmax over their 64 tokens. On the first pair the
-// running state is empty, so nothing is rescaled.
-// With kPatch (the fused RoPE path), ids are the spans' block ids (a lo, a
-// hi, b lo, b hi) and nt the new token, patched into whichever span holds it.
+// Fold one span into the running state of query column j = lane & 15: m, the
+// largest raw score so far (the same in the column's four lanes), lsum, this
+// lane's own sum of weights 2^(c*s - c*m) (c = scale * log2(e) > 0; the
+// column's four sums are added once, at the end), and o, the weighted sum of
+// V rows (lane (g, j) holds query rows 4g..4g+3, dims 16n + j). Spans whose
+// 32 tokens are all live and whose block ids are valid (a wavefront-uniform
+// test) skip every mask; the others give tokens >= lim the score -inf and
+// zero V of those tokens and of invalid blocks. O is rescaled only when some
+// column's maximum grew (the factor is exactly 1 otherwise).
+// With kPatch (the fused RoPE path) the span's K and V take the new token nt
+// in place of the cache's contents, and its cache slot is written.
 template <bool kPatch>
-__device__ __forceinline__ void attend_pair(const AttnArgs& a, Span& ra, Span& rb, bool has_b,
-                                            const v8 qv[4], int sa, int sb, int lim, int g, int j,
-                                            bool first, float& m, float& lsum, f32x4 o[8],
-                                            const NewToken& nt, const int* ids) {
-  int blk_a = -1, blk_b = -1;
+__device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8 qv[4], int span,
+                                            int lo, int hi, int lim, int g, int j, bool first,
+                                            float& m, float& lsum, f32x4 o[8],
+                                            const NewToken& nt) {
+  const int tv = span + 8 * g;
+  const bool full = span + kSpan <= lim && valid_block(lo, a.num_blocks) &&
+                    valid_block(hi, a.num_blocks);
+  int blk = -1;
   if constexpr (kPatch) {
-    blk_a = new_token_block(nt, sa, ids[0], ids[1], a.num_blocks);
-    blk_b = has_b ? new_token_block(nt, sb, ids[2], ids[3], a.num_blocks) : -1;
+    blk = new_token_block(nt, span, lo, hi, a.num_blocks);
+    if (blk >= 0) patch_k(r, span, blk, nt, g, j);
   }
-  float sc[16];
-  if (kPatch && blk_a >= 0) patch_k(ra, sa, blk_a, nt, g, j);
-  span_scores(ra, qv, a.scale_log2, sa + 8 * g, lim, sc);
-  if (has_b) {
-    if (kPatch && blk_b >= 0) patch_k(rb, sb, blk_b, nt, g, j);
-    span_scores(rb, qv, a.scale_log2, sb + 8 * g, lim, sc + 8);
-  } else {
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 8; e < 16; ++e) sc[e] = -INFINITY;
+  for (int s = 0; s < 4; ++s) {
+    s0 = mfma(r.ka[s], qv[s], s0);
+    s1 = mfma(r.kb[s], qv[s], s1);
   }
-  float mx = sc[0];
+  float sc[8];
 #pragma unroll
-  for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
-  mx = column_max(mx);                          // finite: token sa is valid
-  const float m_new = first ? mx : fmaxf(m, mx);
-  float p[16], ps = 0.f;
+  for (int i = 0; i < 4; ++i) {
+    sc[i] = s0[i];
+    sc[4 + i] = s1[i];
+  }
+  if (!full) {
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    p[e] = __builtin_amdgcn_exp2f(sc[e] - m_new);   // argument <= 0; exp2(-inf) = 0
+    for (int e = 0; e < 8; ++e)
+      if (tv + e >= lim) sc[e] = -INFINITY;
+  }
+  float mx = vmax(vmax(vmax(sc[0], sc[1]), vmax(sc[2], sc[3])),
+                  vmax(vmax(sc[4], sc[5]), vmax(sc[6], sc[7])));
+  mx = column_max(mx);                           // finite: token `span` is live
+  const float m_new = first ? mx : vmax(m, mx);
+  const float mc = m_new * a.scale_log2;
+  float p[8], ps = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    p[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], a.scale_log2, -mc));   // <= 0; exp2(-inf) = 0
     ps += p[e];
   }
-  ps = column_sum(ps);
   if (first) {
     lsum = ps;
   } else {
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    const float alpha = __builtin_amdgcn_exp2f(fmaf(m, a.scale_log2, -mc));
     lsum = lsum * alpha + ps;
-    float ar[4];
+    if (__any(m_new > m)) {
+      float ar[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+      for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[n][i] *= ar[i];
+    }
+  }
+  m = m_new;
+  if (!full) {
+    const bool v_ok = valid_block(g < 2 ? lo : hi, a.num_blocks);
+    uint32_t mk[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      mk[w] = (v_ok && tv + 2 * w < lim ? 0x0000ffffu : 0u) |
+              (v_ok && tv + 2 * w + 1 < lim ? 0xffff0000u : 0u);
 #pragma unroll
     for (int n = 0; n < 8; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[n][i] *= ar[i];
+      for (int w = 0; w < 4; ++w) r.vf[n].w[w] &= mk[w];
   }
-  m = m_new;
-  const uint32_t pmask = j < a.G ? 0xffffffffu : 0u;
-  if (kPatch && blk_a >= 0) patch_v(ra, sa, nt, g, j);
-  span_pv(ra, p, pmask, sa + 8 * g, lim, o);
-  if (has_b) {
-    if (kPatch && blk_b >= 0) patch_v(rb, sb, nt, g, j);
-    span_pv(rb, p + 8, pmask, sb + 8 * g, lim, o);
+  if constexpr (kPatch) {
+    if (blk >= 0) patch_v(r, span, nt, g, j);
   }
+  // Rows j >= G of P belong to padding columns; they only reach O rows that
+  // are never read.
+  v8 pv;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) pv.w[w] = pdk::pack_bf16x2_rne(p[2 * w], p[2 * w + 1]);   // in [0, 1]
+#pragma unroll
+  for (int n = 0; n < 8; ++n) o[n] = mfma(pv, r.vf[n], o[n]);
 }
 
 // Scalar arguments, those the first loads need first: the compiler preloads
 // the leading ones into SGPRs (-amdgpu-kernarg-preload-count), so the query,
 // context-length and block-id loads issue without waiting for a kernarg read.
-// hgw packs Hkv (16 bits), G (8) and the wavefront count W (8).
+// The first 14 dwords arrive preloaded in SGPRs, and they hold everything
+// the first loads need: hgw packs Hkv (16 bits), G (8) and log2 of the
+// query-head split (8); mb_b the table width max_blocks (16) and B (16);
+// st_ns the split length split_tokens (16) and the split count nsplit (16).
+// (gridDim would be a load from the hidden kernel arguments: one more round
+// trip before any address exists.)
+//
+// The grid is 1-D: gs = 2^qsplit workgroups share each unit (split, KV head,
+// stream), each taking G / gs of the group's query heads over the same K/V.
+// Units go in groups of 8 and the gs workgroups of a unit are 8 ids apart,
+// so that they run on one XCD (workgroups are handed to the XCDs round robin)
+// and read the unit's K/V once from HBM: the others find it in the XCD's L2.
+// The last group, of U % 8 units, is laid out the same way with a stride of
+// U % 8 (correct anywhere, local when it happens to be).
 //
 // kRope = 0: q [B][Hq][D] bf16 as given. kRope = 1, 2 or 4: q, k and v of the
 // new token come as kRope fp32 split-K partial sums of the q|k|v projection
@@ -313,35 +346,50 @@ __device__ __forceinline__ void attend_pair(const AttnArgs& a, Span& ra, Span& r
 template <int kRope>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_attn_kernel(
     const uint16_t* q, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
-    const int32_t* ctx_lens, uint32_t hgw, int max_blocks, int num_blocks, int split_tokens,
-    int nsplit, float scale_log2, uint16_t* out, float* ws_ml, float* ws_o,
+    const int32_t* ctx_lens, uint32_t hgw, uint32_t mb_b, int num_blocks, uint32_t st_ns,
+    float scale_log2, uint16_t* out, float* ws_ml, float* ws_o,
     const float* part, int64_t part_stride, const float* inv_freq, uint16_t* ck_w,
     uint16_t* cv_w, const float* ssq, int n_ssq, float eps) {
-  __shared__ float sm_m[kMaxWaves][kMaxG];
-  __shared__ float sm_l[kMaxWaves][kMaxG];
+  __shared__ __align__(16) float sm_m[kMaxG][kMaxWaves];
+  __shared__ __align__(16) float sm_l[kMaxG][kMaxWaves];
   __shared__ __align__(16) uint16_t q_rot[kRope ? kMaxG : 1][kD];   // rotated q of the group
   __shared__ __align__(16) uint16_t kv_new[2][kD];                  // rotated k, v of the new token
-  extern __shared__ float sm_o[];                // [W][min(G, kMergeRows)][kOStride]
+  extern __shared__ float sm_o[];                // [min(G, kMergeRows)][kORow]
 
   AttnArgs a;
   a.Hkv = hgw & 0xffff;
   a.G = (hgw >> 16) & 0xff;
   a.Hq = a.Hkv * a.G;
   a.q = q; a.ck = ck; a.cv = cv; a.tables = tables; a.ctx = ctx_lens; a.out = out;
-  a.ws_ml = ws_ml; a.ws_o = ws_o; a.num_blocks = num_blocks; a.max_blocks = max_blocks;
-  a.nsplit = nsplit; a.split_tokens = split_tokens; a.scale_log2 = scale_log2;
-  const int W = hgw >> 24;
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  a.ws_ml = ws_ml; a.ws_o = ws_o; a.num_blocks = num_blocks; a.max_blocks = mb_b & 0xffff;
+  a.nsplit = st_ns >> 16; a.split_tokens = st_ns & 0xffff; a.scale_log2 = scale_log2;
+  constexpr int W = kMaxWaves;                   // every launch runs 8 wavefronts
+  const int nsplit = a.nsplit;
+  const int qsplit = hgw >> 24;
+  const int units = nsplit * a.Hkv * (int)(mb_b >> 16);
+  const int wg = blockIdx.x, full = (units >> 3) << (3 + qsplit);
+  int u, qpart;
+  if (wg < full) {
+    qpart = (wg >> 3) & ((1 << qsplit) - 1);
+    u = ((wg >> (3 + qsplit)) << 3) | (wg & 7);
+  } else {                                       // the last, partial group of units
+    const int r = units & 7, x = wg - full;
+    qpart = div_u24(x, r);
+    u = (units & ~7) + (x - qpart * r);
+  }
+  const int hb = div_u24(u, nsplit), split = u - hb * nsplit;
+  const int b = div_u24(hb, a.Hkv), h = hb - b * a.Hkv;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 4, j = lane & 15;
-  const int G = a.G;
+  const int G = a.G >> qsplit;                   // query heads of this workgroup
+  const int qh0 = h * a.G + qpart * G;           // the first of them
   int ctx_raw = a.ctx[b];
   const int s_begin = split * a.split_tokens;
   const int32_t* table = a.tables + (int64_t)b * a.max_blocks;
 
   v8 qv[4];
   if constexpr (kRope == 0) {
-    const uint16_t* qp = a.q + ((int64_t)b * a.Hq + h * G + min(j, G - 1)) * kD + g * 8;
+    const uint16_t* qp = a.q + ((int64_t)b * a.Hq + qh0 + min(j, G - 1)) * kD + g * 8;
 #pragma unroll
     for (int s = 0; s < 4; ++s) qv[s] = pdk::ld16(qp + 32 * s);
   }
@@ -375,7 +423,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int64_t n_qkv = (int64_t)(a.Hq + 2 * a.Hkv) * kD;
   const float* prow = part + (int64_t)b * n_qkv;
   auto row_col = [&](int r) -> int64_t {
-    return r < G ? (int64_t)(h * G + r) * kD
+    return r < G ? (int64_t)(qh0 + r) * kD
          : r == G ? (int64_t)(a.Hq + h) * kD
                   : (int64_t)(a.Hq + a.Hkv + h) * kD + (r - G - 1) * 64;
   };
@@ -400,12 +448,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   }
+  // Block ids of the spans at sa and sa + stride, read with scalar loads
+  // (constant address space: the table is not written during the launch), so
+  // that waiting for them never waits for the wavefront's K/V loads.
+  typedef const __attribute__((address_space(4))) int32_t* ctable_t;
+  const ctable_t ctab = (ctable_t)table;
   auto ids = [&](int sa, int* id) {
     const int sb = sa + stride;
-    id[0] = table[min(sa >> 4, mb)];
-    id[1] = table[min((sa >> 4) + 1, mb)];
-    id[2] = table[min(sb >> 4, mb)];
-    id[3] = table[min((sb >> 4) + 1, mb)];
+    id[0] = ctab[min(sa >> 4, mb)];
+    id[1] = ctab[min((sa >> 4) + 1, mb)];
+    id[2] = ctab[min(sb >> 4, mb)];
+    id[3] = ctab[min((sb >> 4) + 1, mb)];
   };
   const int sa0 = s_begin + wv * kSpan;
   int id0[4];
@@ -482,34 +535,45 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int s = 0; s < 4; ++s)
       qv[s] = *reinterpret_cast<const v8*>(&q_rot[min(j, G - 1)][32 * s + 8 * g]);
   }
-  const NewToken nt{pos, lane, a.Hkv, h, kv_new[0], kv_new[1], ck_w, cv_w};
+  const NewToken nt{pos, lane, a.Hkv, h, qpart == 0, kv_new[0], kv_new[1], ck_w, cv_w};
+  // A wavefront's spans are sa0 + k * stride. Two of them are in registers at
+  // a time (ra, rb): while one is used the other's loads are in flight, and a
+  // span's registers are refilled with the span two ahead as soon as it has
+  // been used. The block ids of the next pair are read one pair ahead.
+  auto pair = [&](auto first_c, int sa, const int* cur, int* nxt, Span& ra, Span& rb) {
+    constexpr bool kFirst = decltype(first_c)::value;
+    const int sb = sa + stride, sc = sa + 2 * stride, sd = sa + 3 * stride;
+    if (sc < s_end) ids(sc, nxt);
+    attend_span<(kRope > 0)>(a, ra, qv, sa, cur[0], cur[1], s_end, g, j, kFirst, m, lsum, o, nt);
+    if (sc < s_end) load_span(a, h, sc, g, j, nxt[0], nxt[1], ra);
+    if (sb < s_end)
+      attend_span<(kRope > 0)>(a, rb, qv, sb, cur[2], cur[3], s_end, g, j, false, m, lsum, o, nt);
+    if (sd < s_end) load_span(a, h, sd, g, j, nxt[2], nxt[3], rb);
+    return sc;
+  };
   if (active) {
-    attend_pair<(kRope > 0)>(a, ra0, rb0, has_b0, qv, sa0, sb0, s_end, g, j, true, m, lsum, o, nt,
-                             id0);
-    for (int sa = sa0 + 2 * stride; sa < s_end; sa += 2 * stride) {
-      int id[4];
-      ids(sa, id);
-      const int sb = sa + stride;
-      const bool has_b = sb < s_end;
-      Span ra, rb;
-      load_span(a, h, sa, g, j, id[0], id[1], ra);
-      if (has_b) load_span(a, h, sb, g, j, id[2], id[3], rb);
-      attend_pair<(kRope > 0)>(a, ra, rb, has_b, qv, sa, sb, s_end, g, j, false, m, lsum, o, nt,
-                               id);
+    int cur[4], nxt[4];
+    for (int sa = pair(std::true_type{}, sa0, id0, cur, ra0, rb0); sa < s_end;) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) nxt[i] = cur[i];
+      sa = pair(std::false_type{}, sa, nxt, cur, ra0, rb0);
     }
   }
+  lsum = column_sum(lsum);
+  m *= a.scale_log2;                             // log2 domain for the merge (-inf stays)
 
-  // Merge the W wavefronts through LDS, one barrier per 8 query rows. Lane (g, j) holds
-  // O rows 4g..4g+3 (the group's query heads), dims 16n+j; the four lanes of
-  // column j hold the same (m, lsum). The combine reads all kMaxWaves slots
-  // unconditionally (in flight together) and drops slots w >= W by select:
-  // with a runtime trip count each read would wait for the one before it.
+  // Merge the 8 wavefronts through LDS, one barrier per 8 query rows. Lane
+  // (g, j) holds O rows 4g..4g+3 (the group's query heads), dims 16n+j; the
+  // four lanes of column j hold the same (m, lsum). Every wavefront writes its
+  // slot, also one without tokens (m = -inf, lsum = 0, O = 0), so the combine
+  // reads all 8 slots unconditionally: (m, lsum) as two 16-byte vectors per
+  // row, O at fixed offsets from one address. A slot with m = -inf weighs 0.
   if (g == 0 && j < G) {
-    sm_m[wave][j] = m;
-    sm_l[wave][j] = lsum;
+    sm_m[j][wave] = m;
+    sm_l[j][wave] = lsum;
   }
   const int R = min(G, kMergeRows);              // rows per pass; one pass for G <= 8
-  const int64_t bq0 = (int64_t)b * a.Hq + h * G;
+  const int64_t bq0 = (int64_t)b * a.Hq + qh0;
   for (int r0 = 0; r0 < G; r0 += R) {
     if (r0 > 0) __syncthreads();                 // the previous pass has read sm_o
 #pragma unroll
@@ -517,30 +581,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int row = 4 * g + i - r0;
       if (row >= 0 && row < R && row + r0 < G) {
 #pragma unroll
-        for (int n = 0; n < 8; ++n) sm_o[(wave * R + row) * kOStride + 16 * n + j] = o[n][i];
+        for (int n = 0; n < 8; ++n) sm_o[row * kORow + wave * kOStride + 16 * n + j] = o[n][i];
       }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < R * kD; idx += 64 * W) {
-      const int row = idx / kD, d = idx - row * kD;
-      float mw[kMaxWaves], M = -INFINITY;
+    for (int idx = threadIdx.x; idx < R * kD; idx += 64 * kMaxWaves) {
+      const int row = idx >> 7, d = idx & (kD - 1);
+      const f32x4 ma = *reinterpret_cast<const f32x4*>(&sm_m[r0 + row][0]);
+      const f32x4 mb = *reinterpret_cast<const f32x4*>(&sm_m[r0 + row][4]);
+      const f32x4 la = *reinterpret_cast<const f32x4*>(&sm_l[r0 + row][0]);
+      const f32x4 lb = *reinterpret_cast<const f32x4*>(&sm_l[r0 + row][4]);
+      const float* po = &sm_o[row * kORow + d];
+      float ow[kMaxWaves];
 #pragma unroll
-      for (int w = 0; w < kMaxWaves; ++w) {
-        const float x = sm_m[w][r0 + row];
-        mw[w] = w < W ? x : -INFINITY;
-        M = fmaxf(M, mw[w]);
-      }
+      for (int w = 0; w < kMaxWaves; ++w) ow[w] = po[w * kOStride];
+      const float mw[kMaxWaves] = {ma[0], ma[1], ma[2], ma[3], mb[0], mb[1], mb[2], mb[3]};
+      const float lw[kMaxWaves] = {la[0], la[1], la[2], la[3], lb[0], lb[1], lb[2], lb[3]};
+      const float M = vmax(vmax(vmax(mw[0], mw[1]), vmax(mw[2], mw[3])),
+                           vmax(vmax(mw[4], mw[5]), vmax(mw[6], mw[7])));
+      // M = -inf: no token at all in this split (m = -inf everywhere).
+      const float Mc = M == -INFINITY ? 0.f : M;
       float L = 0.f, O = 0.f;
 #pragma unroll
       for (int w = 0; w < kMaxWaves; ++w) {
-        const int wc = min(w, W - 1);            // slots past W read a live row, then drop it
-        const float lw = sm_l[w][r0 + row], ow = sm_o[(wc * R + row) * kOStride + d];
-        // exp2 of a non-positive argument; a wavefront without tokens (m = -inf)
-        // or an unused slot contributes nothing, also when M itself is -inf.
-        const bool live = mw[w] != -INFINITY;
-        const float c = live ? __builtin_amdgcn_exp2f(mw[w] - M) : 0.f;
-        L += live ? lw * c : 0.f;
-        O += live ? ow * c : 0.f;
+        const float c = __builtin_amdgcn_exp2f(mw[w] - Mc);   // <= 0; exp2(-inf) = 0
+        L = fmaf(lw[w], c, L);
+        O = fmaf(ow[w], c, O);
       }
       const int64_t bq = bq0 + r0 + row;
       if (a.nsplit == 1) {
@@ -654,12 +720,19 @@ void* device_scratch() {
 // cache: B=16 one 10.5 us vs two 11.7 us, B=16 ctx 2048 two 28.9 us vs one
 // 32.3 us.
 struct Plan {
-  int nsplit, split_tokens, waves;
+  int nsplit, split_tokens;
+  int qsplit;                    // log2 of the workgroups sharing one unit's K/V
 };
 
 constexpr int kTargetWorkgroups = 256;
 
-Plan plan_for(int B, int Hkv, int max_ctx) {
+// After the context split, units (split, KV head, stream) that still leave
+// CUs idle are shared by 2 or 4 workgroups that divide the group's query
+// heads between them and read the same K/V (once from HBM: they run on one
+// XCD). A query's arithmetic is the same whichever workgroup computes it, so
+// this choice never changes a result. Measured per layer at ctx 512, Hq 32,
+// Hkv 8 (32-layer graph, MI355X).
+Plan plan_for(int B, int Hkv, int G, int max_ctx) {
   const int64_t pairs = (int64_t)B * Hkv;
   const int min_split = pairs >= 128 ? 1024 : pairs >= 32 ? 512 : 128;
   int64_t nsplit = (kTargetWorkgroups + pairs - 1) / pairs;
@@ -667,8 +740,9 @@ Plan plan_for(int B, int Hkv, int max_ctx) {
   nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, kMaxSplits));
   const int split_tokens = (int)round_up((max_ctx + nsplit - 1) / nsplit, kSpan);
   const int ns = (max_ctx + split_tokens - 1) / split_tokens;
-  const int waves = max(1, min(kMaxWaves, (split_tokens + 2 * kSpan - 1) / (2 * kSpan)));
-  return {ns, split_tokens, waves};
+  int qs = 0;
+  while ((2 << qs) <= G && pairs * ns * (2 << qs) <= kTargetWorkgroups) ++qs;
+  return {ns, split_tokens, qs};
 }
 
 size_t ws_bytes(int B, int Hq, int nsplit) {
@@ -721,7 +795,8 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
               "null pointer argument");
   PDK_REQUIRE((!q || pdk::aligned16(q)) && pdk::aligned16(cache_k) && pdk::aligned16(cache_v),
               "q/cache_k/cache_v must be 16-byte aligned");
-  PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1, "num_blocks and max_blocks must be >= 1");
+  PDK_REQUIRE(num_blocks >= 1 && max_blocks >= 1 && max_blocks <= 65535,
+              "num_blocks must be >= 1 and max_blocks in [1, 65535]");
   PDK_REQUIRE(max_ctx >= 1 && max_ctx <= max_blocks * 16,
               "max_ctx=%d outside [1, max_blocks*16=%d]", max_ctx, max_blocks * 16);
   // The largest context the tests cover (and the header promises).
@@ -729,8 +804,10 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
     pdk::set_error("max_ctx=%d above the supported %d", max_ctx, kMaxCtx);
     return PDK_ENOTSUP;
   }
+  PDK_REQUIRE(scale > 0.f && scale < INFINITY, "scale must be positive and finite (got %g)",
+              (double)scale);
   PDK_REQUIRE(plan_B >= B && plan_B <= 65535, "plan_batch=%d must be in [B=%d, 65535]", plan_B, B);
-  const Plan p = plan_for(plan_B, n_kv_heads, max_ctx);
+  const Plan p = plan_for(plan_B, n_kv_heads, G, max_ctx);
   AttnArgs a{};
   a.q = q;
   a.ck = cache_k;
@@ -756,15 +833,20 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
     a.ws_o = reinterpret_cast<float*>(base + round_up(bq * p.nsplit * 2 * 4, 256));
   }
   hipStream_t st = pdk::as_stream(stream);
-  const size_t lds = (size_t)p.waves * min(G, kMergeRows) * kOStride * sizeof(float);
-  const uint32_t hgw = (uint32_t)n_kv_heads | ((uint32_t)G << 16) | ((uint32_t)p.waves << 24);
-  const dim3 grid(p.nsplit, n_kv_heads, B), block(64 * p.waves);
+  const size_t lds = (size_t)min(G, kMergeRows) * kORow * sizeof(float);
+  const int64_t units = (int64_t)p.nsplit * n_kv_heads * B;
+  PDK_REQUIRE(units < (1 << 24), "B * n_kv_heads * splits = %lld is too large", (long long)units);
+  const int64_t n_wg = units << p.qsplit;
+  const uint32_t hgw = (uint32_t)n_kv_heads | ((uint32_t)G << 16) | ((uint32_t)p.qsplit << 24);
+  const uint32_t mb_b = (uint32_t)max_blocks | ((uint32_t)B << 16);
+  const uint32_t st_ns = (uint32_t)p.split_tokens | ((uint32_t)p.nsplit << 16);
+  const dim3 grid((uint32_t)n_wg), block(64 * kMaxWaves);
   const int64_t pstride = (int64_t)B * (n_q_heads + 2 * n_kv_heads) * kD;
 #define PDK_ATTN_LAUNCH(R)                                                                      \
   hipLaunchKernelGGL(decode_attn_kernel<R>, grid, block, lds, st, a.q, a.ck, a.cv, a.tables,   \
-                     a.ctx, hgw, a.max_blocks, a.num_blocks, a.split_tokens, a.nsplit,         \
-                     a.scale_log2, a.out, a.ws_ml, a.ws_o, rope.part, pstride, rope.inv_freq,  \
-                     rope.ck_w, rope.cv_w, rope.ssq, rope.n_ssq, rope.eps)
+                     a.ctx, hgw, mb_b, a.num_blocks, st_ns, a.scale_log2, a.out, a.ws_ml,     \
+                     a.ws_o, rope.part, pstride, rope.inv_freq, rope.ck_w, rope.cv_w, rope.ssq,  \
+                     rope.n_ssq, rope.eps)
   switch (rope.part ? rope.splits : 0) {
     case 0: PDK_ATTN_LAUNCH(0); break;
     case 1: PDK_ATTN_LAUNCH(1); break;
@@ -809,7 +891,7 @@ extern "C" int pdk_decode_attn_noalloc(const uint16_t* q, const uint16_t* cache_
               max_ctx, head_dim);
   PDK_REQUIRE(n_q_heads % n_kv_heads == 0, "n_q_heads=%d must be a multiple of n_kv_heads=%d",
               n_q_heads, n_kv_heads);
-  const Plan p = plan_for(B, n_kv_heads, max_ctx);
+  const Plan p = plan_for(B, n_kv_heads, n_q_heads / n_kv_heads, max_ctx);
   const size_t need = ws_bytes(B, n_q_heads, p.nsplit);
   if (need > PDK_NOALLOC_SCRATCH_BYTES) {
     pdk::set_error("this launch needs %zu bytes of split partials; the no-allocation entry "

@@ -165,6 +165,12 @@ def _attn_case(rng, B, Hq, H, ctx, D=128):
     (2, 16, 8, [200, 37]),
     (2, 64, 8, [200, 37]),
     (2, 128, 8, [300, 5]),
+    # KV-head counts that leave a partial group of 8 units, with the query
+    # heads of a unit shared by 2 or 4 workgroups
+    (1, 12, 3, [200]),
+    (3, 6, 3, [100, 517, 33]),
+    (2, 24, 3, [700, 1]),
+    (5, 80, 5, [64, 1, 999, 300, 16]),
 ])
 def test_decode_attention_vs_fp32(cuda, B, Hq, H, ctx):
     from rngd_pd_amd.kernels import decode_attention
@@ -172,8 +178,10 @@ def test_decode_attention_vs_fp32(cuda, B, Hq, H, ctx):
     q, ck, cv, tables, ctx_a = _attn_case(rng, B, Hq, H, ctx)
     scale = 1.0 / math.sqrt(128)
     want = orc.decode_attn(q, ck, cv, tables, ctx_a, scale)
-    out = decode_attention(to_dev(q), to_dev(ck), to_dev(cv), torch.from_numpy(tables).to(cuda),
-                           torch.from_numpy(ctx_a).to(cuda), int(ctx_a.max()), scale=scale)
+    # every output row must be written: start from NaN
+    out = torch.full((B, Hq, 128), float("nan"), dtype=torch.bfloat16, device=cuda)
+    decode_attention(to_dev(q), to_dev(ck), to_dev(cv), torch.from_numpy(tables).to(cuda),
+                     torch.from_numpy(ctx_a).to(cuda), int(ctx_a.max()), scale=scale, out=out)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
