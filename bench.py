@@ -466,6 +466,27 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
             g.replay()
         torch.cuda.synchronize()
         graphed = (time.perf_counter() - t0) / args.steps
+        # The same launches with attention's loads and none of its arithmetic
+        # (pdk_attn_read_probe), replayed the same way: the floor of this
+        # access pattern, block-id reads included.
+        def probe_step():
+            for l in range(L):
+                K.attn_read_probe(cache_k[l], cache_v[l], tables, ctx_lens, ctx, HQ, outp[l])
+        gp = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            probe_step()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(gp, stream=s):
+                probe_step()
+        torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            gp.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            gp.replay()
+        torch.cuda.synchronize()
+        probe_us = (time.perf_counter() - t0) / args.steps / L * 1e6
         kv_bytes = B * ctx * H * D * 2 * 2 + 2 * B * HQ * D * 2   # K+V read, q read, out write
         kern = timer.mean_s("step") / L                           # one layer's launch(es)
         res[f"B{B}"] = {
@@ -474,13 +495,16 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
             "step_us_graph": round(graphed * 1e6, 1),
             "step_us_eager": round(eager * 1e6, 1),
             "layer_call_us": round(kern * 1e6, 2),
+            "layer_us_graph": round(graphed / L * 1e6, 2),
+            "read_probe_layer_us_graph": round(probe_us, 2),
             "roofline": roofline(kv_bytes, kern,
                                  measured_traffic("decode_attn_B16") if B == 16 else None),
             "step_hbm_frac_graph": round(L * kv_bytes / graphed / 1e9 / HBM_PEAK_GBS, 4),
         }
         log(f"decode B={B}: graph {graphed*1e6:.1f} us/step ({B/graphed:.0f} tok/s), "
-            f"eager {eager*1e6:.1f} us, layer call {kern*1e6:.2f} us")
-        del ws, g
+            f"eager {eager*1e6:.1f} us, layer call {kern*1e6:.2f} us; "
+            f"loads-only probe {probe_us:.2f} us/layer")
+        del ws, g, gp
     out["extra"]["decode_batch"] = res
     out["kernels"] = dict(out.get("kernels", {}), decode_attn_B16=res[f"B{batches[-1]}"]["roofline"])
 

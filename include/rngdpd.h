@@ -513,6 +513,17 @@ int pdk_copy_kernel(void* dev_dst, const void* dev_src, size_t bytes,
 int pdk_stream_probe(int kind, void* dev_dst, const void* dev_src, size_t bytes, int flags,
                      int blocks, uint32_t key, uint32_t* dev_sink, uintptr_t stream);
 
+/* Decode attention's reads without its arithmetic: the launch pdk_decode_attn
+ * makes for the same arguments (grid, split plan, block-id reads, every K/V
+ * load), with the loaded words folded into one register per lane and stored
+ * into out ([B][n_q_heads][head_dim] bf16, contents meaningless). It measures
+ * what a kernel with attention's access pattern costs before any compute. No
+ * counterpart in the reference: measurement only. */
+int pdk_attn_read_probe(const uint16_t* cache_k, const uint16_t* cache_v, int num_blocks,
+                        const int32_t* block_tables, int max_blocks, const int32_t* ctx_lens,
+                        int max_ctx, int B, int n_q_heads, int n_kv_heads, int head_dim,
+                        uint16_t* out, uintptr_t stream);
+
 /* ---- layer-wise staging pipeline ---------------------------------------------
  * The reference hands each layer group to the writer while the next computes
  * (engines/prefill_full.py:337-388, serving/cluster.py:187-218) and loads

@@ -129,6 +129,7 @@ SIGNATURES = {
     "pdk_memcpy_d2d": (_I, [_P, _P, _SZ, _U]),
     "pdk_copy_kernel": (_I, [_P, _P, _SZ, _U]),
     "pdk_stream_probe": (_I, [_I, _P, _P, _SZ, _I, _I, ctypes.c_uint32, _P, _U]),
+    "pdk_attn_read_probe": (_I, [_P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _P, _U]),
     "pdk_stream_create": (_I, [ctypes.POINTER(_U)]),
     "pdk_stream_destroy": (_I, [_U]),
     "pdk_stream_sync": (_I, [_U]),

@@ -235,6 +235,21 @@ __device__ __forceinline__ void patch_v(Span& r, int span, const NewToken& nt, i
 // column's maximum grew (the factor is exactly 1 otherwise).
 // With kPatch (the fused RoPE path) the span's K and V take the new token nt
 // in place of the cache's contents, and its cache slot is written.
+// The read probe's stand-in for attend_span: every loaded word is folded into
+// one register, so the loads stay but no arithmetic of attention is done.
+__device__ __forceinline__ void fold_span(const Span& r, f32x4 o[8]) {
+  uint32_t x = 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) x ^= r.ka[s].w[w] ^ r.kb[s].w[w];
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) x ^= r.vf[n].w[w];
+  o[0][0] += (float)(x & 1u);
+}
+
 template <bool kPatch>
 __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8 qv[4], int span,
                                             int lo, int hi, int lim, int g, int j, bool first,
@@ -343,6 +358,8 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
 // them for the new token in place of the cache's contents. Every value is the
 // one pdk_rope_cache_append_partials computes, so the result is bit-identical
 // to that kernel followed by the kRope = 0 path.
+// kRope = -1 is the read probe (pdk_attn_read_probe): the same launch, block
+// ids and K/V loads, none of the arithmetic, one store per thread.
 template <int kRope>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_attn_kernel(
     const uint16_t* q, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
@@ -393,8 +410,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int s = 0; s < 4; ++s) qv[s] = pdk::ld16(qp + 32 * s);
   }
-  // Columns j >= G repeat query G-1 (index clamped); their P is zeroed before
-  // PV and their (m, lsum) are never read, so Q needs no mask.
+  // Columns j >= G repeat query G-1 (index clamped); their P rows only reach
+  // O rows that are never read, and their (m, lsum) are never read either, so
+  // Q needs no mask.
 
   float m = -INFINITY, lsum = 0.f;
   f32x4 o[8];
@@ -544,10 +562,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr bool kFirst = decltype(first_c)::value;
     const int sb = sa + stride, sc = sa + 2 * stride, sd = sa + 3 * stride;
     if (sc < s_end) ids(sc, nxt);
-    attend_span<(kRope > 0)>(a, ra, qv, sa, cur[0], cur[1], s_end, g, j, kFirst, m, lsum, o, nt);
+    if constexpr (kRope < 0) fold_span(ra, o);
+    else attend_span<(kRope > 0)>(a, ra, qv, sa, cur[0], cur[1], s_end, g, j, kFirst, m, lsum, o, nt);
     if (sc < s_end) load_span(a, h, sc, g, j, nxt[0], nxt[1], ra);
     if (sb < s_end)
-      attend_span<(kRope > 0)>(a, rb, qv, sb, cur[2], cur[3], s_end, g, j, false, m, lsum, o, nt);
+      if constexpr (kRope < 0) fold_span(rb, o);
+      else attend_span<(kRope > 0)>(a, rb, qv, sb, cur[2], cur[3], s_end, g, j, false, m, lsum, o, nt);
     if (sd < s_end) load_span(a, h, sd, g, j, nxt[2], nxt[3], rb);
     return sc;
   };
@@ -558,6 +578,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int i = 0; i < 4; ++i) nxt[i] = cur[i];
       sa = pair(std::false_type{}, sa, nxt, cur, ra0, rb0);
     }
+  }
+  const int64_t bq0 = (int64_t)b * a.Hq + qh0;
+  if constexpr (kRope < 0) {
+    if (threadIdx.x < G * kD) a.out[bq0 * kD + threadIdx.x] = (uint16_t)__float_as_uint(o[0][0]);
+    return;
   }
   lsum = column_sum(lsum);
   m *= a.scale_log2;                             // log2 domain for the merge (-inf stays)
@@ -573,7 +598,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     sm_l[j][wave] = lsum;
   }
   const int R = min(G, kMergeRows);              // rows per pass; one pass for G <= 8
-  const int64_t bq0 = (int64_t)b * a.Hq + qh0;
   for (int r0 = 0; r0 < G; r0 += R) {
     if (r0 > 0) __syncthreads();                 // the previous pass has read sm_o
 #pragma unroll
@@ -771,6 +795,7 @@ struct RopeIn {
   const float* ssq = nullptr;    // folded-norm row scale (pdk::row_rms), or none
   int n_ssq = 0;
   float eps = 0.f;
+  bool probe = false;            // pdk_attn_read_probe: loads only
 };
 
 int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
@@ -791,7 +816,7 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
     pdk::set_error("GQA group %d not in {1,2,4,8,16}", G);
     return PDK_ENOTSUP;
   }
-  PDK_REQUIRE((q || rope.part) && cache_k && cache_v && out && block_tables && ctx_lens,
+  PDK_REQUIRE((q || rope.part || rope.probe) && cache_k && cache_v && out && block_tables && ctx_lens,
               "null pointer argument");
   PDK_REQUIRE((!q || pdk::aligned16(q)) && pdk::aligned16(cache_k) && pdk::aligned16(cache_v),
               "q/cache_k/cache_v must be 16-byte aligned");
@@ -823,7 +848,7 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   a.nsplit = p.nsplit;
   a.split_tokens = p.split_tokens;
   a.scale_log2 = scale * 1.4426950408889634f;
-  if (p.nsplit > 1) {
+  if (p.nsplit > 1 && !rope.probe) {
     const size_t need = ws_bytes(B, n_q_heads, p.nsplit);
     PDK_REQUIRE(workspace && workspace_bytes >= need && pdk::aligned16(workspace),
                 "workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
@@ -847,7 +872,8 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
                      a.ctx, hgw, mb_b, a.num_blocks, st_ns, a.scale_log2, a.out, a.ws_ml,     \
                      a.ws_o, rope.part, pstride, rope.inv_freq, rope.ck_w, rope.cv_w, rope.ssq,  \
                      rope.n_ssq, rope.eps)
-  switch (rope.part ? rope.splits : 0) {
+  switch (rope.probe ? -1 : rope.part ? rope.splits : 0) {
+    case -1: PDK_ATTN_LAUNCH(-1); break;
     case 0: PDK_ATTN_LAUNCH(0); break;
     case 1: PDK_ATTN_LAUNCH(1); break;
     case 2: PDK_ATTN_LAUNCH(2); break;
@@ -858,7 +884,7 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   }
 #undef PDK_ATTN_LAUNCH
   int rc = pdk::check_launch("decode_attn_kernel");
-  if (rc || p.nsplit == 1) return rc;
+  if (rc || p.nsplit == 1 || rope.probe) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3(B * n_q_heads), dim3(kD), 0, st, a.ws_ml, a.ws_o,
                      p.nsplit, out);
   return pdk::check_launch("merge_kernel");
@@ -948,6 +974,18 @@ extern "C" int pdk_decode_attn_rope_rms(const float* qkv_partials, int splits,
   return launch_attn(nullptr, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens,
                      max_ctx, B, n_q_heads, n_kv_heads, head_dim, scale, workspace,
                      workspace_bytes, out, stream, rope, plan_batch > 0 ? plan_batch : B);
+}
+
+extern "C" int pdk_attn_read_probe(const uint16_t* cache_k, const uint16_t* cache_v,
+                                   int num_blocks, const int32_t* block_tables, int max_blocks,
+                                   const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads,
+                                   int n_kv_heads, int head_dim, uint16_t* out, uintptr_t stream) {
+  pdk::clear_error();
+  RopeIn probe{nullptr, 0, nullptr, nullptr, nullptr};
+  probe.probe = true;
+  return launch_attn(nullptr, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens,
+                     max_ctx, B, n_q_heads, n_kv_heads, head_dim, 1.f, nullptr, 0, out, stream,
+                     probe, B);
 }
 
 extern "C" int pdk_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* cache_k,

@@ -142,6 +142,22 @@ def decode_attention_rope(qkv_partials, inv_freq, cache_k, cache_v, block_tables
     return out
 
 
+def attn_read_probe(cache_k, cache_v, block_tables, ctx_lens, max_ctx, n_q_heads, out,
+                    stream=None):
+    """Decode attention's launch with its K/V loads and none of its arithmetic
+    (pdk_attn_read_probe): what attention's access pattern costs by itself.
+    ``out`` [B, n_q_heads, D] bf16 receives meaningless values."""
+    nb, H, D = _check_layer_cache(cache_k, cache_v)
+    B = block_tables.shape[0]
+    _need(out, "out")
+    if tuple(out.shape) != (B, n_q_heads, D):
+        raise ValueError(f"out must be [B, n_q_heads, {D}]")
+    _lib.call("pdk_attn_read_probe", cache_k.data_ptr(), cache_v.data_ptr(), nb,
+              block_tables.data_ptr(), block_tables.shape[1], ctx_lens.data_ptr(), int(max_ctx),
+              B, int(n_q_heads), H, D, out.data_ptr(), stream_handle(stream))
+    return out
+
+
 def cache_append(k_new, v_new, cache_k, cache_v, block_tables, ctx_lens, stream=None):
     """Write each stream's new k/v [B, Hkv, D] at slot ctx_lens[b]-1
     (the one-hot injection of kernels/decode_batch.py:81-82)."""

@@ -375,3 +375,21 @@ def test_stream_probe_moves_every_vector(cuda, blocks, nontemporal):
     words = dst[:n].view(torch.int32)
     assert bool((words == key).all())
     assert int(dst[n:].sum()) == 0
+
+
+@pytest.mark.gpu
+def test_attn_read_probe_runs_every_plan(cuda):
+    """The loads-only probe launches what decode attention launches (splits,
+    shared query heads, partial unit groups) without touching anything but out."""
+    from rngd_pd_amd.kernels import attn_read_probe
+    rng = np.random.default_rng(7)
+    for B, Hq, H, ctx in [(16, 32, 8, [512] * 16), (4, 32, 8, [512, 1, 300, 17]),
+                          (3, 12, 3, [2048, 5, 700]), (1, 8, 8, [1])]:
+        q, ck, cv, tables, ctx_a = _attn_case(rng, B, Hq, H, ctx)
+        dk, dv = to_dev(ck), to_dev(cv)
+        out = torch.empty((B, Hq, 128), dtype=torch.bfloat16, device=cuda)
+        attn_read_probe(dk, dv, torch.from_numpy(tables).to(cuda), torch.from_numpy(ctx_a).to(cuda),
+                        int(ctx_a.max()), Hq, out)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_host(dk), ck)
+        np.testing.assert_array_equal(to_host(dv), cv)
