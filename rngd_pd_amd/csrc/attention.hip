@@ -153,21 +153,18 @@ __device__ __forceinline__ float column_sum(float x) {
   return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
-// The new token of the fused RoPE path: its position, its rotated k and its v
-// (bf16, in LDS), and where its cache slot lives.
+// The new token of the fused RoPE path: its position and its rotated k and
+// its v (bf16, in LDS).
 struct NewToken {
-  int pos, lane, Hkv, h;
-  bool writer;                   // this workgroup writes the token's cache slot
+  int pos;
   const uint16_t* k;
   const uint16_t* v;
-  uint16_t* ck_w;
-  uint16_t* cv_w;
 };
 
 // Block of the new token in the span starting at `span` (its ids lo, hi), or
-// -1 when the span does not hold it or the id is invalid: only a valid block's
-// slot is written, by either path, and V of an invalid block is zeroed by
-// attend_span anyway.
+// -1 when the span does not hold it or the id is invalid (the block the
+// token's slot was written to in the cache, if any; V of an invalid block is
+// zeroed by attend_span anyway).
 __device__ __forceinline__ int new_token_block(const NewToken& nt, int span, int lo, int hi,
                                                int num_blocks) {
   if (nt.pos < span || nt.pos >= span + kSpan) return -1;   // wavefront-uniform
@@ -177,12 +174,10 @@ __device__ __forceinline__ int new_token_block(const NewToken& nt, int span, int
 
 // The span's K tiles take the new token's k in place of the cache's old
 // contents (lane (g, j): tile 0 row j is token span + 16 (j / 8) + 8 ((j % 8)
-// / 4) + j % 4, tile 1 the same + 4, pdk::k_unit's slot order), and the
-// wavefront writes k and v into the token's cache slot. Value selects, not a
-// branch choosing which register to store, keep the span in registers; they
-// sit right before the QK products, which wait for these loads anyway.
-__device__ __forceinline__ void patch_k(Span& r, int span, int blk, const NewToken& nt, int g,
-                                        int j) {
+// / 4) + j % 4, tile 1 the same + 4, pdk::k_unit's slot order). Value selects,
+// not a branch choosing which register to store, keep the span in registers;
+// they sit right before the QK products, which wait for these loads anyway.
+__device__ __forceinline__ void patch_k(Span& r, int span, const NewToken& nt, int g, int j) {
   const int j8 = j & 7;
   const int ta = span + ((j >> 3) << 4) + ((j8 >> 2) << 3) + (j8 & 3);
   const bool in_a = ta == nt.pos, in_b = ta + 4 == nt.pos;
@@ -195,15 +190,6 @@ __device__ __forceinline__ void patch_k(Span& r, int span, int blk, const NewTok
       r.kb[s].w[w] = in_b ? k.w[w] : r.kb[s].w[w];
     }
   }
-  if (!nt.writer) return;
-  const int slot = nt.pos & 15;
-  uint16_t* kb = nt.ck_w + ((int64_t)blk * nt.Hkv + nt.h) * 16 * kD;
-  uint16_t* vb = nt.cv_w + ((int64_t)blk * nt.Hkv + nt.h) * kD * 16;
-  if (nt.lane < kD / 8)
-    pdk::st16(kb + pdk::k_unit(slot, 8 * nt.lane, kD) * 8,
-              *reinterpret_cast<const v8*>(nt.k + 8 * nt.lane));
-#pragma unroll
-  for (int d = nt.lane; d < kD; d += 64) vb[(int64_t)d * 16 + slot] = nt.v[d];
 }
 
 // The span's V rows take the new token's v (lane (g, j) holds dims j + 16n of
@@ -261,7 +247,7 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
   int blk = -1;
   if constexpr (kPatch) {
     blk = new_token_block(nt, span, lo, hi, a.num_blocks);
-    if (blk >= 0) patch_k(r, span, blk, nt, g, j);
+    if (blk >= 0) patch_k(r, span, nt, g, j);
   }
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -307,6 +293,9 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
     }
   }
   m = m_new;
+  if constexpr (kPatch) {
+    if (blk >= 0) patch_v(r, span, nt, g, j);
+  }
   if (!full) {
     const bool v_ok = valid_block(g < 2 ? lo : hi, a.num_blocks);
     uint32_t mk[4];
@@ -318,9 +307,6 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
     for (int n = 0; n < 8; ++n)
 #pragma unroll
       for (int w = 0; w < 4; ++w) r.vf[n].w[w] &= mk[w];
-  }
-  if constexpr (kPatch) {
-    if (blk >= 0) patch_v(r, span, nt, g, j);
   }
   // Rows j >= G of P belong to padding columns; they only reach O rows that
   // are never read.
@@ -349,9 +335,11 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
 // The last group, of U % 8 units, is laid out the same way with a stride of
 // U % 8 (correct anywhere, local when it happens to be).
 //
-// kRope = 0: q [B][Hq][D] bf16 as given. kRope = 1, 2 or 4: q, k and v of the
-// new token come as kRope fp32 split-K partial sums of the q|k|v projection
-// (part, [kRope][B][(Hq + 2 Hkv) D], split s at s * part_stride): the
+// kRope = 0: src is q [B][Hq][D] bf16. kRope = 1, 2 or 4: src is the q, k and
+// v of the new token as kRope fp32 split-K partial sums of the q|k|v
+// projection ([kRope][B][(Hq + 2 Hkv) D]; passing them in q's place keeps them
+// among the preloaded arguments, so their loads, and the K/V loads behind
+// them, do not wait for a kernel-argument read): the
 // workgroup adds them in split order, rounds to bf16, rotates q and k (RoPE at
 // position ctx-1, angle pos * inv_freq[i]) into LDS, writes the new k and v to
 // their cache slot (the workgroup whose split holds that position), and uses
@@ -362,11 +350,12 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
 // ids and K/V loads, none of the arithmetic, one store per thread.
 template <int kRope>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_attn_kernel(
-    const uint16_t* q, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
+    const void* src, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
     const int32_t* ctx_lens, uint32_t hgw, uint32_t mb_b, int num_blocks, uint32_t st_ns,
-    float scale_log2, uint16_t* out, float* ws_ml, float* ws_o,
-    const float* part, int64_t part_stride, const float* inv_freq, uint16_t* ck_w,
-    uint16_t* cv_w, const float* ssq, int n_ssq, float eps) {
+    float scale_log2, uint16_t* out, float* ws_ml, float* ws_o, const float* inv_freq,
+    uint16_t* ck_w, uint16_t* cv_w, const float* ssq, int n_ssq, float eps) {
+  const uint16_t* q = static_cast<const uint16_t*>(src);
+  const float* part = static_cast<const float*>(src);
   __shared__ __align__(16) float sm_m[kMaxG][kMaxWaves];
   __shared__ __align__(16) float sm_l[kMaxG][kMaxWaves];
   __shared__ __align__(16) uint16_t q_rot[kRope ? kMaxG : 1][kD];   // rotated q of the group
@@ -439,6 +428,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int kParts = kRope > 0 ? kRope : 1;
   const int n_rows = G + 3;
   const int64_t n_qkv = (int64_t)(a.Hq + 2 * a.Hkv) * kD;
+  const int64_t part_stride = (int64_t)(mb_b >> 16) * n_qkv;   // one split of the partials
   const float* prow = part + (int64_t)b * n_qkv;
   auto row_col = [&](int r) -> int64_t {
     return r < G ? (int64_t)(qh0 + r) * kD
@@ -447,12 +437,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   float raw[kPre][2][kParts];
   float ifreq = 0.f;
-  // The row scale's loads go out with the partial sums', before any K/V load;
-  // it is finished after those are issued (loads complete in order).
   pdk::RowRms rr{};
   if constexpr (kRope > 0) {
-    if (ssq) rr = pdk::row_rms_load(ssq, b, n_ssq, lane);
-    ifreq = inv_freq[lane];
 #pragma unroll
     for (int k = 0; k < kPre; ++k) {
       const int r = wv + k * W;
@@ -482,6 +468,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int id0[4];
   ids(sa0, id0);
   asm volatile("" : "+s"(ctx_raw) : "s"(id0[0]), "s"(id0[1]), "s"(id0[2]), "s"(id0[3]));
+  // The arguments past the preloaded ones (inv_freq, ssq) arrive with the
+  // block ids; the row scale's loads and the frequencies go out after the
+  // partial sums' and before any K/V load (a wavefront's loads complete in
+  // order), and the scale is finished after the K/V loads are issued.
+  if constexpr (kRope > 0) {
+    if (ssq) rr = pdk::row_rms_load(ssq, b, n_ssq, lane);
+    ifreq = inv_freq[lane];
+  }
   const int ctx = min(ctx_raw, a.max_blocks * 16);
   const int s_end = (split == a.nsplit - 1) ? ctx : min(ctx, s_begin + a.split_tokens);
   const int pos = ctx_raw - 1;                   // the new token (fused RoPE path)
@@ -552,8 +546,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       qv[s] = *reinterpret_cast<const v8*>(&q_rot[min(j, G - 1)][32 * s + 8 * g]);
+    // The new token's k and v into its cache slot, by one wavefront of the
+    // workgroup with the group's first query heads and the split that holds
+    // the position: issued now, behind every K/V load of the wavefront, the
+    // stores complete while the loads' data arrives (the spans that hold the
+    // token take its k and v from LDS, not from the cache).
+    if (qpart == 0 && wv == 0 && pos >= s_begin && pos < s_end) {
+      const int blk = ctab[min(pos >> 4, mb)];
+      if (valid_block(blk, a.num_blocks)) {
+        const int slot = pos & 15;
+        uint16_t* kb = ck_w + ((int64_t)blk * a.Hkv + h) * 16 * kD;
+        uint16_t* vb = cv_w + ((int64_t)blk * a.Hkv + h) * kD * 16;
+        if (lane < kD / 8)
+          pdk::st16(kb + pdk::k_unit(slot, 8 * lane, kD) * 8,
+                    *reinterpret_cast<const v8*>(&kv_new[0][8 * lane]));
+#pragma unroll
+        for (int d = lane; d < kD; d += 64) vb[(int64_t)d * 16 + slot] = kv_new[1][d];
+      }
+    }
   }
-  const NewToken nt{pos, lane, a.Hkv, h, qpart == 0, kv_new[0], kv_new[1], ck_w, cv_w};
+  const NewToken nt{pos, kv_new[0], kv_new[1]};
   // A wavefront's spans are sa0 + k * stride. Two of them are in registers at
   // a time (ra, rb): while one is used the other's loads are in flight, and a
   // span's registers are refilled with the span two ahead as soon as it has
@@ -866,12 +878,11 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   const uint32_t mb_b = (uint32_t)max_blocks | ((uint32_t)B << 16);
   const uint32_t st_ns = (uint32_t)p.split_tokens | ((uint32_t)p.nsplit << 16);
   const dim3 grid((uint32_t)n_wg), block(64 * kMaxWaves);
-  const int64_t pstride = (int64_t)B * (n_q_heads + 2 * n_kv_heads) * kD;
+  const void* src = rope.part ? static_cast<const void*>(rope.part) : static_cast<const void*>(a.q);
 #define PDK_ATTN_LAUNCH(R)                                                                      \
-  hipLaunchKernelGGL(decode_attn_kernel<R>, grid, block, lds, st, a.q, a.ck, a.cv, a.tables,   \
+  hipLaunchKernelGGL(decode_attn_kernel<R>, grid, block, lds, st, src, a.ck, a.cv, a.tables,   \
                      a.ctx, hgw, mb_b, a.num_blocks, st_ns, a.scale_log2, a.out, a.ws_ml,     \
-                     a.ws_o, rope.part, pstride, rope.inv_freq, rope.ck_w, rope.cv_w, rope.ssq,  \
-                     rope.n_ssq, rope.eps)
+                     a.ws_o, rope.inv_freq, rope.ck_w, rope.cv_w, rope.ssq, rope.n_ssq, rope.eps)
   switch (rope.probe ? -1 : rope.part ? rope.splits : 0) {
     case -1: PDK_ATTN_LAUNCH(-1); break;
     case 0: PDK_ATTN_LAUNCH(0); break;
