@@ -98,11 +98,15 @@ constexpr int depth_for(int tiles) {
 template <int kTiles, int kCols, int kEpi, bool kTiled>
 __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w, int B,
-                                                            int K, int N,
+                                                            int K, int N, int splits, float* ssq,
                                                             const uint16_t* r, uint16_t* y,
                                                             uint64_t* keys, float* part,
-                                                            float* ssq, int n_ssq, float eps,
-                                                            int* counters) {
+                                                            float eps, int* counters) {
+  // The arguments up to y (14 dwords) arrive preloaded in SGPRs: everything
+  // the first loads need, including the split count (gridDim.y would be a
+  // load from the hidden kernel arguments, a round trip before the first
+  // weight load) and the row sums of squares. Their row length is K / 16.
+  const int n_ssq = K >> 4;
   constexpr bool kGLU = kEpi == kSwiGLU || kEpi == kSwiGLURms;
   constexpr bool kRowScale = kEpi == kSwiGLURms || kEpi == kArgmaxRms || kEpi == kPartialRms;
   constexpr bool kArg = kEpi == kArgmax || kEpi == kArgmaxRms;
@@ -141,10 +145,10 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   // cycle through kDepth slots; a slot past the wave's last step loads that
   // last step again (a valid address) and its X operand is zeroed, so every
   // load is unconditional and the tail adds nothing.
-  // Split-K over gridDim.y workgroups: this one takes steps [s_lo, s_hi).
+  // Split-K over `splits` (= gridDim.y) workgroups: this one takes steps [s_lo, s_hi).
   const int steps_all = K / kStepK;
-  const int s_lo = (int)((int64_t)blockIdx.y * steps_all / gridDim.y);
-  const int s_hi = (int)((int64_t)(blockIdx.y + 1) * steps_all / gridDim.y);
+  const int s_lo = (int)((int64_t)blockIdx.y * steps_all / splits);
+  const int s_hi = (int)((int64_t)(blockIdx.y + 1) * steps_all / splits);
   const int steps = s_hi - s_lo;
   // Steps of this wave: wave, wave + kWaves, ... (so the workgroup's waves
   // read consecutive k blocks together; with tiled weights that is one
@@ -339,13 +343,13 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
     if (threadIdx.x == 0) {
       int* cnt = counters + blockIdx.x;
       const int done = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = done == (int)gridDim.y - 1;
+      const int last = done == splits - 1;
       if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       is_last = last;
     }
     __syncthreads();
     if (!is_last) return;
-    const int S = gridDim.y;
+    const int S = splits;
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
       for (int e = threadIdx.x; e < 256 * kCols; e += kWaves * 64) {
@@ -390,7 +394,7 @@ int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const
                 int* counters = nullptr) {
   const dim3 grid((N + 16 * kCols - 1) / (16 * kCols), splits), block(kWaves * 64);
 #define PDK_WGEMM(T) \
-  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled>), grid, block, 0, st, x, w, B, K, N, r, y, keys, part, ssq, n_ssq, eps, counters)
+  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled>), grid, block, 0, st, x, w, B, K, N, splits, ssq, r, y, keys, part, eps, counters)
   switch ((B + 15) / 16) {
     case 1: PDK_WGEMM(1); break;
     case 2: PDK_WGEMM(2); break;
