@@ -146,7 +146,10 @@ def test_rope_from_partials_equals_rounded_sum(cuda, splits):
 
 @pytest.mark.parametrize("B,splits,NH,NKV", [(16, 2, 32, 8), (4, 2, 32, 8), (1, 1, 32, 8),
                                              (5, 4, 32, 8), (4, 2, 8, 8), (3, 1, 16, 8),
-                                             (6, 2, 64, 8), (2, 4, 32, 2), (16, 1, 16, 1)])
+                                             (6, 2, 64, 8), (2, 4, 32, 2), (16, 1, 16, 1),
+                                             # units in a partial group of 8, query heads
+                                             # shared by 2 or 4 workgroups
+                                             (5, 2, 12, 3), (7, 1, 6, 3)])
 def test_fused_rope_attention_equals_two_calls(cuda, B, splits, NH, NKV):
     """pdk_decode_attn_rope against pdk_rope_cache_append_partials followed by
     pdk_decode_attn on copies of the same cache: bit-identical outputs and
