@@ -1,10 +1,12 @@
 // GQA decode attention over the paged KV cache, gfx950.
 //
-// Grid (nsplit, Hkv, B); a workgroup of 8 wavefronts owns the token range
-// [split*split_tokens, (split+1)*split_tokens) of stream b, KV head h. With
-// B*Hkv >= 128 the host uses one split (no merge at all); smaller batches
-// split the context so the launch still spreads over the CUs, and a second
-// small kernel merges the splits.
+// A unit is the token range [split*split_tokens, (split+1)*split_tokens) of
+// stream b, KV head h, and 1, 2, 4 or 8 workgroups of 8 wavefronts share it:
+// each computes the scores of its share of the group's query heads over all
+// of the unit's K, and their output over its share of V's dims (all, or one
+// half). With B*Hkv >= 128 the host uses one split (no merge at all); smaller
+// batches split the context so the launch still spreads over the CUs, and a
+// second small kernel merges the splits.
 //
 // A wavefront walks the 32-token spans wave, wave + 8, ... of its range with
 // two spans' loads in flight: while one span is used the next one's loads
@@ -17,8 +19,9 @@
 //   3. online softmax in fp32 in the exp2 domain (two lane swaps per column
 //      reduction), rescaling the running output when a maximum grew; spans
 //      whose tokens are all live skip every mask;
-//   4. PV: 8 v_mfma_f32_16x16x32_bf16 (one per 16-dim tile), A = P straight
-//      from the QK accumulators, B = V.
+//   4. PV: one v_mfma_f32_16x16x32_bf16 per 16-dim tile of V the workgroup
+//      computes (8, or 4 for a half), A = P straight from the QK
+//      accumulators, B = V.
 // MFMA multiplies along the 8 contiguous elements a lane holds, so the cache
 // keeps K as 16-byte units of 8 dims of one token, tiled in the order the QK
 // tiles read them (pdk::k_unit: one K load instruction reads 512 contiguous
@@ -98,6 +101,7 @@ __device__ __forceinline__ bool valid_block(int blk, int num_blocks) {
 // block 0) so they are all in flight together; V of tokens >= lim and of
 // invalid blocks is zeroed before use, K of tokens >= lim needs nothing (their
 // scores become -inf).
+template <int kNV>
 __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, int g, int j,
                                           int blk_lo, int blk_hi, Span& r) {
   // QK tile 0 row j is token span + 8(j/4) + j%4 and tile 1 row j that token
@@ -118,7 +122,7 @@ __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, in
     r.kb[s] = pdk::ld16(pk + ((4 + s) * 4 * 8) * 8);
   }
 #pragma unroll
-  for (int n = 0; n < 8; ++n) r.vf[n] = pdk::ld16(pv + 16 * 16 * n);
+  for (int n = 0; n < kNV; ++n) r.vf[n] = pdk::ld16(pv + 16 * 16 * n);
 }
 
 // Reductions over the four lanes of one query column {i, i^16, i^32, i^48}
@@ -194,14 +198,15 @@ __device__ __forceinline__ void patch_k(Span& r, int span, const NewToken& nt, i
 
 // The span's V rows take the new token's v (lane (g, j) holds dims j + 16n of
 // tokens span + 8g .. + 7), right before the PV products.
+template <int kNV>
 __device__ __forceinline__ void patch_v(Span& r, int span, const NewToken& nt, int g, int j) {
   const int tv = span + 8 * g;
   const bool in_v = nt.pos >= tv && nt.pos < tv + 8;
   const int e = nt.pos - tv, word = e >> 1;
   const uint32_t keep = (e & 1) ? 0x0000ffffu : 0xffff0000u;
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    const uint32_t bits = (uint32_t)nt.v[(j + 16 * n) & (kD - 1)] << ((e & 1) * 16);
+  for (int n = 0; n < kNV; ++n) {
+    const uint32_t bits = (uint32_t)nt.v[j + 16 * n] << ((e & 1) * 16);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const bool hit = in_v && w == word;
@@ -210,19 +215,9 @@ __device__ __forceinline__ void patch_v(Span& r, int span, const NewToken& nt, i
   }
 }
 
-// Fold one span into the running state of query column j = lane & 15: m, the
-// largest raw score so far (the same in the column's four lanes), lsum, this
-// lane's own sum of weights 2^(c*s - c*m) (c = scale * log2(e) > 0; the
-// column's four sums are added once, at the end), and o, the weighted sum of
-// V rows (lane (g, j) holds query rows 4g..4g+3, dims 16n + j). Spans whose
-// 32 tokens are all live and whose block ids are valid (a wavefront-uniform
-// test) skip every mask; the others give tokens >= lim the score -inf and
-// zero V of those tokens and of invalid blocks. O is rescaled only when some
-// column's maximum grew (the factor is exactly 1 otherwise).
-// With kPatch (the fused RoPE path) the span's K and V take the new token nt
-// in place of the cache's contents, and its cache slot is written.
 // The read probe's stand-in for attend_span: every loaded word is folded into
 // one register, so the loads stay but no arithmetic of attention is done.
+template <int kNV>
 __device__ __forceinline__ void fold_span(const Span& r, f32x4 o[8]) {
   uint32_t x = 0;
 #pragma unroll
@@ -230,13 +225,27 @@ __device__ __forceinline__ void fold_span(const Span& r, f32x4 o[8]) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) x ^= r.ka[s].w[w] ^ r.kb[s].w[w];
 #pragma unroll
-  for (int n = 0; n < 8; ++n)
+  for (int n = 0; n < kNV; ++n)
 #pragma unroll
     for (int w = 0; w < 4; ++w) x ^= r.vf[n].w[w];
   o[0][0] += (float)(x & 1u);
 }
 
-template <bool kPatch>
+// Fold one span into the running state of query column j = lane & 15: m, the
+// largest raw score so far (the same in the column's four lanes), lsum, this
+// lane's own sum of weights 2^(c*s - c*m) (c = scale * log2(e) > 0; the
+// column's four sums are added once, at the end), and o, the weighted sum of
+// V rows (lane (g, j) holds query rows 4g..4g+3, dims 16n + j of the kNV
+// 16-dim tiles the workgroup computes: all 8, or one half of V). Spans whose
+// 32 tokens are all live and whose block ids are valid (a wavefront-uniform
+// test) skip every mask; the others give tokens >= lim the score -inf and
+// zero V of those tokens and of invalid blocks. O is rescaled only when some
+// column's maximum grew, by a factor that is exactly 1 for the other columns,
+// so the arithmetic of a query column is the same whatever columns share its
+// wavefront.
+// With kPatch (the fused RoPE path) the span's K and V take the new token nt
+// in place of the cache's contents.
+template <bool kPatch, int kNV>
 __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8 qv[4], int span,
                                             int lo, int hi, int lim, int g, int j, bool first,
                                             float& m, float& lsum, f32x4 o[8],
@@ -280,21 +289,24 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
   if (first) {
     lsum = ps;
   } else {
-    const float alpha = __builtin_amdgcn_exp2f(fmaf(m, a.scale_log2, -mc));
+    // Exactly 1 unless this column's maximum grew (the fma would otherwise
+    // leave the rounding residual of m * c in the exponent): a column's sums
+    // then never depend on which other columns share the wavefront.
+    const float alpha = m_new > m ? __builtin_amdgcn_exp2f(fmaf(m, a.scale_log2, -mc)) : 1.f;
     lsum = lsum * alpha + ps;
     if (__any(m_new > m)) {
       float ar[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
 #pragma unroll
-      for (int n = 0; n < 8; ++n)
+      for (int n = 0; n < kNV; ++n)
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[n][i] *= ar[i];
     }
   }
   m = m_new;
   if constexpr (kPatch) {
-    if (blk >= 0) patch_v(r, span, nt, g, j);
+    if (blk >= 0) patch_v<kNV>(r, span, nt, g, j);
   }
   if (!full) {
     const bool v_ok = valid_block(g < 2 ? lo : hi, a.num_blocks);
@@ -304,7 +316,7 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
       mk[w] = (v_ok && tv + 2 * w < lim ? 0x0000ffffu : 0u) |
               (v_ok && tv + 2 * w + 1 < lim ? 0xffff0000u : 0u);
 #pragma unroll
-    for (int n = 0; n < 8; ++n)
+    for (int n = 0; n < kNV; ++n)
 #pragma unroll
       for (int w = 0; w < 4; ++w) r.vf[n].w[w] &= mk[w];
   }
@@ -314,7 +326,7 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
 #pragma unroll
   for (int w = 0; w < 4; ++w) pv.w[w] = pdk::pack_bf16x2_rne(p[2 * w], p[2 * w + 1]);   // in [0, 1]
 #pragma unroll
-  for (int n = 0; n < 8; ++n) o[n] = mfma(pv, r.vf[n], o[n]);
+  for (int n = 0; n < kNV; ++n) o[n] = mfma(pv, r.vf[n], o[n]);
 }
 
 // Scalar arguments, those the first loads need first: the compiler preloads
@@ -327,13 +339,15 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
 // (gridDim would be a load from the hidden kernel arguments: one more round
 // trip before any address exists.)
 //
-// The grid is 1-D: gs = 2^qsplit workgroups share each unit (split, KV head,
-// stream), each taking G / gs of the group's query heads over the same K/V.
-// Units go in groups of 8 and the gs workgroups of a unit are 8 ids apart,
-// so that they run on one XCD (workgroups are handed to the XCDs round robin)
-// and read the unit's K/V once from HBM: the others find it in the XCD's L2.
-// The last group, of U % 8 units, is laid out the same way with a stride of
-// U % 8 (correct anywhere, local when it happens to be).
+// The grid is 1-D: 2^(qsplit + kVS) workgroups share each unit (split, KV
+// head, stream), each taking G / 2^qsplit of the group's query heads and, with
+// kNV = 4 (kVS = 1), one half of V's dims, over the same K (part id p: query
+// part p >> kVS, V half p & kVS). Units go in groups of 8 and the workgroups
+// of a unit are 8 ids apart, so that they run on one XCD (workgroups are
+// handed to the XCDs round robin) and read the unit's K/V once from HBM: the
+// others find it in the XCD's L2. The last group, of U % 8 units, is laid out
+// the same way with a stride of U % 8 (correct anywhere, local when it
+// happens to be).
 //
 // kRope = 0: src is q [B][Hq][D] bf16. kRope = 1, 2 or 4: src is the q, k and
 // v of the new token as kRope fp32 split-K partial sums of the q|k|v
@@ -348,7 +362,7 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
 // to that kernel followed by the kRope = 0 path.
 // kRope = -1 is the read probe (pdk_attn_read_probe): the same launch, block
 // ids and K/V loads, none of the arithmetic, one store per thread.
-template <int kRope>
+template <int kRope, int kNV>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_attn_kernel(
     const void* src, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
     const int32_t* ctx_lens, uint32_t hgw, uint32_t mb_b, int num_blocks, uint32_t st_ns,
@@ -371,18 +385,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   a.nsplit = st_ns >> 16; a.split_tokens = st_ns & 0xffff; a.scale_log2 = scale_log2;
   constexpr int W = kMaxWaves;                   // every launch runs 8 wavefronts
   const int nsplit = a.nsplit;
+  constexpr int kVS = kNV == 8 ? 0 : 1;         // log2 of the parts V's dims are split in
+  constexpr int kDV = 16 * kNV;                  // dims of O this workgroup computes
   const int qsplit = hgw >> 24;
+  const int gs = qsplit + kVS;                   // log2 of the workgroups sharing a unit
   const int units = nsplit * a.Hkv * (int)(mb_b >> 16);
-  const int wg = blockIdx.x, full = (units >> 3) << (3 + qsplit);
-  int u, qpart;
+  const int wg = blockIdx.x, full = (units >> 3) << (3 + gs);
+  int u, part_id;
   if (wg < full) {
-    qpart = (wg >> 3) & ((1 << qsplit) - 1);
-    u = ((wg >> (3 + qsplit)) << 3) | (wg & 7);
+    part_id = (wg >> 3) & ((1 << gs) - 1);
+    u = ((wg >> (3 + gs)) << 3) | (wg & 7);
   } else {                                       // the last, partial group of units
     const int r = units & 7, x = wg - full;
-    qpart = div_u24(x, r);
-    u = (units & ~7) + (x - qpart * r);
+    part_id = div_u24(x, r);
+    u = (units & ~7) + (x - part_id * r);
   }
+  const int qpart = part_id >> kVS, vd0 = (part_id & kVS) * kDV;
+  a.cv += vd0 * 16;                              // V rows (dims) vd0 .. vd0 + kDV - 1
   const int hb = div_u24(u, nsplit), split = u - hb * nsplit;
   const int b = div_u24(hb, a.Hkv), h = hb - b * a.Hkv;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -492,11 +511,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // the loads stay under the branch (measured 0.5 us per layer faster).
   Span ra0, rb0;
   if constexpr (kRope > 0) {
-    load_span(a, h, sa0, g, j, active ? id0[0] : 0, active ? id0[1] : 0, ra0);
-    load_span(a, h, sb0, g, j, has_b0 ? id0[2] : 0, has_b0 ? id0[3] : 0, rb0);
+    load_span<kNV>(a, h, sa0, g, j, active ? id0[0] : 0, active ? id0[1] : 0, ra0);
+    load_span<kNV>(a, h, sb0, g, j, has_b0 ? id0[2] : 0, has_b0 ? id0[3] : 0, rb0);
   } else if (active) {
-    load_span(a, h, sa0, g, j, id0[0], id0[1], ra0);
-    if (has_b0) load_span(a, h, sb0, g, j, id0[2], id0[3], rb0);
+    load_span<kNV>(a, h, sa0, g, j, id0[0], id0[1], ra0);
+    if (has_b0) load_span<kNV>(a, h, sb0, g, j, id0[2], id0[3], rb0);
   }
   if constexpr (kRope > 0) {
     // Second phase, while the first pair's K/V loads are in flight: add the
@@ -547,11 +566,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int s = 0; s < 4; ++s)
       qv[s] = *reinterpret_cast<const v8*>(&q_rot[min(j, G - 1)][32 * s + 8 * g]);
     // The new token's k and v into its cache slot, by one wavefront of the
-    // workgroup with the group's first query heads and the split that holds
-    // the position: issued now, behind every K/V load of the wavefront, the
+    // unit's first workgroup (part 0), in the split that holds the position: issued now, behind every K/V load of the wavefront, the
     // stores complete while the loads' data arrives (the spans that hold the
     // token take its k and v from LDS, not from the cache).
-    if (qpart == 0 && wv == 0 && pos >= s_begin && pos < s_end) {
+    if (part_id == 0 && wv == 0 && pos >= s_begin && pos < s_end) {
       const int blk = ctab[min(pos >> 4, mb)];
       if (valid_block(blk, a.num_blocks)) {
         const int slot = pos & 15;
@@ -565,7 +583,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   }
-  const NewToken nt{pos, kv_new[0], kv_new[1]};
+  const NewToken nt{pos, kv_new[0], kv_new[1] + vd0};
   // A wavefront's spans are sa0 + k * stride. Two of them are in registers at
   // a time (ra, rb): while one is used the other's loads are in flight, and a
   // span's registers are refilled with the span two ahead as soon as it has
@@ -574,13 +592,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr bool kFirst = decltype(first_c)::value;
     const int sb = sa + stride, sc = sa + 2 * stride, sd = sa + 3 * stride;
     if (sc < s_end) ids(sc, nxt);
-    if constexpr (kRope < 0) fold_span(ra, o);
-    else attend_span<(kRope > 0)>(a, ra, qv, sa, cur[0], cur[1], s_end, g, j, kFirst, m, lsum, o, nt);
-    if (sc < s_end) load_span(a, h, sc, g, j, nxt[0], nxt[1], ra);
-    if (sb < s_end)
-      if constexpr (kRope < 0) fold_span(rb, o);
-      else attend_span<(kRope > 0)>(a, rb, qv, sb, cur[2], cur[3], s_end, g, j, false, m, lsum, o, nt);
-    if (sd < s_end) load_span(a, h, sd, g, j, nxt[2], nxt[3], rb);
+    if constexpr (kRope < 0) fold_span<kNV>(ra, o);
+    else attend_span<(kRope > 0), kNV>(a, ra, qv, sa, cur[0], cur[1], s_end, g, j, kFirst, m, lsum, o, nt);
+    if (sc < s_end) load_span<kNV>(a, h, sc, g, j, nxt[0], nxt[1], ra);
+    if (sb < s_end) {
+      if constexpr (kRope < 0) fold_span<kNV>(rb, o);
+      else attend_span<(kRope > 0), kNV>(a, rb, qv, sb, cur[2], cur[3], s_end, g, j, false, m, lsum, o, nt);
+    }
+    if (sd < s_end) load_span<kNV>(a, h, sd, g, j, nxt[2], nxt[3], rb);
     return sc;
   };
   if (active) {
@@ -593,7 +612,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   const int64_t bq0 = (int64_t)b * a.Hq + qh0;
   if constexpr (kRope < 0) {
-    if (threadIdx.x < G * kD) a.out[bq0 * kD + threadIdx.x] = (uint16_t)__float_as_uint(o[0][0]);
+    const int t = threadIdx.x;
+    if (t < G * kDV) a.out[(bq0 + t / kDV) * kD + vd0 + t % kDV] = (uint16_t)__float_as_uint(o[0][0]);
     return;
   }
   lsum = column_sum(lsum);
@@ -617,12 +637,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int row = 4 * g + i - r0;
       if (row >= 0 && row < R && row + r0 < G) {
 #pragma unroll
-        for (int n = 0; n < 8; ++n) sm_o[row * kORow + wave * kOStride + 16 * n + j] = o[n][i];
+        for (int n = 0; n < kNV; ++n) sm_o[row * kORow + wave * kOStride + 16 * n + j] = o[n][i];
       }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < R * kD; idx += 64 * kMaxWaves) {
-      const int row = idx >> 7, d = idx & (kD - 1);
+    for (int idx = threadIdx.x; idx < R * kDV; idx += 64 * kMaxWaves) {
+      const int row = idx / kDV, d = idx % kDV;
       const f32x4 ma = *reinterpret_cast<const f32x4*>(&sm_m[r0 + row][0]);
       const f32x4 mb = *reinterpret_cast<const f32x4*>(&sm_m[r0 + row][4]);
       const f32x4 la = *reinterpret_cast<const f32x4*>(&sm_l[r0 + row][0]);
@@ -647,10 +667,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int64_t bq = bq0 + r0 + row;
       if (a.nsplit == 1) {
         const float inv = L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
-        a.out[bq * kD + d] = (uint16_t)pdk::f32_to_bf16_rne(O * inv);
+        a.out[bq * kD + vd0 + d] = (uint16_t)pdk::f32_to_bf16_rne(O * inv);
       } else {
-        a.ws_o[(bq * a.nsplit + split) * kD + d] = O;
-        if (d == 0) {
+        a.ws_o[(bq * a.nsplit + split) * kD + vd0 + d] = O;
+        if (vd0 + d == 0) {
           a.ws_ml[(bq * a.nsplit + split) * 2 + 0] = M;
           a.ws_ml[(bq * a.nsplit + split) * 2 + 1] = L;
         }
@@ -757,28 +777,38 @@ void* device_scratch() {
 // 32.3 us.
 struct Plan {
   int nsplit, split_tokens;
-  int qsplit;                    // log2 of the workgroups sharing one unit's K/V
+  int qsplit;                    // log2 of the parts a unit's query heads are split in
+  int vsplit;                    // 1: V's dims split in two halves, 0: whole
 };
 
 constexpr int kTargetWorkgroups = 256;
 
 // After the context split, units (split, KV head, stream) that still leave
-// CUs idle are shared by 2 or 4 workgroups that divide the group's query
-// heads between them and read the same K/V (once from HBM: they run on one
-// XCD). A query's arithmetic is the same whichever workgroup computes it, so
-// this choice never changes a result. Measured per layer at ctx 512, Hq 32,
-// Hkv 8 (32-layer graph, MI355X).
-Plan plan_for(int B, int Hkv, int G, int max_ctx) {
-  const int64_t pairs = (int64_t)B * Hkv;
+// CUs idle are shared by 2, 4 or 8 workgroups on one XCD, which read the same
+// K from HBM once (the others find it in the XCD's L2). First V's dims are
+// split in two halves (each workgroup reads all of K, half of V, and computes
+// all the group's scores and half of their output), then the group's query
+// heads. A query's arithmetic is the same whichever workgroup computes it and
+// whatever other queries share its wavefront, so the plan never changes a
+// result. Measured per layer at ctx 512, Hq 32, Hkv 8 (32-layer graph, MI355X,
+// us, heads split in 2^q, V split in 2^v, as (q, v)): B=16 (1, 0) 9.12,
+// (0, 1) 8.72, (1, 1) 13.0 (512 workgroups); B=8 (2, 0) 7.91, (0, 1) 7.26,
+// (1, 1) 6.99; B=4 (2, 0) 7.13, (1, 1) 6.17, (2, 1) 6.07.
+// The context split is chosen for plan_B streams (it orders the fp32 sums, so
+// a decoder keeps it fixed across steps), the sharing for the B launched.
+Plan plan_for(int B, int plan_B, int Hkv, int G, int max_ctx) {
+  const int64_t pairs = (int64_t)plan_B * Hkv;
   const int min_split = pairs >= 128 ? 1024 : pairs >= 32 ? 512 : 128;
   int64_t nsplit = (kTargetWorkgroups + pairs - 1) / pairs;
   nsplit = std::min<int64_t>(nsplit, (max_ctx + min_split - 1) / min_split);
   nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, kMaxSplits));
   const int split_tokens = (int)round_up((max_ctx + nsplit - 1) / nsplit, kSpan);
   const int ns = (max_ctx + split_tokens - 1) / split_tokens;
+  const int64_t units = (int64_t)B * Hkv * ns;
+  const int vs = units * 2 <= kTargetWorkgroups ? 1 : 0;
   int qs = 0;
-  while ((2 << qs) <= G && pairs * ns * (2 << qs) <= kTargetWorkgroups) ++qs;
-  return {ns, split_tokens, qs};
+  while ((2 << qs) <= G && (units << (vs + qs + 1)) <= kTargetWorkgroups) ++qs;
+  return {ns, split_tokens, qs, vs};
 }
 
 size_t ws_bytes(int B, int Hq, int nsplit) {
@@ -844,7 +874,7 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   PDK_REQUIRE(scale > 0.f && scale < INFINITY, "scale must be positive and finite (got %g)",
               (double)scale);
   PDK_REQUIRE(plan_B >= B && plan_B <= 65535, "plan_batch=%d must be in [B=%d, 65535]", plan_B, B);
-  const Plan p = plan_for(plan_B, n_kv_heads, G, max_ctx);
+  const Plan p = plan_for(B, plan_B, n_kv_heads, G, max_ctx);
   AttnArgs a{};
   a.q = q;
   a.ck = cache_k;
@@ -873,16 +903,19 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   const size_t lds = (size_t)min(G, kMergeRows) * kORow * sizeof(float);
   const int64_t units = (int64_t)p.nsplit * n_kv_heads * B;
   PDK_REQUIRE(units < (1 << 24), "B * n_kv_heads * splits = %lld is too large", (long long)units);
-  const int64_t n_wg = units << p.qsplit;
+  const int64_t n_wg = units << (p.qsplit + p.vsplit);
   const uint32_t hgw = (uint32_t)n_kv_heads | ((uint32_t)G << 16) | ((uint32_t)p.qsplit << 24);
   const uint32_t mb_b = (uint32_t)max_blocks | ((uint32_t)B << 16);
   const uint32_t st_ns = (uint32_t)p.split_tokens | ((uint32_t)p.nsplit << 16);
   const dim3 grid((uint32_t)n_wg), block(64 * kMaxWaves);
   const void* src = rope.part ? static_cast<const void*>(rope.part) : static_cast<const void*>(a.q);
 #define PDK_ATTN_LAUNCH(R)                                                                      \
-  hipLaunchKernelGGL(decode_attn_kernel<R>, grid, block, lds, st, src, a.ck, a.cv, a.tables,   \
-                     a.ctx, hgw, mb_b, a.num_blocks, st_ns, a.scale_log2, a.out, a.ws_ml,     \
-                     a.ws_o, rope.inv_freq, rope.ck_w, rope.cv_w, rope.ssq, rope.n_ssq, rope.eps)
+  do {                                                                                         \
+    const auto kern = p.vsplit ? decode_attn_kernel<R, 4> : decode_attn_kernel<R, 8>;          \
+    hipLaunchKernelGGL(kern, grid, block, lds, st, src, a.ck, a.cv, a.tables, a.ctx, hgw, mb_b, \
+                       a.num_blocks, st_ns, a.scale_log2, a.out, a.ws_ml, a.ws_o,              \
+                       rope.inv_freq, rope.ck_w, rope.cv_w, rope.ssq, rope.n_ssq, rope.eps);   \
+  } while (0)
   switch (rope.probe ? -1 : rope.part ? rope.splits : 0) {
     case -1: PDK_ATTN_LAUNCH(-1); break;
     case 0: PDK_ATTN_LAUNCH(0); break;
@@ -928,7 +961,7 @@ extern "C" int pdk_decode_attn_noalloc(const uint16_t* q, const uint16_t* cache_
               max_ctx, head_dim);
   PDK_REQUIRE(n_q_heads % n_kv_heads == 0, "n_q_heads=%d must be a multiple of n_kv_heads=%d",
               n_q_heads, n_kv_heads);
-  const Plan p = plan_for(B, n_kv_heads, n_q_heads / n_kv_heads, max_ctx);
+  const Plan p = plan_for(B, B, n_kv_heads, n_q_heads / n_kv_heads, max_ctx);
   const size_t need = ws_bytes(B, n_q_heads, p.nsplit);
   if (need > PDK_NOALLOC_SCRATCH_BYTES) {
     pdk::set_error("this launch needs %zu bytes of split partials; the no-allocation entry "

@@ -187,6 +187,27 @@ def test_decode_attention_vs_fp32(cuda, B, Hq, H, ctx):
     np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
 
 
+def test_decode_attention_sharing_never_changes_a_result(cuda):
+    """At ctx 512 with Hq 32, Hkv 8, batches of 16, 8 and 4 all run one context
+    split, but share each (stream, KV head) unit differently: V's dims in two
+    halves alone, or also the query heads in 2 or in 4 parts (so 4, 2 or 1
+    query heads per wavefront). Streams 0-3 come out bit for bit the same."""
+    from rngd_pd_amd.kernels import decode_attention
+    rng = np.random.default_rng(31)
+    q, ck, cv, tables, ctx_a = _attn_case(rng, 16, 32, 8, [512, 300, 17, 511] * 4)
+    dq, dk, dv = to_dev(q), to_dev(ck), to_dev(cv)
+    dt, dc = torch.from_numpy(tables).to(cuda), torch.from_numpy(ctx_a).to(cuda)
+    outs = []
+    for B in (16, 8, 4):
+        print(f"sharing: B={B}", flush=True)
+        outs.append(decode_attention(dq[:B], dk, dv, dt[:B], dc[:B], 512, scale=0.125))
+    torch.cuda.synchronize()
+    want = orc.decode_attn(q[:4], ck, cv, tables[:4], ctx_a[:4], 0.125)
+    np.testing.assert_allclose(outs[2].float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+    for o in outs[:2]:
+        assert torch.equal(o[:4].view(torch.int16), outs[2].view(torch.int16))
+
+
 def test_decode_attention_max_ctx_bound_above_actual(cuda):
     """A launch sized for a larger max_ctx gives the same result (empty splits)."""
     from rngd_pd_amd.kernels import decode_attention
