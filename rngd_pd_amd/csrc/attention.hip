@@ -97,11 +97,13 @@ __device__ __forceinline__ bool valid_block(int blk, int num_blocks) {
 
 // Issue every load of the 32-token span starting at `span`, whose tokens lie
 // in the blocks blk_lo (tokens span..span+15) and blk_hi (span+16..span+31).
+// kVStream: V with non-temporal loads (each V byte has one reader; K has one
+// per workgroup sharing the unit).
 // Loads are unconditional from in-bounds addresses (an invalid block id reads
 // block 0) so they are all in flight together; V of tokens >= lim and of
 // invalid blocks is zeroed before use, K of tokens >= lim needs nothing (their
 // scores become -inf).
-template <int kNV>
+template <int kNV, bool kVStream>
 __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, int g, int j,
                                           int blk_lo, int blk_hi, Span& r) {
   // QK tile 0 row j is token span + 8(j/4) + j%4 and tile 1 row j that token
@@ -122,7 +124,7 @@ __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, in
     r.kb[s] = pdk::ld16(pk + ((4 + s) * 4 * 8) * 8);
   }
 #pragma unroll
-  for (int n = 0; n < kNV; ++n) r.vf[n] = pdk::ld16(pv + 16 * 16 * n);
+  for (int n = 0; n < kNV; ++n) r.vf[n] = pdk::ld16_as<kVStream>(pv + 16 * 16 * n);
 }
 
 // Reductions over the four lanes of one query column {i, i^16, i^32, i^48}
@@ -387,6 +389,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int nsplit = a.nsplit;
   constexpr int kVS = kNV == 8 ? 0 : 1;         // log2 of the parts V's dims are split in
   constexpr int kDV = 16 * kNV;                  // dims of O this workgroup computes
+  // Non-temporal V loads: measured per layer at ctx 512 (32-layer graph) on the
+  // plain path B=16 8.71 -> 8.37 us, B=8 6.98 -> 6.75, B=4 6.06 -> 5.88; on
+  // the fused RoPE path no faster, and 0.15-0.3 us slower between streaming
+  // kernels, so it keeps ordinary loads.
+  constexpr bool kVStream = kRope <= 0;
   const int qsplit = hgw >> 24;
   const int gs = qsplit + kVS;                   // log2 of the workgroups sharing a unit
   const int units = nsplit * a.Hkv * (int)(mb_b >> 16);
@@ -511,11 +518,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // the loads stay under the branch (measured 0.5 us per layer faster).
   Span ra0, rb0;
   if constexpr (kRope > 0) {
-    load_span<kNV>(a, h, sa0, g, j, active ? id0[0] : 0, active ? id0[1] : 0, ra0);
-    load_span<kNV>(a, h, sb0, g, j, has_b0 ? id0[2] : 0, has_b0 ? id0[3] : 0, rb0);
+    load_span<kNV, kVStream>(a, h, sa0, g, j, active ? id0[0] : 0, active ? id0[1] : 0, ra0);
+    load_span<kNV, kVStream>(a, h, sb0, g, j, has_b0 ? id0[2] : 0, has_b0 ? id0[3] : 0, rb0);
   } else if (active) {
-    load_span<kNV>(a, h, sa0, g, j, id0[0], id0[1], ra0);
-    if (has_b0) load_span<kNV>(a, h, sb0, g, j, id0[2], id0[3], rb0);
+    load_span<kNV, kVStream>(a, h, sa0, g, j, id0[0], id0[1], ra0);
+    if (has_b0) load_span<kNV, kVStream>(a, h, sb0, g, j, id0[2], id0[3], rb0);
   }
   if constexpr (kRope > 0) {
     // Second phase, while the first pair's K/V loads are in flight: add the
@@ -594,12 +601,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (sc < s_end) ids(sc, nxt);
     if constexpr (kRope < 0) fold_span<kNV>(ra, o);
     else attend_span<(kRope > 0), kNV>(a, ra, qv, sa, cur[0], cur[1], s_end, g, j, kFirst, m, lsum, o, nt);
-    if (sc < s_end) load_span<kNV>(a, h, sc, g, j, nxt[0], nxt[1], ra);
+    if (sc < s_end) load_span<kNV, kVStream>(a, h, sc, g, j, nxt[0], nxt[1], ra);
     if (sb < s_end) {
       if constexpr (kRope < 0) fold_span<kNV>(rb, o);
       else attend_span<(kRope > 0), kNV>(a, rb, qv, sb, cur[2], cur[3], s_end, g, j, false, m, lsum, o, nt);
     }
-    if (sd < s_end) load_span<kNV>(a, h, sd, g, j, nxt[2], nxt[3], rb);
+    if (sd < s_end) load_span<kNV, kVStream>(a, h, sd, g, j, nxt[2], nxt[3], rb);
     return sc;
   };
   if (active) {
