@@ -17,7 +17,8 @@ decode_batch tokens/s alongside.
             staging with DMA-engine copies, one 512-token request, KONI token
             blocks and the host-link rates.
   decode    GQA decode attention, 32 layers x B streams at context 512, per-layer
-            launches, eager and replayed from a HIP graph.
+            launches, eager and replayed from a HIP graph; B=16 at context 2048
+            (context split in two + merge) from a graph.
   step      the full Llama-3.1-8B decode step (random-init weights) at B=4 and
             B=16, context 512, eager and from a HIP graph, beside the
             reference's published 21.54 / 35.54 ms per step.
@@ -509,6 +510,62 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
     out["kernels"] = dict(out.get("kernels", {}), decode_attn_B16=res[f"B{batches[-1]}"]["roofline"])
 
 
+def bench_decode_long(args, torch, K, dev, out, B=16, ctx=2048):
+    """Decode attention at a longer context, B=16 x 2048 tokens (134 MB of K+V
+    per layer, 4.3 GB for 32 layers): the launch splits the context in two
+    and a merge launch combines the halves. 32 layers replayed from a HIP
+    graph, timed with events around the replays."""
+    nb_per = ctx // BS
+    nb = B * nb_per
+    gen = torch.Generator(device=dev).manual_seed(17)
+    cache_k = torch.randn((L, nb, H, BS, D), generator=gen, device=dev).to(torch.bfloat16)
+    cache_v = torch.randn((L, nb, H, D, BS), generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn((L, B, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
+    tables = torch.from_numpy(np.random.default_rng(17).permutation(nb).astype(np.int32)
+                              .reshape(B, nb_per)).to(dev)
+    ctx_lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    outp = torch.empty_like(q)
+    ws = torch.zeros(max(1, K.workspace_bytes(B, HQ, ctx, D) // 4), dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def step():
+        for l in range(L):
+            K.decode_attention(q[l], cache_k[l], cache_v[l], tables, ctx_lens, ctx, scale=scale,
+                               out=outp[l], workspace=ws)
+    step()
+    torch.cuda.synchronize()
+    eager_out = outp.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.synchronize()
+    for _ in range(max(1, args.warmup)):
+        g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(outp.view(torch.int16), eager_out.view(torch.int16)):
+        raise RuntimeError("graph replay differs from eager attention (ctx 2048)")
+    ta, tb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(5, args.steps)
+    ta.record()
+    for _ in range(reps):
+        g.replay()
+    tb.record()
+    torch.cuda.synchronize()
+    us = ta.elapsed_time(tb) * 1e3 / reps / L
+    kv_bytes = B * ctx * H * D * 2 * 2 + 2 * B * HQ * D * 2
+    out["extra"]["decode_batch_ctx2048"] = {
+        f"B{B}": {"layer_us_graph": round(us, 2),
+                  "tokens_per_s_graph": round(B / (us * L) * 1e6, 1),
+                  "roofline": roofline(kv_bytes, us * 1e-6)}}
+    log(f"decode B={B} ctx={ctx}: {us:.2f} us per layer (graph, attention + merge), "
+        f"{kv_bytes / us / 1e3:.0f} GB/s")
+    del g, cache_k, cache_v
+    torch.cuda.empty_cache()
+
+
 def bench_attn_floor(args, torch, K, dev, out, batches=(4, 8, 16), ctx=512):
     """What one launch per layer can reach at decode attention's sizes: 32
     launches of the one-shot read probe (one 16-byte vector per lane, a
@@ -918,6 +975,7 @@ def main():
         bench_handoff(args, torch, K, lib, dev, out)
     if args.legs & {"all", "decode"}:
         bench_decode(args, torch, K, lib, dev, out)
+        bench_decode_long(args, torch, K, dev, out)
         bench_attn_floor(args, torch, K, dev, out)
     if args.legs & {"all", "step"}:
         bench_step(args, torch, dev, out)
