@@ -562,8 +562,14 @@ int linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int 
   PDK_REQUIRE(splits >= 1 && splits <= 16 && splits <= K / kStepK,
               "splits must be in [1, min(16, K/%d)] (got %d)", kStepK, splits);
   hipStream_t st = pdk::as_stream(stream);
+  // Two column tiles (with the caller's two K splits at the Llama-8B down
+  // projection: 128 x 2 workgroups, 7 steps per wave) rather than four with
+  // four splits (28 steps per workgroup: waves 0-3 take 4 and waves 4-7 take 3):
+  // the decode step B=4 2.890 -> 2.848 ms, B=16 3.100 -> 3.097 in one process.
+  // One tile without a split was faster still at B=4 (2.819) but 0.08 ms
+  // slower at B=16, where x's loads are as many bytes as the weights.
   if (N >= 1024)
-    return launch_cols<4, kPartialFinal, kTiled>(x, w, B, K, N, residual, residual, nullptr, st,
+    return launch_cols<2, kPartialFinal, kTiled>(x, w, B, K, N, residual, residual, nullptr, st,
                                                  partials, splits, ssq, 0, 0.f, counters);
   return launch_cols<1, kPartialFinal, kTiled>(x, w, B, K, N, residual, residual, nullptr, st,
                                                partials, splits, ssq, 0, 0.f, counters);

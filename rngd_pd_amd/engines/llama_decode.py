@@ -152,8 +152,11 @@ class LlamaDecoder:
         self.tokens = torch.empty(B, dtype=torch.int32, device=dev)
         self.keys = torch.zeros(B, dtype=torch.int64, device=dev)    # argmax scratch, kept zero
         # The down projection runs split over K (its 14336-long rows) into fp32
-        # partial sums, which the next norm adds to the residual.
-        groups = (H + 63) // 64 if H >= 1024 else (H + 15) // 16
+        # partial sums, which its last-arriving split adds to the residual:
+        # enough splits for about 256 workgroups of 32 columns (16 below
+        # hidden 1024). The count follows the model's shape alone, never B,
+        # so a row's sums do not depend on the batch.
+        groups = (H + 31) // 32 if H >= 1024 else (H + 15) // 16
         self.down_splits = max(1, min(8, cfg.inter // 128, -(-256 // groups)))
         self.part = torch.empty((self.down_splits, B, H), dtype=torch.float32, device=dev)
         # The q|k|v projection (N = 6144 at 8B) splits K in two when every wave
