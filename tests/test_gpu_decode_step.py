@@ -189,6 +189,43 @@ def test_fused_rope_attention_equals_two_calls(cuda, B, splits, NH, NKV):
     np.testing.assert_array_equal(to_host(cv_b), to_host(cv_a))
 
 
+def test_fused_rope_attention_batch_invariant(cuda):
+    """With plan_batch 16, the fused path at B=16 and at B=4 (the first four
+    streams) runs the same context split but shares each unit differently (V
+    halves only, or also 1 query head per workgroup): the four streams' outputs
+    and cache contents are bit for bit the same, at contexts of one and of two
+    context splits."""
+    from rngd_pd_amd import kernels as K
+    D, NH, NKV, splits = 128, 32, 8, 2
+    for ctx in ([512, 300, 17, 511] * 4, [2048, 1500, 700, 1] * 4):
+        rng = np.random.default_rng(77 + len(ctx) + ctx[0])
+        max_blocks = (max(ctx) + 15) // 16
+        nb = 16 * max_blocks + 3
+        tables = rng.permutation(nb)[:16 * max_blocks].astype(np.int32).reshape(16, max_blocks)
+        N = (NH + 2 * NKV) * D
+        part = (rng.standard_normal((splits, 16, N)) * 2).astype(np.float32)
+        ck0, cv0 = rand_bf16(rng, (nb, NKV, 16, D)), rand_bf16(rng, (nb, NKV, D, 16))
+        inv = torch.from_numpy(od.inv_freq(D, 500000.0, LLAMA3)).to(cuda)
+        outs, caches = [], []
+        for B in (16, 4):
+            print(f"fused rope batch invariance: B={B} max ctx {max(ctx)}", flush=True)
+            ck, cv = to_dev(ck0), to_dev(cv0)
+            out = K.decode_attention_rope(
+                torch.from_numpy(np.ascontiguousarray(part[:, :B])).to(cuda), inv, ck, cv,
+                torch.from_numpy(np.ascontiguousarray(tables[:B])).to(cuda),
+                torch.tensor(ctx[:B], dtype=torch.int32, device=cuda), max(ctx), NH,
+                scale=1.0 / math.sqrt(D), plan_batch=16)
+            torch.cuda.synchronize()
+            outs.append(to_host(out))
+            caches.append((to_host(ck), to_host(cv)))
+        np.testing.assert_array_equal(outs[1], outs[0][:4])
+        # the cache blocks of streams 0-3 hold the same new tokens
+        own = tables[:4].ravel()
+        own = own[own >= 0]
+        np.testing.assert_array_equal(caches[1][0][own], caches[0][0][own])
+        np.testing.assert_array_equal(caches[1][1][own], caches[0][1][own])
+
+
 def _rand_ssq(rng, n_tiles, B):
     """[B, n_tiles] per-tile sums of squares of plausible residual rows."""
     return (rng.chisquare(16, (B, n_tiles)) * rng.uniform(0.1, 3.0, (B, 1))).astype(np.float32)
