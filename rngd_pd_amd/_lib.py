@@ -117,6 +117,14 @@ SIGNATURES = {
     "pdk_linear_splitk_final_tiled": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _U]),
     "pdk_linear_argmax_rms": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _P, _P, _U]),
     "pdk_linear_argmax_rms_tiled": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _P, _P, _U]),
+    "pdk_linear_ssq_xt": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _U]),
+    "pdk_linear_swiglu_rms_xt": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _U]),
+    "pdk_linear_splitk_rms_xt": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _F, _P, _U]),
+    "pdk_linear_splitk_final_xt": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _U]),
+    "pdk_linear_argmax_rms_xt": (_I, [_P, _P, _I, _I, _I, _P, _I, _F, _P, _P, _P, _U]),
+    "pdk_embed_ssq_xt": (_I, [_P, _I64, _P, _I, _I, _I, _P, _P, _U]),
+    "pdk_decode_attn_rope_xt": (_I, [_P, _I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I,
+                                     ctypes.c_float, _P, _SZ, _P, _I, _U]),
     "pdk_row_ssq": (_I, [_P, _I, _I, _P, _U]),
     "pdk_embed_ssq": (_I, [_P, _I64, _P, _I, _I, _I, _P, _P, _U]),
     "pdk_scatter_koni": (_I, [_P, _I64, _P, _I, _I, _P, _I, _P, _P, _I64, _I, _I, _I, _U]),

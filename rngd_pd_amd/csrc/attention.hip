@@ -373,7 +373,9 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
 // to that kernel followed by the kRope = 0 path.
 // kRope = -1 is the read probe (pdk_attn_read_probe): the same launch, block
 // ids and K/V loads, none of the arithmetic, one store per thread.
-template <int kRope, int kNV>
+// kAct: out in the decode step's tiled activation layout (pdk::act_at, row b,
+// column qh * D + d of Hq * D) instead of row-major [B][Hq][D].
+template <int kRope, int kNV, bool kAct = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_attn_kernel(
     const void* src, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
     const int32_t* ctx_lens, uint32_t hgw, uint32_t mb_b, int num_blocks, uint32_t st_ns,
@@ -686,7 +688,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int64_t bq = bq0 + r0 + row;
       if (a.nsplit == 1) {
         const float inv = L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
-        a.out[bq * kD + vd0 + d] = (uint16_t)pdk::f32_to_bf16_rne(O * inv);
+        const int64_t at = kAct ? pdk::act_at(b, (qh0 + r0 + row) * kD + vd0 + d, a.Hq * kD)
+                                : bq * kD + vd0 + d;
+        a.out[at] = (uint16_t)pdk::f32_to_bf16_rne(O * inv);
       } else {
         a.ws_o[(bq * a.nsplit + split) * kD + vd0 + d] = O;
         if (vd0 + d == 0) {
@@ -699,8 +703,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // out = sum_s 2^(m_s-M) O_s / sum_s 2^(m_s-M) l_s, all partial loads independent.
+// kAct: out in the tiled activation layout (row bq / Hq, column (bq % Hq) * D + d).
+template <bool kAct>
 __global__ __launch_bounds__(128) void merge_kernel(const float* ws_ml, const float* ws_o,
-                                                    int nsplit, uint16_t* out) {
+                                                    int nsplit, uint16_t* out, int Hq) {
   const int64_t bq = blockIdx.x;
   const int d = threadIdx.x;
   const float* ml = ws_ml + bq * nsplit * 2;
@@ -727,7 +733,9 @@ __global__ __launch_bounds__(128) void merge_kernel(const float* ws_ml, const fl
       }
     }
   }
-  out[bq * kD + d] = (uint16_t)pdk::f32_to_bf16_rne(L > 0.f ? O * __builtin_amdgcn_rcpf(L) : 0.f);
+  const int64_t at = kAct ? pdk::act_at((int)(bq / Hq), (int)(bq % Hq) * kD + d, Hq * kD)
+                          : bq * kD + d;
+  out[at] = (uint16_t)pdk::f32_to_bf16_rne(L > 0.f ? O * __builtin_amdgcn_rcpf(L) : 0.f);
 }
 
 // New token's k/v into slot ctx[b]-1 (kernels/decode_batch.py:81-82 as a store).
@@ -857,6 +865,7 @@ struct RopeIn {
   int n_ssq = 0;
   float eps = 0.f;
   bool probe = false;            // pdk_attn_read_probe: loads only
+  bool act = false;              // out in the tiled activation layout (pdk::act_at)
 };
 
 int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
@@ -928,28 +937,44 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   const uint32_t st_ns = (uint32_t)p.split_tokens | ((uint32_t)p.nsplit << 16);
   const dim3 grid((uint32_t)n_wg), block(64 * kMaxWaves);
   const void* src = rope.part ? static_cast<const void*>(rope.part) : static_cast<const void*>(a.q);
-#define PDK_ATTN_LAUNCH(R)                                                                      \
+#define PDK_ATTN_LAUNCH(R, A)                                                                   \
   do {                                                                                         \
-    const auto kern = p.vsplit ? decode_attn_kernel<R, 4> : decode_attn_kernel<R, 8>;          \
+    const auto kern = p.vsplit ? decode_attn_kernel<R, 4, A> : decode_attn_kernel<R, 8, A>;    \
     hipLaunchKernelGGL(kern, grid, block, lds, st, src, a.ck, a.cv, a.tables, a.ctx, hgw, mb_b, \
                        a.num_blocks, st_ns, a.scale_log2, a.out, a.ws_ml, a.ws_o,              \
                        rope.inv_freq, rope.ck_w, rope.cv_w, rope.ssq, rope.n_ssq, rope.eps);   \
   } while (0)
-  switch (rope.probe ? -1 : rope.part ? rope.splits : 0) {
-    case -1: PDK_ATTN_LAUNCH(-1); break;
-    case 0: PDK_ATTN_LAUNCH(0); break;
-    case 1: PDK_ATTN_LAUNCH(1); break;
-    case 2: PDK_ATTN_LAUNCH(2); break;
-    case 4: PDK_ATTN_LAUNCH(4); break;
-    default:
-      pdk::set_error("splits must be 1, 2 or 4 (got %d)", rope.splits);
-      return PDK_EINVAL;
+  const int mode = rope.probe ? -1 : rope.part ? rope.splits : 0;
+  if (rope.act) {
+    switch (mode) {
+      case 1: PDK_ATTN_LAUNCH(1, true); break;
+      case 2: PDK_ATTN_LAUNCH(2, true); break;
+      case 4: PDK_ATTN_LAUNCH(4, true); break;
+      default:
+        pdk::set_error("splits must be 1, 2 or 4 (got %d)", rope.splits);
+        return PDK_EINVAL;
+    }
+  } else {
+    switch (mode) {
+      case -1: PDK_ATTN_LAUNCH(-1, false); break;
+      case 0: PDK_ATTN_LAUNCH(0, false); break;
+      case 1: PDK_ATTN_LAUNCH(1, false); break;
+      case 2: PDK_ATTN_LAUNCH(2, false); break;
+      case 4: PDK_ATTN_LAUNCH(4, false); break;
+      default:
+        pdk::set_error("splits must be 1, 2 or 4 (got %d)", rope.splits);
+        return PDK_EINVAL;
+    }
   }
 #undef PDK_ATTN_LAUNCH
   int rc = pdk::check_launch("decode_attn_kernel");
   if (rc || p.nsplit == 1 || rope.probe) return rc;
-  hipLaunchKernelGGL(merge_kernel, dim3(B * n_q_heads), dim3(kD), 0, st, a.ws_ml, a.ws_o,
-                     p.nsplit, out);
+  if (rope.act)
+    hipLaunchKernelGGL(merge_kernel<true>, dim3(B * n_q_heads), dim3(kD), 0, st, a.ws_ml, a.ws_o,
+                       p.nsplit, out, n_q_heads);
+  else
+    hipLaunchKernelGGL(merge_kernel<false>, dim3(B * n_q_heads), dim3(kD), 0, st, a.ws_ml,
+                       a.ws_o, p.nsplit, out, n_q_heads);
   return pdk::check_launch("merge_kernel");
 }
 
@@ -1014,6 +1039,27 @@ extern "C" int pdk_decode_attn_rope(const float* qkv_partials, int splits, const
                      workspace_bytes, out, stream,
                      RopeIn{qkv_partials, splits, inv_freq, cache_k, cache_v},
                      plan_batch > 0 ? plan_batch : B);
+}
+
+extern "C" int pdk_decode_attn_rope_xt(const float* qkv_partials, int splits,
+                                       const float* inv_freq, uint16_t* cache_k,
+                                       uint16_t* cache_v, int num_blocks,
+                                       const int32_t* block_tables, int max_blocks,
+                                       const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads,
+                                       int n_kv_heads, int head_dim, float scale, void* workspace,
+                                       size_t workspace_bytes, uint16_t* out, int plan_batch,
+                                       uintptr_t stream) {
+  pdk::clear_error();
+  PDK_REQUIRE(qkv_partials && inv_freq, "null pointer argument");
+  PDK_REQUIRE(splits == 1 || splits == 2 || splits == 4, "splits must be 1, 2 or 4 (got %d)",
+              splits);
+  PDK_REQUIRE((int64_t)n_q_heads * head_dim % 128 == 0,
+              "tiled activations need n_q_heads * head_dim %% 128 == 0");
+  RopeIn rope{qkv_partials, splits, inv_freq, cache_k, cache_v};
+  rope.act = true;
+  return launch_attn(nullptr, cache_k, cache_v, num_blocks, block_tables, max_blocks, ctx_lens,
+                     max_ctx, B, n_q_heads, n_kv_heads, head_dim, scale, workspace,
+                     workspace_bytes, out, stream, rope, plan_batch > 0 ? plan_batch : B);
 }
 
 extern "C" int pdk_decode_attn_rope_rms(const float* qkv_partials, int splits,

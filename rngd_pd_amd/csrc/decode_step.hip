@@ -237,7 +237,8 @@ __global__ __launch_bounds__(256) void row_ssq_kernel(const uint16_t* x, int B, 
 // x[b] = table[tokens[b]] and its per-tile sums of squares (row_ssq_kernel's
 // values, bit for bit): the step's embedding lookup and the first layer's
 // folded-norm input in one launch. A token outside [0, vocab) gives a zero row.
-template <typename Tok>
+// kAct: x in the tiled activation layout (pdk::act_at; H % 128 == 0).
+template <typename Tok, bool kAct = false>
 __global__ __launch_bounds__(256) void embed_ssq_kernel(const uint16_t* table, int64_t vocab,
                                                         const Tok* tokens, int H, uint16_t* x,
                                                         float* ssq) {
@@ -248,9 +249,8 @@ __global__ __launch_bounds__(256) void embed_ssq_kernel(const uint16_t* table, i
   for (int t = threadIdx.x; t < H / 16; t += 256) {
     v8 lo = pdk::ld16(row + 16 * t), hi = pdk::ld16(row + 16 * t + 8);
     if (!ok) lo = hi = pdk::zero8();
-    uint16_t* o = x + (int64_t)b * H + 16 * t;
-    pdk::st16(o, lo);
-    pdk::st16(o + 8, hi);
+    pdk::st16(x + (kAct ? pdk::act_at(b, 16 * t, H) : (int64_t)b * H + 16 * t), lo);
+    pdk::st16(x + (kAct ? pdk::act_at(b, 16 * t + 8, H) : (int64_t)b * H + 16 * t + 8), hi);
     ssq[(int64_t)b * (H / 16) + t] = tile_ssq(lo, hi);
   }
 }
@@ -267,10 +267,12 @@ extern "C" int pdk_row_ssq(const uint16_t* x, int B, int H, float* ssq, uintptr_
   return pdk::check_launch("row_ssq_kernel");
 }
 
-extern "C" int pdk_embed_ssq(const uint16_t* table, int64_t vocab, const void* tokens,
-                             int tok_bytes, int B, int H, uint16_t* x, float* ssq,
-                             uintptr_t stream) {
+namespace {
+template <bool kAct>
+int embed_ssq(const uint16_t* table, int64_t vocab, const void* tokens, int tok_bytes, int B,
+              int H, uint16_t* x, float* ssq, uintptr_t stream) {
   pdk::clear_error();
+  PDK_REQUIRE(!kAct || H % 128 == 0, "tiled activations need H %% 128 == 0 (got %d)", H);
   PDK_REQUIRE(table && tokens && x && ssq, "null pointer argument");
   PDK_REQUIRE(vocab >= 1, "vocab must be >= 1");
   PDK_REQUIRE(tok_bytes == 4 || tok_bytes == 8, "tok_bytes must be 4 (int32) or 8 (int64)");
@@ -281,12 +283,25 @@ extern "C" int pdk_embed_ssq(const uint16_t* table, int64_t vocab, const void* t
               "tokens must be aligned to their %d-byte size", tok_bytes);
   hipStream_t st = pdk::as_stream(stream);
   if (tok_bytes == 4)
-    hipLaunchKernelGGL(embed_ssq_kernel<int32_t>, dim3(B), dim3(256), 0, st, table, vocab,
+    hipLaunchKernelGGL((embed_ssq_kernel<int32_t, kAct>), dim3(B), dim3(256), 0, st, table, vocab,
                        static_cast<const int32_t*>(tokens), H, x, ssq);
   else
-    hipLaunchKernelGGL(embed_ssq_kernel<int64_t>, dim3(B), dim3(256), 0, st, table, vocab,
+    hipLaunchKernelGGL((embed_ssq_kernel<int64_t, kAct>), dim3(B), dim3(256), 0, st, table, vocab,
                        static_cast<const int64_t*>(tokens), H, x, ssq);
   return pdk::check_launch("embed_ssq_kernel");
+}
+}  // namespace
+
+extern "C" int pdk_embed_ssq(const uint16_t* table, int64_t vocab, const void* tokens,
+                             int tok_bytes, int B, int H, uint16_t* x, float* ssq,
+                             uintptr_t stream) {
+  return embed_ssq<false>(table, vocab, tokens, tok_bytes, B, H, x, ssq, stream);
+}
+
+extern "C" int pdk_embed_ssq_xt(const uint16_t* table, int64_t vocab, const void* tokens,
+                                int tok_bytes, int B, int H, uint16_t* x, float* ssq,
+                                uintptr_t stream) {
+  return embed_ssq<true>(table, vocab, tokens, tok_bytes, B, H, x, ssq, stream);
 }
 
 static int check_norm(const void* x, const void* weight, const void* out, int B, int H) {

@@ -81,6 +81,20 @@ __host__ __device__ __forceinline__ int k_unit(int slot, int d0, int D) {
   return ((t * (D >> 5) + (d0 >> 5)) * 4 + ((d0 >> 3) & 3)) * 8 + j8;
 }
 
+// Tiled activation layout of the decode step's bf16 [rows][K] operands (K %
+// 128 == 0; rows padded to a multiple of 16): the 16 x 128 block of rows
+// 16t..16t+15 and columns 128s..128s+127 is 2048 contiguous elements, in the
+// order the GEMM lanes read their MFMA operand (lane l = 16 kg + r, r the row
+// in the tile, reads 8 columns 32c + 8kg .. + 7 at element (c * 64 + l) * 8),
+// so each load instruction of a GEMM reads 1 KiB of consecutive bytes instead
+// of 64-byte pieces of 16 rows. Element (m, n) of such an operand is at
+//   ((m / 16) * (K / 128) + n / 128) * 2048 + (((n % 128) / 8) * 16 + m % 16) * 8 + n % 8
+// (columns 32c + 8kg .. + 7 of a block are its 16-byte group 4c + kg).
+__host__ __device__ __forceinline__ int64_t act_at(int m, int n, int K) {
+  return ((int64_t)(m >> 4) * (K >> 7) + (n >> 7)) * 2048 +
+         ((((n & 127) >> 3) << 4) + (m & 15)) * 8 + (n & 7);
+}
+
 // Zero the elements e with first + e >= limit (first..first+7 are the token
 // indices of the 8 elements).
 __device__ __forceinline__ void mask_tail(v8& v, int first, int limit) {

@@ -31,6 +31,18 @@
 //   tile t = rows 16t .. 16t+15 (rows >= N zero), K/128 step blocks of 2048
 //   elements each; element ((c * 4 + kg) * 16 + col) * 8 + e of step block s
 //   is W[16t + col][128 s + 32 c + 8 kg + e].
+//
+// Tiled activations. The _xt entry points take the decode step's bf16
+// activations (x, the residual and the output y) in the tiled layout of
+// pdk::act_at, the same order for rows that the tiled weights use for
+// columns: an X load instruction then reads 1 KiB of consecutive bytes
+// instead of a 64-byte piece of each of 16 rows. At Llama-3.1-8B shapes and
+// B = 16 (32 launches of each in a HIP graph, tiled weights) that took the
+// five GEMMs of a layer from 82.1 to 78.5 us: O 9.55 -> 8.28, q|k|v 11.84 ->
+// 11.02, gate|up 38.04 -> 37.30, down 22.68 -> 21.89. Rows past B are never
+// read (lanes of rows >= B read row B - 1, as in the row-major layout), so
+// the padding rows of a tile may hold anything. fp32 partials, logits and
+// the sums of squares keep their row-major layouts.
 
 #include <math.h>
 
@@ -97,7 +109,7 @@ constexpr int depth_for(int tiles) {
 // its waves share them and split K); kEpi selects the epilogue. For kSwiGLU the
 // workgroup also computes the matching up columns (rows n and M + n of W) and
 // writes silu(g) * u.
-template <int kTiles, int kCols, int kEpi, bool kTiled>
+template <int kTiles, int kCols, int kEpi, bool kTiled, bool kAct>
 __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w, int B,
                                                             int K, int N, int splits, float* ssq,
@@ -133,9 +145,16 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
       else
         wp[p * kCols + c] = w + ((int64_t)p * N + min(n0 + 16 * c + col, N - 1)) * K + kg * 8;
     }
+  // X operand of row tile t: row min(16t + col, B - 1), k offsets 32c + 8kg.
+  // Tiled activations (kAct): that row's 16-byte group 4c + kg of each
+  // 2048-element block, pdk::act_at.
   const uint16_t* xp[kTiles];
 #pragma unroll
-  for (int t = 0; t < kTiles; ++t) xp[t] = x + (int64_t)min(t * 16 + col, B - 1) * K + kg * 8;
+  for (int t = 0; t < kTiles; ++t) {
+    const int row = min(t * 16 + col, B - 1);
+    xp[t] = kAct ? x + (int64_t)(row >> 4) * 16 * K + (kg * 16 + (row & 15)) * 8
+                 : x + (int64_t)row * K + kg * 8;
+  }
 
   f32x4 acc[kW][kTiles];
 #pragma unroll
@@ -172,7 +191,9 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
 #pragma unroll
     for (int t = 0; t < kTiles; ++t)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) xv[slot][t][c] = pdk::ld16(xp[t] + k + 32 * c);
+      for (int c = 0; c < 4; ++c)
+        xv[slot][t][c] = kAct ? pdk::ld16(xp[t] + (int64_t)k * 16 + 512 * c)
+                              : pdk::ld16(xp[t] + k + 32 * c);
   };
   // Row scales (kRowScale): 32 lanes per row (16 rows per pass over the
   // workgroup, kTiles passes), each adding every 32nd tile's sum of squares,
@@ -284,7 +305,9 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
         for (int q = 0; q < kWaves; ++q) sum += red[q][p * kCols + c][e & 255];
         v[p] = sum;
       }
-      const int64_t at = (int64_t)m * N + n;
+      // Logits (the argmax epilogues) stay row-major; y and the residual are
+      // activations, tiled with kAct.
+      const int64_t at = kAct && !kArg ? pdk::act_at(m, n, N) : (int64_t)m * N + n;
       if (kEpi == kPartial || kEpi == kPartialRms) {
         const float pv = kEpi == kPartialRms ? v[0] * rms[m < 64 ? m : 63] : v[0];
         if (ok) part[((int64_t)blockIdx.y * B + m) * N + n] = pv;
@@ -357,7 +380,9 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
       for (int e = threadIdx.x; e < 256 * kCols; e += kWaves * 64) {
         const int c = e >> 8, m = t * 16 + ((e >> 4) & 15), n = n0 + 16 * c + (e & 15);
         const bool ok = m < B && n < N;
-        const int64_t at = (int64_t)min(m, B - 1) * N + min(n, N - 1);
+        const int mc = min(m, B - 1), nc = min(n, N - 1);
+        const int64_t at = (int64_t)mc * N + nc;  // the fp32 partials are row-major
+        const int64_t ra = kAct ? pdk::act_at(mc, nc, N) : at;
         float pv[16];
 #pragma unroll
         for (int sp = 0; sp < 16; ++sp)
@@ -368,8 +393,8 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
 #pragma unroll
         for (int sp = 0; sp < 16; ++sp)
           if (sp < S) acc += pv[sp];
-        const uint32_t h = pdk::f32_to_bf16_rne(pdk::bf16_to_f32(r[at]) + acc);
-        if (ok) y[at] = (uint16_t)h;
+        const uint32_t h = pdk::f32_to_bf16_rne(pdk::bf16_to_f32(r[ra]) + acc);
+        if (ok) y[ra] = (uint16_t)h;
         const float hv = pdk::bf16_to_f32(h);
         float sq = ok ? hv * hv : 0.f;
 #pragma unroll
@@ -389,14 +414,14 @@ __global__ void argmax_finish_kernel(uint64_t* keys, int B, int32_t* tokens) {
   keys[b] = 0;
 }
 
-template <int kCols, int kEpi, bool kTiled>
+template <int kCols, int kEpi, bool kTiled, bool kAct = false>
 int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
                 uint16_t* y, uint64_t* keys, hipStream_t st, float* part = nullptr,
                 int splits = 1, float* ssq = nullptr, int n_ssq = 0, float eps = 0.f,
                 int* counters = nullptr) {
   const dim3 grid((N + 16 * kCols - 1) / (16 * kCols), splits), block(kWaves * 64);
 #define PDK_WGEMM(T) \
-  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled>), grid, block, 0, st, x, w, B, K, N, splits, ssq, r, y, keys, part, eps, counters)
+  hipLaunchKernelGGL((wgemm_kernel<T, kCols, kEpi, kTiled, kAct>), grid, block, 0, st, x, w, B, K, N, splits, ssq, r, y, keys, part, eps, counters)
   switch ((B + 15) / 16) {
     case 1: PDK_WGEMM(1); break;
     case 2: PDK_WGEMM(2); break;
@@ -412,7 +437,7 @@ int launch_cols(const uint16_t* x, const uint16_t* w, int B, int K, int N, const
 // itself at B = 16 with one tile) but leave fewer workgroups. Measured at the
 // Llama-3.1-8B shapes: gate|up (M = 14336) and the lm_head at B > 8 run best
 // with 4 tiles; N = 4096 and 6144 need every workgroup one tile gives.
-template <int kEpi, bool kTiled>
+template <int kEpi, bool kTiled, bool kAct = false>
 int launch(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* r,
            uint16_t* y, uint64_t* keys, hipStream_t st, float* ssq = nullptr, int n_ssq = 0,
            float eps = 0.f) {
@@ -422,9 +447,10 @@ int launch(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint
   // tiled weights runs 4 tiles wide at every B (B = 4: 181 -> 178 us).
   constexpr bool kGLU = kEpi == kSwiGLU || kEpi == kSwiGLURms;
   const bool four = kGLU ? (wide >= 192 && B <= 32) : ((B > 8 || kTiled) && wide >= 1024);
-  if (four) return launch_cols<4, kEpi, kTiled>(x, w, B, K, N, r, y, keys, st, nullptr, 1, ssq,
-                                                n_ssq, eps);
-  return launch_cols<1, kEpi, kTiled>(x, w, B, K, N, r, y, keys, st, nullptr, 1, ssq, n_ssq, eps);
+  if (four) return launch_cols<4, kEpi, kTiled, kAct>(x, w, B, K, N, r, y, keys, st, nullptr, 1,
+                                                      ssq, n_ssq, eps);
+  return launch_cols<1, kEpi, kTiled, kAct>(x, w, B, K, N, r, y, keys, st, nullptr, 1, ssq, n_ssq,
+                                            eps);
 }
 
 // Tiled copy of W [N][K]: one thread per 16-byte group of the copy.
@@ -476,18 +502,19 @@ int linear_swiglu(const uint16_t* x, const uint16_t* w_gate_up, int B, int K, in
                                  pdk::as_stream(stream));
 }
 
-template <bool kTiled>
+template <bool kTiled, bool kAct = false>
 int linear_ssq(const uint16_t* x, const uint16_t* w, int B, int K, int N, const uint16_t* residual,
                uint16_t* y, float* ssq, uintptr_t stream) {
   pdk::clear_error();
   if (int rc = check_shape(x, w, y, B, K, N)) return rc;
   PDK_REQUIRE(residual && ssq, "null pointer argument");
   PDK_REQUIRE(N % 16 == 0, "N must be a multiple of 16 (got %d)", N);
-  return launch<kResidualSsq, kTiled>(x, w, B, K, N, residual, y, nullptr, pdk::as_stream(stream),
+  PDK_REQUIRE(!kAct || N % kStepK == 0, "tiled activations need N %% %d == 0 (got %d)", kStepK, N);
+  return launch<kResidualSsq, kTiled, kAct>(x, w, B, K, N, residual, y, nullptr, pdk::as_stream(stream),
                                       ssq);
 }
 
-template <bool kTiled>
+template <bool kTiled, bool kAct = false>
 int linear_swiglu_rms(const uint16_t* x, const uint16_t* w_gate_up, int B, int K, int M,
                       const float* ssq, int n_ssq, float eps, uint16_t* y, uintptr_t stream) {
   pdk::clear_error();
@@ -496,7 +523,8 @@ int linear_swiglu_rms(const uint16_t* x, const uint16_t* w_gate_up, int B, int K
   PDK_REQUIRE(n_ssq >= 1 && n_ssq * 16 == K, "n_ssq must be K / 16 = %d (got %d)", K / 16, n_ssq);
   PDK_REQUIRE(eps > 0.f, "eps must be positive");
   PDK_REQUIRE(!kTiled || M % 16 == 0, "tiled gate|up weights need M %% 16 == 0 (got %d)", M);
-  return launch<kSwiGLURms, kTiled>(x, w_gate_up, B, K, M, nullptr, y, nullptr,
+  PDK_REQUIRE(!kAct || M % kStepK == 0, "tiled activations need M %% %d == 0 (got %d)", kStepK, M);
+  return launch<kSwiGLURms, kTiled, kAct>(x, w_gate_up, B, K, M, nullptr, y, nullptr,
                                     pdk::as_stream(stream), const_cast<float*>(ssq), n_ssq, eps);
 }
 
@@ -514,7 +542,7 @@ int linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N, uin
   return pdk::check_launch("argmax_finish_kernel");
 }
 
-template <bool kTiled>
+template <bool kTiled, bool kAct = false>
 int linear_argmax_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N, const float* ssq,
                       int n_ssq, float eps, uint16_t* logits, uint64_t* keys, int32_t* tokens,
                       uintptr_t stream) {
@@ -525,14 +553,14 @@ int linear_argmax_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N,
   PDK_REQUIRE(n_ssq >= 1 && n_ssq * 16 == K, "n_ssq must be K / 16 = %d (got %d)", K / 16, n_ssq);
   PDK_REQUIRE(eps > 0.f, "eps must be positive");
   hipStream_t st = pdk::as_stream(stream);
-  if (int rc = launch<kArgmaxRms, kTiled>(x, w, B, K, N, nullptr, logits, keys, st,
+  if (int rc = launch<kArgmaxRms, kTiled, kAct>(x, w, B, K, N, nullptr, logits, keys, st,
                                           const_cast<float*>(ssq), n_ssq, eps))
     return rc;
   hipLaunchKernelGGL(argmax_finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, keys, B, tokens);
   return pdk::check_launch("argmax_finish_kernel");
 }
 
-template <bool kTiled>
+template <bool kTiled, bool kAct = false>
 int linear_splitk_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N, int splits,
                       const float* ssq, int n_ssq, float eps, float* partials, uintptr_t stream) {
   pdk::clear_error();
@@ -544,14 +572,22 @@ int linear_splitk_rms(const uint16_t* x, const uint16_t* w, int B, int K, int N,
               "splits must be in [1, min(16, K/%d)] (got %d)", kStepK, splits);
   hipStream_t st = pdk::as_stream(stream);
   float* q = const_cast<float*>(ssq);
+  // Three column tiles per workgroup where that fills the 256 CUs exactly and
+  // four would leave some idle (q|k|v at Llama-3.1-8B: 384 tiles x 2 splits =
+  // 256 workgroups, not 192): with tiled activations, 11.59 -> 10.54 us per
+  // launch at B = 16 and 10.41 -> 10.39 at B = 4 (32 launches in a HIP graph).
+  const int64_t tiles = (N + 15) / 16;
+  if (kAct && tiles % 3 == 0 && tiles / 3 * splits <= 256 && tiles / 4 * splits < 256)
+    return launch_cols<3, kPartialRms, kTiled, kAct>(x, w, B, K, N, nullptr, nullptr, nullptr, st,
+                                                     partials, splits, q, n_ssq, eps);
   if (N >= 1024)
-    return launch_cols<4, kPartialRms, kTiled>(x, w, B, K, N, nullptr, nullptr, nullptr, st,
+    return launch_cols<4, kPartialRms, kTiled, kAct>(x, w, B, K, N, nullptr, nullptr, nullptr, st,
                                                partials, splits, q, n_ssq, eps);
-  return launch_cols<1, kPartialRms, kTiled>(x, w, B, K, N, nullptr, nullptr, nullptr, st,
+  return launch_cols<1, kPartialRms, kTiled, kAct>(x, w, B, K, N, nullptr, nullptr, nullptr, st,
                                              partials, splits, q, n_ssq, eps);
 }
 
-template <bool kTiled>
+template <bool kTiled, bool kAct = false>
 int linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int N, int splits,
                         float* partials, uint16_t* residual, float* ssq, int* counters,
                         uintptr_t stream) {
@@ -559,6 +595,7 @@ int linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int 
   if (int rc = check_shape(x, w, partials, B, K, N)) return rc;
   PDK_REQUIRE(residual && ssq && counters, "null pointer argument");
   PDK_REQUIRE(N % 16 == 0, "N must be a multiple of 16 (got %d)", N);
+  PDK_REQUIRE(!kAct || N % kStepK == 0, "tiled activations need N %% %d == 0 (got %d)", kStepK, N);
   PDK_REQUIRE(splits >= 1 && splits <= 16 && splits <= K / kStepK,
               "splits must be in [1, min(16, K/%d)] (got %d)", kStepK, splits);
   hipStream_t st = pdk::as_stream(stream);
@@ -569,9 +606,9 @@ int linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int 
   // One tile without a split was faster still at B=4 (2.819) but 0.08 ms
   // slower at B=16, where x's loads are as many bytes as the weights.
   if (N >= 1024)
-    return launch_cols<2, kPartialFinal, kTiled>(x, w, B, K, N, residual, residual, nullptr, st,
+    return launch_cols<2, kPartialFinal, kTiled, kAct>(x, w, B, K, N, residual, residual, nullptr, st,
                                                  partials, splits, ssq, 0, 0.f, counters);
-  return launch_cols<1, kPartialFinal, kTiled>(x, w, B, K, N, residual, residual, nullptr, st,
+  return launch_cols<1, kPartialFinal, kTiled, kAct>(x, w, B, K, N, residual, residual, nullptr, st,
                                                partials, splits, ssq, 0, 0.f, counters);
 }
 
@@ -717,4 +754,39 @@ extern "C" int pdk_linear_splitk_final_tiled(const uint16_t* x, const uint16_t* 
 extern "C" int pdk_linear_splitk_tiled(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
                                        int splits, float* partials, uintptr_t stream) {
   return linear_splitk<true>(x, wt, B, K, N, splits, partials, stream);
+}
+
+// ---- tiled activations (pdk::act_at) with tiled weights ---------------------
+extern "C" int pdk_linear_ssq_xt(const uint16_t* x, const uint16_t* wt, int B, int K, int N,
+                                 const uint16_t* residual, uint16_t* y, float* ssq,
+                                 uintptr_t stream) {
+  return linear_ssq<true, true>(x, wt, B, K, N, residual, y, ssq, stream);
+}
+
+extern "C" int pdk_linear_swiglu_rms_xt(const uint16_t* x, const uint16_t* wt_gate_up, int B,
+                                        int K, int M, const float* ssq, int n_ssq, float eps,
+                                        uint16_t* y, uintptr_t stream) {
+  return linear_swiglu_rms<true, true>(x, wt_gate_up, B, K, M, ssq, n_ssq, eps, y, stream);
+}
+
+extern "C" int pdk_linear_argmax_rms_xt(const uint16_t* x, const uint16_t* wt, int B, int K,
+                                        int N, const float* ssq, int n_ssq, float eps,
+                                        uint16_t* logits, uint64_t* keys, int32_t* tokens,
+                                        uintptr_t stream) {
+  return linear_argmax_rms<true, true>(x, wt, B, K, N, ssq, n_ssq, eps, logits, keys, tokens,
+                                       stream);
+}
+
+extern "C" int pdk_linear_splitk_rms_xt(const uint16_t* x, const uint16_t* wt, int B, int K,
+                                        int N, int splits, const float* ssq, int n_ssq,
+                                        float eps, float* partials, uintptr_t stream) {
+  return linear_splitk_rms<true, true>(x, wt, B, K, N, splits, ssq, n_ssq, eps, partials, stream);
+}
+
+extern "C" int pdk_linear_splitk_final_xt(const uint16_t* x, const uint16_t* wt, int B, int K,
+                                          int N, int splits, float* partials,
+                                          uint16_t* residual, float* ssq, int* counters,
+                                          uintptr_t stream) {
+  return linear_splitk_final<true, true>(x, wt, B, K, N, splits, partials, residual, ssq,
+                                         counters, stream);
 }

@@ -28,8 +28,12 @@ Weights are [out, in] contiguous (torch Linear layout) with q|k|v and gate|up
 stacked, so each projection is one pass over its weights. By default the
 decoder streams tiled copies of them (pdk_weight_tile, made once at
 construction: each 16-row x 128-column block contiguous in the order the GEMM
-reads it) through the *_tiled entry points, with bit-identical results. Activations are bf16 at every tensor boundary, as the
-reference's are; the kernels accumulate in fp32 and round once.
+reads it) through the *_tiled entry points, with bit-identical results, and
+keeps the activations (the residual stream, attention's output and SwiGLU's
+output) in the matching tiled layout (act_tile; the *_xt entry points), so
+each GEMM reads its activation operand 1 KiB at a time as well.
+Activations are bf16 at every tensor boundary, as the reference's are; the
+kernels accumulate in fp32 and round once.
 """
 import contextlib
 import math
@@ -38,7 +42,7 @@ import torch
 
 from .. import _lib
 from ..kernels import attention as _attn
-from ..kernels.decode_step import fold_norm, tile_weight
+from ..kernels.decode_step import act_rows, act_untile, fold_norm, tile_weight
 from ..kernels.handoff import stream_handle
 
 BF16 = torch.bfloat16
@@ -145,9 +149,21 @@ class LlamaDecoder:
             raise ValueError(f"plan_batch={plan_batch} below max_batch={max_batch}")
         self._captured = False
         e = lambda *s: torch.empty(s, dtype=BF16, device=dev)   # noqa: E731
-        self.x = e(B, H)
-        self.ao = e(B, cfg.n_heads, cfg.head_dim)
-        self.act = e(B, cfg.inter)
+        # Activations (the residual stream x, attention's output, SwiGLU's
+        # output) in the tiled layout the GEMMs read as their MFMA operand
+        # (act_tile; the _xt entry points) when the weights are tiled and every
+        # width is a multiple of 128, else row-major [B, .].
+        self.act_tiled = bool(tiled) and cfg.inter % 16 == 0 and all(
+            d % 128 == 0 for d in (H, cfg.inter, cfg.n_heads * cfg.head_dim))
+        if self.act_tiled:
+            rows = act_rows(B)
+            self.x_buf = e(rows * H)
+            self.ao = e(rows * cfg.n_heads * cfg.head_dim)
+            self.act = e(rows * cfg.inter)
+        else:
+            self.x_buf = e(B, H)
+            self.ao = e(B, cfg.n_heads, cfg.head_dim)
+            self.act = e(B, cfg.inter)
         self.logits = e(B, cfg.vocab)
         self.tokens = torch.empty(B, dtype=torch.int32, device=dev)
         self.keys = torch.zeros(B, dtype=torch.int64, device=dev)    # argmax scratch, kept zero
@@ -197,14 +213,27 @@ class LlamaDecoder:
             # The copies are written on the current stream; a step may run on
             # another one, so they are complete before the constructor returns.
             torch.cuda.current_stream(dev).synchronize()
-        self._gemm = {n: n + "_tiled" if self.tiled else n for n in
+        suffix = "_xt" if self.act_tiled else "_tiled" if self.tiled else ""
+        self._gemm = {n: n + suffix for n in
                       ("pdk_linear_splitk_rms", "pdk_linear_ssq", "pdk_linear_swiglu_rms",
                        "pdk_linear_splitk_final", "pdk_linear_argmax_rms")}
+        self._gemm["pdk_embed_ssq"] = "pdk_embed_ssq_xt" if self.act_tiled else "pdk_embed_ssq"
+        self._gemm["pdk_decode_attn_rope"] = ("pdk_decode_attn_rope_xt" if self.act_tiled
+                                              else "pdk_decode_attn_rope")
         if cfg.hidden % 16 or cfg.head_dim != 128:
             raise ValueError("the fused norms need hidden % 16 == 0 and head_dim 128")
         self._layers = [tuple(t.data_ptr() for t in (wt[0], wt[1], wt[2], wt[3], cache.k[i],
                                                      cache.v[i]))
                         for i, wt in enumerate(self._wt)]
+
+    @property
+    def x(self):
+        """The residual stream [max_batch, hidden] (bf16), row-major: after a
+        step, rows :B hold the final hidden state before the final norm. A
+        copy when the decoder keeps it tiled (x_buf is the buffer itself)."""
+        if self.act_tiled:
+            return act_untile(self.x_buf, self.max_batch, self.cfg.hidden)
+        return self.x_buf
 
     def reserve(self, max_ctx):
         """Allocate the attention workspace for max_batch streams at ``max_ctx``
@@ -232,8 +261,8 @@ class LlamaDecoder:
         holding at least ceil(ctx/16) blocks each; max_ctx (<= max_blocks*16)
         sizes the attention's split plan and should cover every ctx_lens. Returns
         the next token per stream (int32 [B], device) and leaves the final hidden
-        state in self.x[:B] (the residual stream before the final norm) and the
-        logits in self.logits[:B]. ``stream``: a torch stream for every launch (default:
+        state in rows :B of the residual stream (self.x, before the final norm)
+        and the logits in self.logits[:B]. ``stream``: a torch stream for every launch (default:
         the current stream)."""
         cfg, w, cache = self.cfg, self.w, self.cache
         B = tokens.shape[0]
@@ -253,13 +282,12 @@ class LlamaDecoder:
         st = stream_handle(stream)
         H, NH, NKV, HD, M = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.inter
         QKV, eps = cfg.qkv_dim, cfg.eps
-        x = self.x[:B]
         ws = self._workspace(max(B, self.plan_batch), max_ctx)
         ws_ptr = ws.data_ptr() if ws is not None else None
         ws_bytes = ws.numel() * 4 if ws is not None else 0
         mb, nb = tables.shape[1], cache.num_blocks
         tp, cp = tables.data_ptr(), ctx_lens.data_ptr()
-        xp = x.data_ptr()
+        xp = self.x_buf.data_ptr()
         aop, actp, inv = self.ao.data_ptr(), self.act.data_ptr(), self.inv.data_ptr()
         call = _lib.call
         g = self._gemm
@@ -268,14 +296,15 @@ class LlamaDecoder:
                                      g["pdk_linear_argmax_rms"])
         ssqp, ssqa, cntp, n_ssq = (self.ssq.data_ptr(), self.ssq_a.data_ptr(),
                                    self.counters.data_ptr(), H // 16)
+        emb, attn = g["pdk_embed_ssq"], g["pdk_decode_attn_rope"]
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
-            call("pdk_embed_ssq", w.embed.data_ptr(), cfg.vocab, tokens.data_ptr(),
+            call(emb, w.embed.data_ptr(), cfg.vocab, tokens.data_ptr(),
                  tokens.element_size(), B, H, xp, ssqa, st)
             partp, sp = self.part.data_ptr(), self.down_splits
             pqp, qs = self.part_qkv.data_ptr(), self.qkv_splits
             for wqkv, wo, wgu, wd, ck, cv in self._layers:
                 call(lin_skr, xp, wqkv, B, H, QKV, qs, ssqa, n_ssq, eps, pqp, st)
-                call("pdk_decode_attn_rope", pqp, qs, inv, ck, cv, nb, tp, mb, cp, int(max_ctx),
+                call(attn, pqp, qs, inv, ck, cv, nb, tp, mb, cp, int(max_ctx),
                      B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, self.plan_batch, st)
                 call(lin_ssq, aop, wo, B, NH * HD, H, xp, xp, ssqp, st)
                 call(lin_swr, xp, wgu, B, H, M, ssqp, n_ssq, eps, actp, st)

@@ -7,7 +7,8 @@ from .attention import (decode_attention, decode_attention_rope, cache_append, g
 from .decode_step import (rmsnorm, rope_cache_append, rope_cache_append_partials, swiglu, linear,
                           linear_swiglu, linear_argmax, linear_splitk, rmsnorm_partials,
                           linear_ssq, linear_swiglu_rms, fold_norm, linear_splitk_final, linear_splitk_rms,
-                          linear_argmax_rms, row_ssq, embed_ssq, TiledWeight, tile_weight)
+                          linear_argmax_rms, row_ssq, embed_ssq, TiledWeight, tile_weight,
+                          act_rows, act_tile, act_untile)
 
 __all__ = ["pack_kv", "pack_kv_batch", "scatter_paged", "scatter_paged_batch", "gather_paged",
            "frame_shape", "frame_views", "stream_handle", "validate_table", "copy_kernel",
@@ -17,4 +18,4 @@ __all__ = ["pack_kv", "pack_kv_batch", "scatter_paged", "scatter_paged_batch", "
            "rmsnorm", "rope_cache_append", "rope_cache_append_partials", "swiglu", "linear", "linear_swiglu", "linear_argmax",
            "linear_splitk", "rmsnorm_partials", "linear_ssq", "linear_swiglu_rms", "fold_norm",
            "linear_splitk_final", "linear_splitk_rms", "linear_argmax_rms", "row_ssq", "embed_ssq",
-           "TiledWeight", "tile_weight"]
+           "TiledWeight", "tile_weight", "act_rows", "act_tile", "act_untile"]

@@ -190,6 +190,33 @@ def tile_weight(w, stream=None):
     return TiledWeight(data, N, K)
 
 
+def act_rows(B):
+    """Rows a tiled activation buffer holds for B streams: 16 ceil(B/16)."""
+    return (B + 15) // 16 * 16
+
+
+def act_tile(x):
+    """Row-major [B, K] (K % 128 == 0) -> the flat tiled activation layout of
+    the _xt entry points (act_rows(B) rows; padding rows zero): the 16 x 128
+    block of rows 16t.. and columns 128s.. is contiguous at (t K/128 + s)
+    2048, and inside it column 8j + e of row r is at (16 j + r) 8 + e."""
+    B, K = x.shape
+    if K % 128:
+        raise ValueError(f"K={K} must be a multiple of 128")
+    Bp = act_rows(B)
+    xp = torch.zeros((Bp, K), dtype=x.dtype, device=x.device)
+    xp[:B] = x
+    # [t, r, s, j, e] -> [t, s, j, r, e]
+    return xp.view(Bp // 16, 16, K // 128, 16, 8).permute(0, 2, 3, 1, 4).contiguous().view(-1)
+
+
+def act_untile(xt, B, K):
+    """The inverse of act_tile: rows 0..B-1 of a tiled buffer as [B, K]."""
+    Bp = act_rows(B)
+    v = xt.view(-1)[:Bp * K].view(Bp // 16, K // 128, 16, 16, 8).permute(0, 3, 1, 2, 4)
+    return v.reshape(Bp, K)[:B]
+
+
 def _check_linear(x, w, rows_per_col=1):
     _need(x, "x")
     if isinstance(w, TiledWeight):

@@ -787,7 +787,7 @@ def test_graph_replays_match_eager(cuda):
     want_x, want_tok = dec.x[:B].clone(), dec.tokens[:B].clone()
     graph = dec.capture(tok, ctx_d, tables, cap)
     for r in range(3):
-        dec.x.zero_()
+        dec.x_buf.zero_()
         dec.tokens.fill_(-1)
         torch.cuda.synchronize()
         graph.replay()
