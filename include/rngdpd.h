@@ -107,8 +107,11 @@ int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_layers,
  * (engines/decode_batch.py:357-377). Writes blocks 0 .. ceil(P/16)-1 of the
  * request; token slots >= P inside the last block are written as zero, as
  * the reference's one-hot injection needs a zero slot
- * (connector/rngd_kv.py:155-159). Block ids outside [0, num_blocks) are
- * skipped by the kernel; callers validate tables before the call.
+ * (connector/rngd_kv.py:155-159). A block id outside [0, num_blocks) among
+ * a request's first ceil(P/16) table entries is skipped: nothing is written
+ * for its 16 tokens and the call still returns 0. The Python wrappers check
+ * host tables before the call; pdk_scatter_paged_batch_counted reports the
+ * skipped ids of device tables without a host synchronisation.
  */
 typedef struct pdk_scatter_req {
   const uint16_t* frame;   /* [L][2][Hkv*D*S]                               */
@@ -128,6 +131,20 @@ int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs,
                             uint16_t* cache_k, uint16_t* cache_v,
                             int64_t cache_layer_stride, int num_blocks,
                             uintptr_t stream);
+
+/* pdk_scatter_paged_batch that also adds to *skipped (device int32, zeroed by
+ * the caller, e.g. once before a run of calls) the number of (request, block)
+ * ids it skipped because they lie outside [0, num_blocks): each such id once
+ * per call. Read it after the stream has passed the call (an event, or the
+ * request's own fence): a nonzero count means KV was not placed. No
+ * reference counterpart: the reference writes dense per-lane caches with no
+ * block table (engines/decode_batch.py:357-377). */
+int pdk_scatter_paged_batch_counted(const pdk_scatter_req* reqs, int n_reqs,
+                                    int n_layers, int S, int n_kv_heads,
+                                    int head_dim, uint16_t* cache_k,
+                                    uint16_t* cache_v, int64_t cache_layer_stride,
+                                    int num_blocks, int32_t* skipped,
+                                    uintptr_t stream);
 
 /* ---- gather: paged decode cache -> transport frame -----------------------
  * Inverse of the scatter (the frame is written S-wide, zero for t >= P).
@@ -149,7 +166,12 @@ int pdk_gather_paged(const uint16_t* cache_k, const uint16_t* cache_v,
  *   q      [B][Hq][D] bf16; query head qh reads KV head qh / (Hq/Hkv)
  *   ctx    device int32 [B]: stream b attends to tokens 0 .. ctx[b]-1
  *          (the reference's slots 0..pos inclusive, pos = ctx-1)
- *   tables device int32 [B][max_blocks]
+ *   tables device int32 [B][max_blocks]. A block id outside [0, num_blocks)
+ *          inside a stream's context masks that block's 16 tokens: they
+ *          take no part in the softmax, as slots past the context do (a
+ *          stream with no token left gets a zero output). The reference's
+ *          dense per-lane cache has no block ids; this is the paged cache's
+ *          counterpart of its -1e4 mask (engines/decode_batch.py:246-261).
  *   scale  multiplies q.k (1.0 when the scale is folded into q, as the
  *          reference folds 1/sqrt(D) into wq, kernels/decode_batch.py:204)
  *   max_ctx  host upper bound of ctx[] used for the launch grid (tokens

@@ -156,7 +156,11 @@ int orc_cache_append(const uint16_t* k_new, const uint16_t* v_new, uint16_t* cac
  * q.k * scale over slots 0..pos (pos = ctx-1; slots > pos get -1e4, whose
  * exp underflows to exactly 0 after the max subtraction, so they drop out),
  * max-subtracted softmax, then p.V. Query head qh reads KV head qh/(Hq/Hkv)
- * (q.reshape(B, NKV, G, HD), :151). Accumulates in double, returns float. */
+ * (q.reshape(B, NKV, G, HD), :151). Accumulates in double, returns float.
+ * The paged cache adds one case the reference's dense per-lane cache cannot
+ * have: a block id outside [0, num_blocks) inside the context. Its tokens
+ * are masked like slots past pos (they take no part in the softmax); a
+ * stream with no token left gets a zero output. */
 int orc_decode_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
                     int num_blocks, const int32_t* tables, int max_blocks, const int32_t* ctx,
                     int B, int Hq, int Hkv, int D, float scale, float* out) {
@@ -172,18 +176,21 @@ int orc_decode_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* 
       const uint16_t* qp = q + ((int64_t)b * Hq + qh) * D;
       float* op = out + ((int64_t)b * Hq + qh) * D;
       double mx = -INFINITY;
+      int live = 0;
       for (int t = 0; t < n; ++t) {
         const int blk = tables[(int64_t)b * max_blocks + t / BS];
+        if (blk < 0 || blk >= num_blocks) continue;          /* masked */
+        const uint16_t* kb = cache_k + ((int64_t)blk * Hkv + h) * BS * D;
         double s = 0.0;
-        if (blk >= 0 && blk < num_blocks) {
-          const uint16_t* kb = cache_k + ((int64_t)blk * Hkv + h) * BS * D;
-          for (int d = 0; d < D; ++d) s += (double)widen(qp[d]) * (double)widen(kb[k_index(t % BS, d, D)]);
-        }
+        for (int d = 0; d < D; ++d) s += (double)widen(qp[d]) * (double)widen(kb[k_index(t % BS, d, D)]);
         sc[t] = s * scale;
         if (sc[t] > mx) mx = sc[t];
+        ++live;
       }
       double sum = 0.0;
       for (int t = 0; t < n; ++t) {
+        const int blk = tables[(int64_t)b * max_blocks + t / BS];
+        if (blk < 0 || blk >= num_blocks) continue;
         sc[t] = exp(sc[t] - mx);
         sum += sc[t];
       }
@@ -194,7 +201,7 @@ int orc_decode_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* 
           if (blk < 0 || blk >= num_blocks) continue;
           acc += sc[t] * (double)widen(cache_v[(((int64_t)blk * Hkv + h) * D + d) * BS + t % BS]);
         }
-        op[d] = n > 0 ? (float)(acc / sum) : 0.0f;
+        op[d] = live > 0 ? (float)(acc / sum) : 0.0f;
       }
     }
   }

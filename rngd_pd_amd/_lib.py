@@ -75,6 +75,8 @@ SIGNATURES = {
     "pdk_scatter_paged": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I64, _I, _U]),
     "pdk_scatter_paged_batch": (_I, [ctypes.POINTER(ScatterReq), _I, _I, _I, _I, _I, _P, _P,
                                      _I64, _I, _U]),
+    "pdk_scatter_paged_batch_counted": (_I, [ctypes.POINTER(ScatterReq), _I, _I, _I, _I, _I, _P,
+                                             _P, _I64, _I, _P, _U]),
     "pdk_gather_paged": (_I, [_P, _P, _I64, _I, _P, _I, _I, _I, _I, _I, _I, _P, _U]),
     "pdk_decode_attn_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "pdk_decode_attn": (_I, [_P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, ctypes.c_float,

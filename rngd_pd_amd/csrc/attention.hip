@@ -1,10 +1,11 @@
 // GQA decode attention over the paged KV cache, gfx950.
 //
 // A unit is the token range [split*split_tokens, (split+1)*split_tokens) of
-// stream b, KV head h, and 1, 2, 4 or 8 workgroups of 8 wavefronts share it:
-// each computes the scores of its share of the group's query heads over all
-// of the unit's K, and their output over its share of V's dims (all, or one
-// half). With B*Hkv >= 128 the host uses one split (no merge at all); smaller
+// stream b, KV head h, and 2^(qsplit + vsplit) workgroups of 8 wavefronts
+// share it (1 to 32: V's dims in 1 or 2 parts times the group's query heads
+// in 1 to 16): each computes the scores of its share of the group's query
+// heads over all of the unit's K, and their output over its share of V's
+// dims (all, or one half). With B*Hkv >= 128 the host uses one split (no merge at all); smaller
 // batches split the context so the launch still spreads over the CUs, and a
 // second small kernel merges the splits.
 //
@@ -281,16 +282,21 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
     sc[i] = s0[i];
     sc[4 + i] = s1[i];
   }
+  // This lane's 8 tokens lie in one block: lo for lane groups 0-1, hi for 2-3.
+  const bool blk_ok = valid_block(g < 2 ? lo : hi, a.num_blocks);
   if (!full) {
+    // Tokens past the context and tokens of an invalid block id take no part.
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      if (tv + e >= lim) sc[e] = -INFINITY;
+      if (!blk_ok || tv + e >= lim) sc[e] = -INFINITY;
   }
   float mx = vmax(vmax(vmax(sc[0], sc[1]), vmax(sc[2], sc[3])),
                   vmax(vmax(sc[4], sc[5]), vmax(sc[6], sc[7])));
-  mx = column_max(mx);                           // finite: token `span` is live
+  mx = column_max(mx);                           // -inf when no token of the span is live
   const float m_new = first ? mx : vmax(m, mx);
-  const float mc = m_new * a.scale_log2;
+  // With no live token so far (m_new = -inf) every weight must come out 0:
+  // exp2(-inf - 0), not exp2(-inf + inf).
+  const float mc = m_new == -INFINITY ? 0.f : m_new * a.scale_log2;
   float p[8], ps = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -303,6 +309,7 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
     // Exactly 1 unless this column's maximum grew (the fma would otherwise
     // leave the rounding residual of m * c in the exponent): a column's sums
     // then never depend on which other columns share the wavefront.
+    // m = -inf (nothing live before this span): exp2(-inf) = 0, and O and lsum are 0.
     const float alpha = m_new > m ? __builtin_amdgcn_exp2f(fmaf(m, a.scale_log2, -mc)) : 1.f;
     lsum = lsum * alpha + ps;
     if (__any(m_new > m)) {
@@ -320,12 +327,11 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
     if (blk >= 0) patch_v<kNV>(r, span, nt, g, j);
   }
   if (!full) {
-    const bool v_ok = valid_block(g < 2 ? lo : hi, a.num_blocks);
     uint32_t mk[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w)
-      mk[w] = (v_ok && tv + 2 * w < lim ? 0x0000ffffu : 0u) |
-              (v_ok && tv + 2 * w + 1 < lim ? 0xffff0000u : 0u);
+      mk[w] = (blk_ok && tv + 2 * w < lim ? 0x0000ffffu : 0u) |
+              (blk_ok && tv + 2 * w + 1 < lim ? 0xffff0000u : 0u);
 #pragma unroll
     for (int n = 0; n < kNV; ++n)
 #pragma unroll

@@ -178,6 +178,7 @@ struct ScatterArgs {
   uint16_t* cache_k;
   uint16_t* cache_v;
   int64_t cache_ls;              // elements between layers of the cache
+  int32_t* skipped;              // or null: += block ids outside [0, num_blocks) not written
   int n_req, num_blocks, S, Hkv, D, nD;
 };
 
@@ -236,11 +237,18 @@ __global__ __launch_bounds__(256) void scatter_kernel(const ScatterArgs a) {
   const int nblk = min(rP >> 4, R.n_table);
   const int j0 = ct * (kTileT / 16);
   int blk[4];
+  int bad = 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int id = R.table[min(j0 + q, nblk - 1)];
     blk[q] = (j0 + q < nblk && id >= 0 && id < a.num_blocks) ? id : -1;
+    bad += j0 + q < nblk && blk[q] < 0;
   }
+  // Invalid ids are skipped (nothing is written for their tokens); with a
+  // counter, the first unit of each chunk (layer 0, head 0, dims 0..63)
+  // reports them, so each (request, block) counts once per launch.
+  if (a.skipped && bad && l == 0 && h == 0 && dt == 0 && lane == 0)
+    atomicAdd(a.skipped, bad);
   if (t0 + 8 > P) {              // a narrow frame leaves tokens >= P unwritten
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -448,10 +456,10 @@ extern "C" int pdk_pack_kv(const uint16_t* src_k, const uint16_t* src_v, int64_t
   return pdk_pack_kv_batch(&r, 1, n_layers, S, n_kv_heads, head_dim, stream);
 }
 
-extern "C" int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs, int n_layers,
-                                       int S, int n_kv_heads, int head_dim, uint16_t* cache_k,
-                                       uint16_t* cache_v, int64_t cache_layer_stride,
-                                       int num_blocks, uintptr_t stream) {
+namespace {
+int scatter_batch(const pdk_scatter_req* reqs, int n_reqs, int n_layers, int S, int n_kv_heads,
+                  int head_dim, uint16_t* cache_k, uint16_t* cache_v, int64_t cache_layer_stride,
+                  int num_blocks, int32_t* skipped, uintptr_t stream) {
   pdk::clear_error();
   int rc = check_common(n_layers, S, n_kv_heads, head_dim);
   if (rc) return rc;
@@ -467,6 +475,7 @@ extern "C" int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs, 
               (long long)cache_layer_stride, (long long)per_layer);
   PDK_REQUIRE(cache_layer_stride % 8 == 0, "cache_layer_stride must be a multiple of 8");
   ScatterArgs a{};
+  a.skipped = skipped;
   int max_p = 0;
   for (int i = 0; i < n_reqs; ++i) {
     const pdk_scatter_req& r = reqs[i];
@@ -505,6 +514,25 @@ extern "C" int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs, 
   else
     hipLaunchKernelGGL(scatter_kernel<false>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
   return pdk::check_launch("scatter_kernel");
+}
+}  // namespace
+
+extern "C" int pdk_scatter_paged_batch(const pdk_scatter_req* reqs, int n_reqs, int n_layers,
+                                       int S, int n_kv_heads, int head_dim, uint16_t* cache_k,
+                                       uint16_t* cache_v, int64_t cache_layer_stride,
+                                       int num_blocks, uintptr_t stream) {
+  return scatter_batch(reqs, n_reqs, n_layers, S, n_kv_heads, head_dim, cache_k, cache_v,
+                       cache_layer_stride, num_blocks, nullptr, stream);
+}
+
+extern "C" int pdk_scatter_paged_batch_counted(const pdk_scatter_req* reqs, int n_reqs,
+                                               int n_layers, int S, int n_kv_heads, int head_dim,
+                                               uint16_t* cache_k, uint16_t* cache_v,
+                                               int64_t cache_layer_stride, int num_blocks,
+                                               int32_t* skipped, uintptr_t stream) {
+  PDK_REQUIRE(skipped && ((uintptr_t)skipped & 3u) == 0, "skipped must be a 4-byte aligned int32");
+  return scatter_batch(reqs, n_reqs, n_layers, S, n_kv_heads, head_dim, cache_k, cache_v,
+                       cache_layer_stride, num_blocks, skipped, stream);
 }
 
 extern "C" int pdk_scatter_paged(const uint16_t* frame, const int32_t* block_table, int n_table,

@@ -1,7 +1,7 @@
 """HIP kernels of the handoff, decode attention and the decode step, called through the C ABI."""
 from .handoff import (pack_kv, pack_kv_batch, scatter_paged, scatter_paged_batch, gather_paged,
                       frame_shape, frame_views, stream_handle, validate_table, copy_kernel,
-                      stream_probe)
+                      stream_probe, check_skipped)
 from .attention import (decode_attention, decode_attention_rope, cache_append, greedy_argmax,
                         workspace_bytes, get_workspace, attn_read_probe)
 from .decode_step import (rmsnorm, rope_cache_append, rope_cache_append_partials, swiglu, linear,
@@ -12,6 +12,7 @@ from .decode_step import (rmsnorm, rope_cache_append, rope_cache_append_partials
 
 __all__ = ["pack_kv", "pack_kv_batch", "scatter_paged", "scatter_paged_batch", "gather_paged",
            "frame_shape", "frame_views", "stream_handle", "validate_table", "copy_kernel",
+           "check_skipped",
            "stream_probe",
            "decode_attention", "decode_attention_rope", "cache_append", "greedy_argmax", "workspace_bytes", "get_workspace",
            "attn_read_probe",

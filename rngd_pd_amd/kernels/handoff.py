@@ -177,8 +177,14 @@ def scatter_paged(frame, block_table, num_tokens, S, cache_k, cache_v, n_kv_head
               cache_k.stride(0), nb, stream_handle(stream))
 
 
-def scatter_paged_batch(reqs, S, cache_k, cache_v, stream=None):
-    """reqs: list of (frame, device int32 table, num_tokens)."""
+def scatter_paged_batch(reqs, S, cache_k, cache_v, stream=None, skipped=None):
+    """reqs: list of (frame, device int32 table, num_tokens).
+
+    Block ids outside [0, num_blocks) are skipped by the kernel. ``skipped``
+    (a device int32 tensor of one element): the calls add the number of
+    skipped ids to it, with no host synchronisation; read it once the stream
+    has passed them (nonzero: some KV was not placed). check_skipped() does
+    that read and raises."""
     cache_k, cache_v = _check_cache(cache_k, cache_v)
     L, nb, H, _, D = cache_k.shape
     arr = []
@@ -188,12 +194,28 @@ def scatter_paged_batch(reqs, S, cache_k, cache_v, stream=None):
             raise ValueError(f"frame must be contiguous {frame_shape(L, H, D, S)}")
         _need(table, "table", torch.int32)
         arr.append(ScatterReq(frame.data_ptr(), table.data_ptr(), int(P), table.numel()))
+    if skipped is not None:
+        _need(skipped, "skipped", torch.int32)
     st = stream_handle(stream)
     for i in range(0, len(arr), PDK_MAX_BATCH):
         chunk = arr[i:i + PDK_MAX_BATCH]
         c_arr = (ScatterReq * len(chunk))(*chunk)
-        _lib.call("pdk_scatter_paged_batch", c_arr, len(chunk), L, S, H, D,
-                  cache_k.data_ptr(), cache_v.data_ptr(), cache_k.stride(0), nb, st)
+        if skipped is None:
+            _lib.call("pdk_scatter_paged_batch", c_arr, len(chunk), L, S, H, D,
+                      cache_k.data_ptr(), cache_v.data_ptr(), cache_k.stride(0), nb, st)
+        else:
+            _lib.call("pdk_scatter_paged_batch_counted", c_arr, len(chunk), L, S, H, D,
+                      cache_k.data_ptr(), cache_v.data_ptr(), cache_k.stride(0), nb,
+                      skipped.data_ptr(), st)
+
+
+def check_skipped(skipped, stream=None):
+    """Wait for ``stream`` (default: the current one) and raise ValueError if
+    the counted scatters before it skipped any block id."""
+    (stream or torch.cuda.current_stream(skipped.device)).synchronize()
+    n = int(skipped.item())
+    if n:
+        raise ValueError(f"{n} block ids outside [0, num_blocks): their tokens were not placed")
 
 
 def gather_paged(cache_k, cache_v, block_table, num_tokens, S, frame=None, stream=None):

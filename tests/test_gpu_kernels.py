@@ -171,6 +171,10 @@ def _attn_case(rng, B, Hq, H, ctx, D=128):
     (3, 6, 3, [100, 517, 33]),
     (2, 24, 3, [700, 1]),
     (5, 80, 5, [64, 1, 999, 300, 16]),
+    # a unit's query heads split 8 ways (with the V halves, 16 workgroups per
+    # unit) and 16 ways (32 per unit)
+    (1, 64, 8, [200]),
+    (2, 32, 2, [16, 1]),
 ])
 def test_decode_attention_vs_fp32(cuda, B, Hq, H, ctx):
     from rngd_pd_amd.kernels import decode_attention
@@ -185,6 +189,81 @@ def test_decode_attention_vs_fp32(cuda, B, Hq, H, ctx):
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("B,Hq,H,ctx", [(4, 32, 8, [70, 512, 40, 300]), (16, 32, 8, [512] * 16),
+                                        (1, 32, 8, [2000]), (3, 32, 2, [100, 600, 17])])
+def test_decode_attention_masks_invalid_block_ids(cuda, B, Hq, H, ctx):
+    """Block ids outside [0, num_blocks) inside a context mask their tokens, as
+    the oracle does: a masked block in the middle, a stream's first two blocks
+    (a whole first span, so its running maximum starts at -inf), a stream's
+    last partial block, and a stream with every block invalid (zero output);
+    one context split and several."""
+    from rngd_pd_amd.kernels import decode_attention
+    rng = np.random.default_rng(B * 13 + Hq + sum(ctx))
+    q, ck, cv, tables, ctx_a = _attn_case(rng, B, Hq, H, ctx)
+    nb = ck.shape[0]
+    n0 = (ctx[0] + 15) // 16
+    tables[0, n0 // 2] = -1
+    if B > 1:
+        tables[1, :2] = [nb, nb + 100]
+    if B > 2:
+        tables[2, (ctx[2] - 1) // 16] = -5
+    if B > 3:
+        tables[3, :(ctx[3] + 15) // 16] = -1
+    scale = 1.0 / math.sqrt(128)
+    want = orc.decode_attn(q, ck, cv, tables, ctx_a, scale)
+    out = torch.full((B, Hq, 128), float("nan"), dtype=torch.bfloat16, device=cuda)
+    print(f"attention with invalid block ids B={B} Hq={Hq} H={H} ctx={ctx[:4]}", flush=True)
+    decode_attention(to_dev(q), to_dev(ck), to_dev(cv), torch.from_numpy(tables).to(cuda),
+                     torch.from_numpy(ctx_a).to(cuda), int(ctx_a.max()), scale=scale, out=out)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    if B > 3:
+        assert np.all(got[3] == 0.0)
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+
+
+def test_scatter_reports_skipped_block_ids(cuda):
+    """Invalid ids in device tables are skipped and counted: the valid blocks
+    hold what the oracle's scatter writes (it skips the same ids), nothing
+    else changes, and the counter holds one per skipped (request, block)."""
+    from rngd_pd_amd.kernels import check_skipped, scatter_paged_batch
+    rng = np.random.default_rng(23)
+    L, S, H, D = 2, 256, 8, 128
+    Ps = [200, 17, 256]
+    need = [(p + 15) // 16 for p in Ps]
+    nb = sum(need) + 4
+    perm = rng.permutation(nb).astype(np.int32)
+    tables, off = [], 0
+    for n in need:
+        tables.append(perm[off:off + n].copy())
+        off += n
+    tables[0][3] = -1
+    tables[0][12] = nb
+    tables[2][0] = nb + 9
+    ck, cv = _cache(L, nb, H, D)
+    want_k, want_v = ck.copy(), cv.copy()
+    frames = []
+    for P, t in zip(Ps, tables):
+        k, v = _prefill(rng, L, S, H, D)
+        f = orc.pack_kv(k, v, P, S)
+        frames.append(f)
+        orc.scatter_paged(f, t, P, S, H, D, want_k, want_v)
+    dk, dv = to_dev(ck), to_dev(cv)
+    skipped = torch.zeros(1, dtype=torch.int32, device=cuda)
+    reqs = [(to_dev(f), torch.from_numpy(t).to(cuda), P) for f, t, P in zip(frames, tables, Ps)]
+    print("scatter with invalid block ids", flush=True)
+    scatter_paged_batch(reqs, S, dk, dv, skipped=skipped)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host(dk), want_k)
+    np.testing.assert_array_equal(to_host(dv), want_v)
+    assert int(skipped.item()) == 3
+    with pytest.raises(ValueError, match="3 block ids"):
+        check_skipped(skipped)
+    skipped.zero_()
+    scatter_paged_batch(reqs[1:2], S, dk, dv, skipped=skipped)
+    check_skipped(skipped)                                    # a valid table: no error
 
 
 def test_decode_attention_sharing_never_changes_a_result(cuda):

@@ -223,6 +223,37 @@ def test_attention_matches_torch_float64(B, Hq, H, ctx):
                                rtol=1e-5, atol=1e-6)
 
 
+def test_attention_masks_invalid_block_ids():
+    """A block id outside [0, num_blocks) inside the context masks that block's
+    tokens: the result is the float64 softmax attention over the other
+    tokens alone (gathered by token, the invalid ones dropped), and a stream
+    with no valid block gets zeros."""
+    rng = np.random.default_rng(14)
+    B, Hq, H, D = 3, 8, 2, 32
+    q, ck, cv, tables, c = _attn_case(rng, B, Hq, H, [70, 40, 33], D)
+    nb = ck.shape[0]
+    tables[0, 1] = -1                      # tokens 16..31 of stream 0
+    tables[0, 4] = nb + 3                  # its last, partial block
+    tables[1, 0] = nb                      # stream 1's first block
+    tables[2, :3] = -7                     # every block of stream 2
+    scale = 1 / math.sqrt(D)
+    got = orc.decode_attn(q, ck, cv, tables, c, scale)
+    w = lambda u: torch.from_numpy(orc.bf16_widen(u)).double()   # noqa: E731
+    Q, CK, CV = w(q), w(oatt.k_block_rows(ck)), w(cv)
+    for b in range(B):
+        t = torch.tensor([i for i in range(int(c[b])) if 0 <= tables[b, i // 16] < nb],
+                         dtype=torch.int64)
+        if t.numel() == 0:
+            np.testing.assert_array_equal(got[b], 0.0)
+            continue
+        blk = torch.from_numpy(tables[b].astype(np.int64))[t // 16]
+        Kb, Vb = CK[blk, :, t % 16, :], CV[blk, :, :, t % 16]
+        for qh in range(Hq):
+            s_ = (Kb[:, qh // (Hq // H)] @ Q[b, qh]) * scale
+            want = (torch.softmax(s_, 0) @ Vb[:, qh // (Hq // H)]).numpy()
+            np.testing.assert_allclose(got[b, qh], want, rtol=1e-5, atol=1e-6)
+
+
 def test_attention_matches_cpu_layer_restatement():
     """The literal cpu_layer lines (kernels/decode_batch.py:147-156) on the dense
     layout, including the new-token write at positions[b]."""
