@@ -8,6 +8,7 @@
 
 #include <algorithm>
 
+#include <exception>
 #include <thread>
 #include <vector>
 
@@ -208,12 +209,23 @@ extern "C" int pdk_host_zero_frame_tail(uint16_t* frame, int n_layers, int n_kv_
     for (int l = 0; l < n_layers; ++l) layer(l);
     return PDK_OK;
   }
+  // Thread t takes layers t, t + nt, ...; the calling thread is thread 0 and
+  // also takes the share of any thread that could not be started (no
+  // exception leaves this C entry point).
   std::vector<std::thread> pool;
-  pool.reserve(nt - 1);
-  for (int t = 1; t < nt; ++t)
-    pool.emplace_back([&, t] {
-      for (int l = t; l < n_layers; l += nt) layer(l);
-    });
+  int started = 1;
+  try {
+    pool.reserve(nt - 1);
+    for (int t = 1; t < nt; ++t) {
+      pool.emplace_back([&, t] {
+        for (int l = t; l < n_layers; l += nt) layer(l);
+      });
+      ++started;
+    }
+  } catch (const std::exception&) {
+  }
+  for (int t = started; t < nt; ++t)
+    for (int l = t; l < n_layers; l += nt) layer(l);
   for (int l = 0; l < n_layers; l += nt) layer(l);
   for (auto& th : pool) th.join();
   return PDK_OK;

@@ -363,6 +363,21 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
     // (counters[blockIdx.x] counts the splits of this column group that are
     // done); the last one resets the count for the next call and finishes the
     // group. No workgroup waits for another.
+    //
+    // Ordering. Every access to the partials and the counter is an
+    // agent-scope atomic, which gfx950 performs at the device's coherence
+    // point (sc1: through the XCD's L2, not cached in it), so no write-back
+    // or invalidation of a cache is needed for them to meet across XCDs. What
+    // remains is order: s_waitcnt vmcnt(0) completes this workgroup's partial
+    // stores (gfx9 counts stores in vmcnt) before the barrier and the ticket;
+    // in the last split the loads of the partials follow the ticket's result
+    // through the barrier and the is_last branch, so they issue after it
+    // returned. The C++ model would want an acquire-release ticket instead,
+    // but at agent scope that is a buffer_wbl2 + buffer_inv pair per
+    // workgroup, which measured +80 us (B = 4) and +120 us (B = 16) on the
+    // Llama-3.1-8B decode step (3-4 us per launch); the GPU tests hold this
+    // launch bit-identical to the separate partials-plus-norm path, on two
+    // calls in a row.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {

@@ -95,7 +95,7 @@ class HostStagedHandoff:
             # end of the last run's scatters (a later run's host zeros may not
             # land where those scatters still read).
             self.ev_layer = EventArray(n_layers)
-            self.ev_read = EventArray(1, PDK_EVENT_SYNC)
+            self.ev_read = EventArray(2, PDK_EVENT_SYNC)
         else:
             # Per request: its pack, each of its down copies (at most one K
             # and one V copy per layer), its last up copy; and the run's last
@@ -103,7 +103,7 @@ class HostStagedHandoff:
             self.ev_pack = EventArray(max_requests)
             self.ev_down = EventArray(2 * max_requests * n_layers)
             self.ev_up = EventArray(max_requests)
-            self.ev_read = EventArray(1, PDK_EVENT_SYNC)
+            self.ev_read = EventArray(2, PDK_EVENT_SYNC)
             shape = (max_requests, n_layers, 2, self.F)
             self.out_frames = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
             self.in_frames = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
@@ -111,6 +111,11 @@ class HostStagedHandoff:
             raise ValueError(f"copy_bytes must be positive, got {copy_bytes}")
         self.copy_bytes = int(copy_bytes)
         self.slot_P = [None] * max_requests
+        # Run n records the end of its uploads (kernel mode: of its scatters)
+        # in ev_read[n % 2]; run n + 1's host thread waits on that one while
+        # the calling thread records ev_read[(n + 1) % 2], so the wait never
+        # lands on an event this run has re-recorded.
+        self.runs = 0
         self.host_threads = int(host_threads or min(8, os.cpu_count() or 1))
         # Two side streams per process at most (the hardware has four queues
         # per process, and the caller's stream is a third).
@@ -176,12 +181,13 @@ class HostStagedHandoff:
         # the last run's uploads first.
         lengths = [int(P) for _, _, P, _ in requests]
         wait = any(self.slot_P[r] is not None and lengths[r] < self.slot_P[r] for r in range(n))
+        prev, slot = (self.runs - 1) % 2, self.runs % 2
         errors = []
 
         def zero_tails():
             try:
-                if wait:
-                    self.ev_read.sync(0)
+                if wait:                    # a slot with a P is from an earlier run: runs >= 1
+                    self.ev_read.sync(prev)
                 for r, P in enumerate(lengths):
                     ok(lib.pdk_host_zero_frame_tail(ctypes.c_void_p(self.host_ptr(r)), L, H, D, S,
                                                     P, 64 if kernel else 16, self.host_threads),
@@ -195,9 +201,9 @@ class HostStagedHandoff:
             self.save_stream.wait_stream(cur)
             self.load_stream.wait_stream(cur)
             if kernel:
-                self._run_kernel(lib, ok, packs, scats, cache_k, cache_v, nb)
+                self._run_kernel(lib, ok, packs, scats, cache_k, cache_v, nb, slot)
             else:
-                self._run_dma(lib, ok, packs, scats, lengths, cache_k, cache_v, nb, cur)
+                self._run_dma(lib, ok, packs, scats, lengths, cache_k, cache_v, nb, cur, slot)
             cur.wait_stream(self.load_stream)
             cur.wait_stream(self.save_stream)
         finally:
@@ -206,8 +212,9 @@ class HostStagedHandoff:
             raise errors[0]
         for r, P in enumerate(lengths):
             self.slot_P[r] = P
+        self.runs += 1
 
-    def _run_kernel(self, lib, ok, packs, scats, cache_k, cache_v, nb):
+    def _run_kernel(self, lib, ok, packs, scats, cache_k, cache_v, nb, slot):
         # Layer by layer, all requests in one launch each way: 2 L launches
         # for the batch.
         L, S, H, D, n = self.L, self.S, self.H, self.D, len(packs)
@@ -218,7 +225,7 @@ class HostStagedHandoff:
                                            cache_k.stride(0), nb, self.ev_layer.ptr,
                                            self.load_stream.cuda_stream),
            "pdk_scatter_paged_layerwise")
-        ok(lib.pdk_event_record(self.ev_read[0], self.load_stream.cuda_stream),
+        ok(lib.pdk_event_record(self.ev_read[slot], self.load_stream.cuda_stream),
            "pdk_event_record")
 
     def layer_chunks(self, P):
@@ -238,7 +245,7 @@ class HostStagedHandoff:
             l0 += m
         return out
 
-    def _run_dma(self, lib, ok, packs, scats, lengths, cache_k, cache_v, nb, cur):
+    def _run_dma(self, lib, ok, packs, scats, lengths, cache_k, cache_v, nb, cur, slot):
         L, S, H, D = self.L, self.S, self.H, self.D
         st, save, load = cur.cuda_stream, self.save_stream.cuda_stream, self.load_stream.cuda_stream
         for r, pr in enumerate(packs):
@@ -260,7 +267,7 @@ class HostStagedHandoff:
                                                 PDK_COPY_H2D, part, load),
                        "pdk_copy_frame_valid (up)")
             ok(lib.pdk_event_record(self.ev_up[r], load), "pdk_event_record")
-        ok(lib.pdk_event_record(self.ev_read[0], load), "pdk_event_record")
+        ok(lib.pdk_event_record(self.ev_read[slot], load), "pdk_event_record")
         for r, sr in enumerate(scats):
             ok(lib.pdk_stream_wait_event(st, self.ev_up[r]), "pdk_stream_wait_event")
             ok(lib.pdk_scatter_paged_batch(ctypes.byref(sr), 1, L, S, H, D, cache_k.data_ptr(),

@@ -68,8 +68,10 @@ class ContinuousScheduler:
         self.admit_stall_ms = 0.0
         # (start on the monotonic clock, duration ms, streams) of each step
         # since the last take_step_log(): what a serving run correlates with
-        # other processes' work on the same GPU.
+        # other processes' work on the same GPU. The loop appends and
+        # take_step_log swaps under _log_lock, so no step is lost in between.
         self.step_log = []
+        self._log_lock = threading.Lock()
         # Step inputs: one pinned host block and its device copy, as int32
         # [tokens B | ctx B | tables B x max_blocks]; the step reads views of
         # the device copy, so a captured graph sees each step's values.
@@ -149,7 +151,8 @@ class ContinuousScheduler:
 
     def take_step_log(self):
         """The steps since the last call: [(start s, duration ms, streams)]."""
-        log, self.step_log = self.step_log, []
+        with self._log_lock:
+            log, self.step_log = self.step_log, []
         return log
 
     def _active(self):
@@ -299,8 +302,9 @@ class ContinuousScheduler:
                 dt = (time.perf_counter() - t1) * 1e3
                 self.lane_steps += len(live)
                 self.steps += 1
-                if len(self.step_log) < 1_000_000:
-                    self.step_log.append((t_mono, dt, len(live)))
+                with self._log_lock:
+                    if len(self.step_log) < 1_000_000:
+                        self.step_log.append((t_mono, dt, len(live)))
                 for row, i in enumerate(live):
                     s = self.slots[i]
                     s["steps"].append(dt)

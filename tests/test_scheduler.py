@@ -196,6 +196,7 @@ def test_step_log_is_taken_and_cleared():
     from rngd_pd_amd.serving.scheduler import ContinuousScheduler
     sched = ContinuousScheduler.__new__(ContinuousScheduler)
     sched.step_log = [(1.0, 2.0, 3)]
+    sched._log_lock = threading.Lock()
     assert sched.take_step_log() == [(1.0, 2.0, 3)]
     assert sched.take_step_log() == []
 
