@@ -7,15 +7,24 @@ lengths uniform in [64, 512] from seed 0), with the ms per 512-token request and
 decode_batch tokens/s alongside.
 
   handoff   (the value) the batch staged through pinned host memory as a
-            pipeline across requests: layer-wise pack stores each request's
-            S-wide frames straight into pinned host frames (save stream);
-            layer-wise scatter reads each layer's valid columns back from them
-            into the paged decode cache (block 16, seeded permuted block
-            table; load stream), waiting only for that layer's pack. A step is
-            one batch; handoff bytes = sum(P) * 131072 B. Beside it: the
-            device-only pack and scatter kernels (HBM roofline), the same
-            staging with DMA-engine copies, one 512-token request, KONI token
-            blocks and the host-link rates.
+            pipeline across requests ("dma" mode): each request is packed
+            narrow (valid columns) into a device frame; the DMA engines copy
+            its valid columns down into its pinned S-wide wire frame, a few
+            layers per copy, on a save stream and back up into a second device
+            frame on a load stream; host threads write the frames' zero tails;
+            one scatter per request places the frame in the paged decode cache
+            (block 16, seeded permuted block table). A step is one batch;
+            handoff bytes = sum(P) * 131072 B. The step is bound by the host
+            link (value_bound: its link bytes per second against this run's
+            both-ways DMA rate); its own kernels are timed under kernels.
+            Beside it: the device-only S-wide pack and scatter of the batch
+            (the HBM-bound kernels; roofline is that pack), the same staging
+            with the kernels' own loads and stores through pinned memory
+            ("kernel" mode), one 512-token request, KONI token blocks and the
+            host-link rates.
+  shm       the drop-in shm transport on the device path: RngdKVConnector on
+            select_transport("shm"), device save -> /dev/shm -> device load
+            into the paged cache, for one 512-token request and for the batch.
   decode    GQA decode attention, 32 layers x B streams at context 512, per-layer
             launches, eager and replayed from a HIP graph; B=16 at context 2048
             (context split in two + merge) from a graph.
@@ -35,6 +44,7 @@ import gc
 import json
 import math
 import os
+import shutil
 import statistics
 import sys
 import tempfile
@@ -58,11 +68,11 @@ def parse():
                     help="bound on the CPU baseline sample (0 skips it)")
     ap.add_argument("--only", default="all",
                     help="restrict the run (for profiler passes): all, or a comma-separated "
-                         "subset of handoff, decode, step, long, serve, copy")
+                         "subset of handoff, shm, decode, step, long, serve, copy")
     ap.add_argument("--copy-mib", type=int, default=1024,
                     help="bytes moved by --only copy (traffic-counter calibration)")
     args = ap.parse_args()
-    legs = {"all", "handoff", "decode", "step", "long", "serve", "copy"}
+    legs = {"all", "handoff", "shm", "decode", "step", "long", "serve", "copy"}
     args.legs = set(args.only.split(","))
     if not args.legs <= legs:
         ap.error(f"--only: unknown legs {sorted(args.legs - legs)}")
@@ -224,7 +234,11 @@ def bench_handoff(args, torch, K, lib, dev, out):
     dev_wall = (time.perf_counter() - t0) / args.steps
     pack_bytes = (tokens + n * S) * TOKEN_BYTES       # read valid tokens + write S-wide frames
     scat_bytes = 2 * tokens * TOKEN_BYTES             # read valid frame columns + write blocks
-    out["roofline"] = roofline(pack_bytes, timer.mean_s("pack"), measured_traffic("pack_kv_batch"))
+    out["roofline"] = dict(roofline(pack_bytes, timer.mean_s("pack"),
+                                    measured_traffic("pack_kv_batch")),
+                           kernel="pack_kv_batch: the 8 requests' S-wide frames in one launch, "
+                                  "device-only (HBM-bound); the timed step is host-link-bound "
+                                  "(value_bound) and its own kernels are under kernels")
     out["kernels"] = {"pack_kv_batch": out["roofline"],
                       "scatter_paged_batch": roofline(scat_bytes, timer.mean_s("scatter"),
                                                       measured_traffic("scatter_paged_batch"))}
@@ -234,6 +248,55 @@ def bench_handoff(args, torch, K, lib, dev, out):
     log(f"device batch: {handoff_bytes / dev_wall / 1e9:.1f} GB/s, pack "
         f"{timer.mean_s('pack') * 1e6:.1f} us, scatter {timer.mean_s('scatter') * 1e6:.1f} us")
     ref_k, ref_v = cache_k.clone(), cache_v.clone()
+
+    # -- the kernels the staged step itself runs -------------------------------
+    # The dma-mode step packs each request narrow (valid columns only) into a
+    # device frame and scatters each request from its uploaded frame: 8
+    # launches of each per step, timed here on device frames as one group per
+    # kind (events around the 8 launches, mean per launch).
+    from rngd_pd_amd._lib import PDK_PACK_NARROW
+    narrow = [PackReq(p.data_ptr(), p[:, 1].data_ptr(), f.data_ptr(), p.stride(0), p.stride(2),
+                      P, PDK_PACK_NARROW) for p, f, P in zip(prefill, frames, lengths)]
+    timer_n = Timer(torch, 4 * args.steps)
+    for i in range(args.warmup + args.steps):
+        if i >= args.warmup:
+            timer_n.begin("pack")
+        for r in range(n):
+            if lib.pdk_pack_kv_batch(ctypes.byref(narrow[r]), 1, L, S, H, D, st):
+                raise RuntimeError("narrow pack failed: " + lib.pdk_last_error().decode())
+        if i >= args.warmup:
+            timer_n.end("pack")
+            timer_n.begin("scatter")
+        for r in range(n):
+            if lib.pdk_scatter_paged_batch(ctypes.byref(scat[r]), 1, L, S, H, D,
+                                           cache_k.data_ptr(), cache_v.data_ptr(),
+                                           cache_k.stride(0), nb, st):
+                raise RuntimeError("scatter failed: " + lib.pdk_last_error().decode())
+        if i >= args.warmup:
+            timer_n.end("scatter")
+    torch.cuda.synchronize()
+    half = L * H * D * 2                                # one token of K (or V), all layers
+    narrow_bytes = sum(P * TOKEN_BYTES + (min((P + 63) // 64 * 64, S) + P) * half
+                       for P in lengths) / n
+    scat_req_bytes = scat_bytes / n
+    out["kernels"]["pack_kv_narrow_per_request"] = dict(
+        roofline(narrow_bytes, timer_n.mean_s("pack") / n),
+        what="pack_kernel on one request into a device frame, valid columns only (the staged "
+             "step's pack); mean per launch over the batch's 8 requests")
+    out["kernels"]["scatter_paged_per_request"] = dict(
+        roofline(scat_req_bytes, timer_n.mean_s("scatter") / n),
+        what="scatter_kernel of one request (the staged step's scatter); mean per launch")
+    log(f"staged step's kernels: narrow pack {timer_n.mean_s('pack') / n * 1e6:.1f} us, "
+        f"scatter {timer_n.mean_s('scatter') / n * 1e6:.1f} us per request")
+    torch.cuda.synchronize()
+    if not (torch.equal(cache_k.view(torch.int16), ref_k.view(torch.int16))
+            and torch.equal(cache_v.view(torch.int16), ref_v.view(torch.int16))):
+        raise RuntimeError("per-request scatters differ from the batched scatter")
+    # The narrow packs left the frames' tails as they were (the S-wide pack
+    # wrote zeros there); restore the S-wide frames for the checks below.
+    if lib.pdk_pack_kv_batch(pack, n, L, S, H, D, st):
+        raise RuntimeError("pack launch failed: " + lib.pdk_last_error().decode())
+    torch.cuda.synchronize()
 
     # -- config 2: staged through pinned host memory (value) ------------------
     reqs = [(p[:, 0], p[:, 1], P, t) for p, P, t in zip(prefill, lengths, tables)]
@@ -335,6 +398,134 @@ def bench_handoff(args, torch, K, lib, dev, out):
     both = out["extra"]["host_link"]["dma_both_ways_total_gbps"]
     for mode, row in staged.items():
         row["host_link_frac_of_dma_both_ways"] = round(row["host_link_gbps"] / both, 3)
+    # What bounds the timed step: the host link, both directions at once.
+    dma = staged["dma"]
+    out["value_bound"] = {
+        "bound": "host link", "unit": "GB/s",
+        "link_bytes_per_step": dma["host_link_bytes"], "achieved": dma["host_link_gbps"],
+        "ceiling": both, "ceiling_what": "64 MiB DMA copies down and up at once, this run",
+        "frac": dma["host_link_frac_of_dma_both_ways"],
+        "kernels": "pack_kv_narrow_per_request, scatter_paged_per_request (under kernels)"}
+
+
+def bench_shm(args, torch, K, dev, out):
+    """The drop-in shm transport on the device path, timed per request as the
+    reference times its shm handoff (bench/nixl_kv_check.py:211-221: save,
+    download, load of one request): RngdKVConnector on
+    select_transport("shm"), device save (pack on a side stream, pinned
+    staging, one ordered writer: tmp + fsync + rename per blob) -> /dev/shm
+    files (the reference's wire, byte for byte) -> device load (read into
+    pinned memory, copy up, scatter into the paged cache, files consumed).
+    One 512-token Llama-3.1-8B request (64 MiB on the wire), then the 8
+    requests of the handoff batch saved one after the other and loaded one
+    after the other. The files' payloads and the loaded cache are checked
+    against the device pack once, outside the timed loops."""
+    from rngd_pd_amd.connector import transport as kvt
+    from rngd_pd_amd.connector.rngd_kv import KVConnectorRole, RngdKVConnector
+    from rngd_pd_amd.connector.wire import decode_payload
+    from rngd_pd_amd.engines.paged_cache import PagedKVCache
+    lengths = workload()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    prefill = [torch.randn((L, 2, S, H, D), generator=gen, device=dev).to(torch.bfloat16)
+               for _ in lengths]
+    root = tempfile.mkdtemp(prefix="pd-shm-bench-", dir="/dev/shm" if os.path.isdir("/dev/shm")
+                            else None)
+    saved_env = {k: os.environ.get(k) for k in ("PD_SHM_ROOT", "AIRM_KV_TRANSPORT")}
+    os.environ["PD_SHM_ROOT"], os.environ["AIRM_KV_TRANSPORT"] = root, "shm"
+    kvt.reset_selection()
+    per = (S + BS - 1) // BS
+    cache = PagedKVCache(L, per * (len(lengths) + 1), H, D, device=dev)
+
+    def save(req, p, P):
+        c = RngdKVConnector(KVConnectorRole.WORKER, req_id=req, n_layers=L, frame_tokens=S)
+        for i in range(L):
+            c.save_kv_layer(f"layer.{i}", (p[i, 0], p[i, 1]), num_tokens=P)
+        c.wait_for_save()
+        c.close()
+
+    def load(req, P):
+        c = RngdKVConnector(KVConnectorRole.WORKER, req_id=req, n_layers=L)
+        c.register_kv_caches(cache.view(req, P, S))
+        c.start_load_kv()
+        for i in range(L):
+            c.wait_for_layer_load(f"layer.{i}")
+        c.close()
+        torch.cuda.synchronize()
+
+    try:
+        # Check: request 0's files hold the packed frame's bytes, and the
+        # load places exactly that frame.
+        P0 = lengths[0]
+        frame = K.pack_kv(prefill[0][:, 0], prefill[0][:, 1], P0, S)
+        torch.cuda.synchronize()
+        want = frame.view(torch.int16).cpu().numpy().view(np.uint16).reshape(L, 2, -1)
+        save("chk", prefill[0], P0)
+        for i in (0, L - 1):
+            for part, name in ((0, "k"), (1, "v")):
+                with open(os.path.join(root, f"chk__layer.{i}__{name}"), "rb") as f:
+                    got = decode_payload(f.read())
+                if not np.array_equal(got.reshape(-1), want[i, part]):
+                    raise RuntimeError(f"shm file layer {i} {name} differs from the packed frame")
+        load("chk", P0)
+        back = cache.read_frame("chk", P0, S)
+        torch.cuda.synchronize()
+        if not torch.equal(back.view(torch.int16), frame.view(torch.int16)):
+            raise RuntimeError("shm device load differs from the packed frame")
+        if os.listdir(root):
+            raise RuntimeError("the load left files behind")
+        cache.free("chk")
+
+        reps = max(5, min(args.steps, 20))
+        save_ms, load_ms = [], []
+        for i in range(max(1, args.warmup) + reps):
+            req = f"one{i}"
+            torch.cuda.synchronize()
+            a = time.perf_counter()
+            save(req, prefill[0], S)
+            b = time.perf_counter()
+            load(req, S)
+            c = time.perf_counter()
+            cache.free(req)
+            if i >= max(1, args.warmup):
+                save_ms.append((b - a) * 1e3)
+                load_ms.append((c - b) * 1e3)
+        sv, ld = statistics.median(save_ms), statistics.median(load_ms)
+        tot = statistics.median([x + y for x, y in zip(save_ms, load_ms)])
+        batch_ms = []
+        for i in range(max(1, args.warmup) + max(3, reps // 2)):
+            torch.cuda.synchronize()
+            a = time.perf_counter()
+            for r, (p, P) in enumerate(zip(prefill, lengths)):
+                save(f"b{i}r{r}", p, P)
+            for r, P in enumerate(lengths):
+                load(f"b{i}r{r}", P)
+            t = time.perf_counter() - a
+            for r in range(len(lengths)):
+                cache.free(f"b{i}r{r}")
+            if i >= max(1, args.warmup):
+                batch_ms.append(t * 1e3)
+        bt = statistics.median(batch_ms)
+        handoff = sum(lengths) * TOKEN_BYTES
+        out["extra"]["shm_device_path"] = {
+            "what": "RngdKVConnector on select_transport('shm'): device save -> /dev/shm -> "
+                    "device load into the paged cache (the reference's shm handoff per request)",
+            "ms_per_512_request": round(tot, 3), "save_ms": round(sv, 3), "load_ms": round(ld, 3),
+            "gbps_512_request": round(S * TOKEN_BYTES / tot / 1e6, 2),
+            "batch_ms": round(bt, 3), "batch_gbps": round(handoff / bt / 1e6, 2),
+            "batch_lengths": lengths, "reps": reps,
+            "files_and_cache_checked": True}
+        log(f"shm device path: 512-token request {tot:.2f} ms (save {sv:.2f}, load {ld:.2f}); "
+            f"8-request batch {bt:.1f} ms, {handoff / bt / 1e6:.2f} GB/s")
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+        for k, v in saved_env.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        kvt.reset_selection()
+        del prefill, cache
+        torch.cuda.empty_cache()
 
 
 def bench_host_link(args, torch, lib, dev, out, dframe):
@@ -973,6 +1164,8 @@ def main():
         return 0
     if args.legs & {"all", "handoff"}:
         bench_handoff(args, torch, K, lib, dev, out)
+    if args.legs & {"all", "shm"}:
+        bench_shm(args, torch, K, dev, out)
     if args.legs & {"all", "decode"}:
         bench_decode(args, torch, K, lib, dev, out)
         bench_decode_long(args, torch, K, dev, out)
