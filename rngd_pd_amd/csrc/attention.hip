@@ -99,15 +99,17 @@ __device__ __forceinline__ bool valid_block(int blk, int num_blocks) {
 // Issue every load of the 32-token span starting at `span`, whose tokens lie
 // in the blocks blk_lo (tokens span..span+15) and blk_hi (span+16..span+31).
 // kVStream: V with non-temporal loads (each V byte has one reader; K has one
-// per workgroup sharing the unit); k_nt: K too, for units whose K has two
+// per workgroup sharing the unit); kKnt: K too, for units whose K has two
 // readers (the two V halves).
 // Loads are unconditional from in-bounds addresses (an invalid block id reads
 // block 0) so they are all in flight together; V of tokens >= lim and of
 // invalid blocks is zeroed before use, K of tokens >= lim needs nothing (their
-// scores become -inf).
-template <int kNV, bool kVStream>
+// scores become -inf). live = false (wavefront-uniform): a span that is never
+// used, loaded only so that every path issues the same loads; each
+// instruction then reads one 16-byte piece of block 0 in all lanes.
+template <int kNV, bool kVStream, bool kKnt>
 __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, int g, int j,
-                                          int blk_lo, int blk_hi, Span& r, bool k_nt = false) {
+                                          int blk_lo, int blk_hi, Span& r, bool live = true) {
   // QK tile 0 row j is token span + 8(j/4) + j%4 and tile 1 row j that token
   // + 4: slots (j%8 -> j8 = j%8) of blk_lo for j < 8, of blk_hi otherwise. In
   // the tiled K block (pdk::k_unit) lanes j%8 = 0..7 of one dim group g read
@@ -117,10 +119,10 @@ __device__ __forceinline__ void load_span(const AttnArgs& a, int h, int span, in
   const int bv = (g < 2) ? blk_lo : blk_hi;
   const int cbk = valid_block(bk, a.num_blocks) ? bk : 0;
   const int cbv = valid_block(bv, a.num_blocks) ? bv : 0;
-  const uint16_t* pk = a.ck + ((int64_t)cbk * a.Hkv + h) * 16 * kD + (g * 8 + (j & 7)) * 8;
-  const uint16_t* pv = a.cv + ((int64_t)cbv * a.Hkv + h) * kD * 16 + (tv & 15) + j * 16;
+  const uint16_t* pk = a.ck + ((int64_t)cbk * a.Hkv + h) * 16 * kD + (live ? (g * 8 + (j & 7)) * 8 : 0);
+  const uint16_t* pv = a.cv + ((int64_t)cbv * a.Hkv + h) * kD * 16 + (live ? (tv & 15) + j * 16 : 0);
   // unit(t, s) = ((t * 4 + s) * 4 + g) * 8 + j8 with kD / 32 = 4 dim groups per tile
-  if (k_nt) {
+  if constexpr (kKnt) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       r.ka[s] = pdk::ld16_stream(pk + (s * 4 * 8) * 8);
@@ -381,7 +383,14 @@ __device__ __forceinline__ void attend_span(const AttnArgs& a, Span& r, const v8
 // ids and K/V loads, none of the arithmetic, one store per thread.
 // kAct: out in the decode step's tiled activation layout (pdk::act_at, row b,
 // column qh * D + d of Hq * D) instead of row-major [B][Hq][D].
-template <int kRope, int kNV, bool kAct = false>
+// kKnt: K with non-temporal loads (plain path and probe with V split in two
+// halves and the query heads not split, so the two halves are K's only
+// readers): B=16 8.37 -> 8.26 us per layer; with 4 or 8 readers no faster.
+// It is a template argument because a choice made at run time puts each K
+// load between two alternative instructions, and the compiler's wait counts
+// then ignore the loads on both sides of that choice: every K/V wait of the
+// wavefront became a wait for nearly all of its loads.
+template <int kRope, int kNV, bool kAct = false, bool kKnt = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_attn_kernel(
     const void* src, const uint16_t* ck, const uint16_t* cv, const int32_t* tables,
     const int32_t* ctx_lens, uint32_t hgw, uint32_t mb_b, int num_blocks, uint32_t st_ns,
@@ -412,9 +421,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // kernels, so it keeps ordinary loads.
   constexpr bool kVStream = kRope <= 0;
   const int qsplit = hgw >> 24;
-  // Streaming K as well when only the two V halves read it (query heads not
-  // split): B=16 8.37 -> 8.26 us per layer; with 4 or 8 readers no faster.
-  const bool knt = kRope <= 0 && kVS == 1 && qsplit == 0;
+  static_assert(!kKnt || (kRope <= 0 && kNV == 4), "non-temporal K only on the plain V-split path");
+  constexpr bool knt = kKnt;
   const int gs = qsplit + kVS;                   // log2 of the workgroups sharing a unit
   const int units = nsplit * a.Hkv * (int)(mb_b >> 16);
   const int wg = blockIdx.x, full = (units >> 3) << (3 + gs);
@@ -525,25 +533,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ctx = min(ctx_raw, a.max_blocks * 16);
   const int s_end = (split == a.nsplit - 1) ? ctx : min(ctx, s_begin + a.split_tokens);
   const int pos = ctx_raw - 1;                   // the new token (fused RoPE path)
-  // The first pair is peeled out of the loop: a split of up to 2*stride tokens
-  // (512 with 8 wavefronts) then runs straight-line, with its loads issued
-  // right behind the query loads instead of after a loop-header wait.
+  // Loads and waits. A wavefront's loads complete in order, and the compiler
+  // waits for a register with a count of the loads issued after it, taken
+  // over every path that reaches the wait. So no load of the span loop sits
+  // under a branch that a path around it could skip: on such a path fewer
+  // loads follow, and the wait before a span's first product would drain the
+  // next span's loads too (measured: waiting for 25 of a wavefront's 28 loads
+  // before its first product; without it, ctx 512, 32-layer graph, B=16 8.36
+  // -> 7.92 us per layer, B=8 6.84 -> 6.42, B=4 5.97 -> 5.60).
+  // The first two spans' loads are issued together, and in the span loop every
+  // refill is issued; a span without tokens is loaded as a dead span (one
+  // 16-byte piece of block 0 per instruction, see load_span).
   const bool active = sa0 < s_end;
   const int sb0 = sa0 + stride;
   const bool has_b0 = sb0 < s_end;
-  // With the fused RoPE both spans' loads are issued unconditionally, those of
-  // a span without tokens from block 0 (cached after its first read): every
-  // path then has the same loads in flight, so the RoPE phase's wait counts
-  // only the partial sums' loads instead of draining all of them. Without it
-  // the loads stay under the branch (measured 0.5 us per layer faster).
   Span ra0, rb0;
-  if constexpr (kRope > 0) {
-    load_span<kNV, kVStream>(a, h, sa0, g, j, active ? id0[0] : 0, active ? id0[1] : 0, ra0);
-    load_span<kNV, kVStream>(a, h, sb0, g, j, has_b0 ? id0[2] : 0, has_b0 ? id0[3] : 0, rb0);
-  } else if (active) {
-    load_span<kNV, kVStream>(a, h, sa0, g, j, id0[0], id0[1], ra0, knt);
-    if (has_b0) load_span<kNV, kVStream>(a, h, sb0, g, j, id0[2], id0[3], rb0, knt);
-  }
+  auto first_loads = [&]() {
+    load_span<kNV, kVStream, knt>(a, h, sa0, g, j, active ? id0[0] : 0, active ? id0[1] : 0, ra0,
+                                  active);
+    load_span<kNV, kVStream, knt>(a, h, sb0, g, j, has_b0 ? id0[2] : 0, has_b0 ? id0[3] : 0, rb0,
+                                  has_b0);
+  };
+  // With the fused RoPE a wavefront without tokens issues them too (the
+  // barrier after the rotation keeps every wavefront on one path up to it);
+  // on the other paths such a wavefront skips the loads and the spans at once.
+  if constexpr (kRope > 0) first_loads();
   if constexpr (kRope > 0) {
     // Second phase, while the first pair's K/V loads are in flight: add the
     // partials in split order, round to bf16 (the projection's output), rotate
@@ -615,27 +629,46 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // a time (ra, rb): while one is used the other's loads are in flight, and a
   // span's registers are refilled with the span two ahead as soon as it has
   // been used. The block ids of the next pair are read one pair ahead.
-  auto pair = [&](auto first_c, int sa, const int* cur, int* nxt, Span& ra, Span& rb) {
-    constexpr bool kFirst = decltype(first_c)::value;
-    const int sb = sa + stride, sc = sa + 2 * stride, sd = sa + 3 * stride;
-    if (sc < s_end) ids(sc, nxt);
-    if constexpr (kRope < 0) fold_span<kNV>(ra, o);
-    else attend_span<(kRope > 0), kNV>(a, ra, qv, sa, cur[0], cur[1], s_end, g, j, kFirst, m, lsum, o, nt);
-    if (sc < s_end) load_span<kNV, kVStream>(a, h, sc, g, j, nxt[0], nxt[1], ra, knt);
-    if (sb < s_end) {
-      if constexpr (kRope < 0) fold_span<kNV>(rb, o);
-      else attend_span<(kRope > 0), kNV>(a, rb, qv, sb, cur[2], cur[3], s_end, g, j, false, m, lsum, o, nt);
+  auto use = [&](auto first_c, Span& r, int s, int lo, int hi) {
+    if constexpr (kRope < 0) fold_span<kNV>(r, o);
+    else attend_span<(kRope > 0), kNV>(a, r, qv, s, lo, hi, s_end, g, j,
+                                       decltype(first_c)::value, m, lsum, o, nt);
+  };
+  // Spans sa and sa + stride with the span sa + 2 stride still to come: use
+  // both and refill both (the second refill dead when sa + 3 stride has no
+  // tokens).
+  auto pair = [&](auto first_c, int sa, const int* cur, int* nxt) {
+    const int sc = sa + 2 * stride, sd = sc + stride;
+    const bool has_d = sd < s_end;
+    ids(sc, nxt);
+    use(first_c, ra0, sa, cur[0], cur[1]);
+    load_span<kNV, kVStream, knt>(a, h, sc, g, j, nxt[0], nxt[1], ra0);
+    use(std::false_type{}, rb0, sa + stride, cur[2], cur[3]);
+    load_span<kNV, kVStream, knt>(a, h, sd, g, j, has_d ? nxt[2] : 0, has_d ? nxt[3] : 0, rb0, has_d);
+  };
+  // The last one or two spans, already in registers: no loads.
+  auto last = [&](auto first_c, int sa, const int* cur) {
+    use(first_c, ra0, sa, cur[0], cur[1]);
+    if (sa + stride < s_end) use(std::false_type{}, rb0, sa + stride, cur[2], cur[3]);
+  };
+  auto spans = [&]() {
+    if (sa0 + 2 * stride < s_end) {
+      int cur[4], nxt[4];
+      pair(std::true_type{}, sa0, id0, nxt);
+      int sa = sa0 + 2 * stride;
+      for (; sa + 2 * stride < s_end; sa += 2 * stride) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+        pair(std::false_type{}, sa, cur, nxt);
+      }
+      last(std::false_type{}, sa, nxt);
+    } else {
+      last(std::true_type{}, sa0, id0);
     }
-    if (sd < s_end) load_span<kNV, kVStream>(a, h, sd, g, j, nxt[2], nxt[3], rb, knt);
-    return sc;
   };
   if (active) {
-    int cur[4], nxt[4];
-    for (int sa = pair(std::true_type{}, sa0, id0, cur, ra0, rb0); sa < s_end;) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) nxt[i] = cur[i];
-      sa = pair(std::false_type{}, sa, nxt, cur, ra0, rb0);
-    }
+    if constexpr (kRope <= 0) first_loads();
+    spans();
   }
   const int64_t bq0 = (int64_t)b * a.Hq + qh0;
   if constexpr (kRope < 0) {
@@ -874,6 +907,16 @@ struct RopeIn {
   bool act = false;              // out in the tiled activation layout (pdk::act_at)
 };
 
+// The kernel for a plan: V in halves or whole, and on the plain path and the
+// probe non-temporal K when the two V halves are K's only readers.
+template <int kRope, bool kAct>
+auto attn_kernel_for(const Plan& p) {
+  if constexpr (kRope <= 0) {
+    if (p.vsplit && p.qsplit == 0) return decode_attn_kernel<kRope, 4, kAct, true>;
+  }
+  return p.vsplit ? decode_attn_kernel<kRope, 4, kAct, false> : decode_attn_kernel<kRope, 8, kAct, false>;
+}
+
 int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
                 int num_blocks, const int32_t* block_tables, int max_blocks,
                 const int32_t* ctx_lens, int max_ctx, int B, int n_q_heads, int n_kv_heads,
@@ -945,7 +988,7 @@ int launch_attn(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cach
   const void* src = rope.part ? static_cast<const void*>(rope.part) : static_cast<const void*>(a.q);
 #define PDK_ATTN_LAUNCH(R, A)                                                                   \
   do {                                                                                         \
-    const auto kern = p.vsplit ? decode_attn_kernel<R, 4, A> : decode_attn_kernel<R, 8, A>;    \
+    const auto kern = attn_kernel_for<R, A>(p);                                                \
     hipLaunchKernelGGL(kern, grid, block, lds, st, src, a.ck, a.cv, a.tables, a.ctx, hgw, mb_b, \
                        a.num_blocks, st_ns, a.scale_log2, a.out, a.ws_ml, a.ws_o,              \
                        rope.inv_freq, rope.ck_w, rope.cv_w, rope.ssq, rope.n_ssq, rope.eps);   \
