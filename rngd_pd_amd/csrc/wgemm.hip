@@ -130,6 +130,7 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   __shared__ float red[kWaves][kW][256];
   __shared__ float rms[kRowScale ? 64 : 1];
   __shared__ int is_last;
+  __shared__ uint64_t kbest[kArg ? 16 : 1][kArg ? kCols : 1];   // per row of a tile, per column tile
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
   const int n0 = blockIdx.x * 16 * kCols;
@@ -342,19 +343,32 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
       }
       if (kArg) {
         // The 16 lanes e .. e|15 hold one row's 16 columns of this tile: the
-        // best of them goes to keys[m] (an atomic only when it beats the
-        // value already there, so few of the workgroups write).
+        // best of them goes to LDS, and below the best of the workgroup's
+        // column tiles to keys[m].
         uint64_t key = ok ? argmax_key(h, n) : 0;
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) {
           const uint64_t other = __shfl_xor(key, o);
           key = other > key ? other : key;
         }
-        if ((e & 15) == 0 && ok) {
-          uint64_t* slot = keys + m;
-          if (key > __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-            __hip_atomic_fetch_max(slot, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if ((e & 15) == 0) kbest[(e >> 4) & 15][c] = key;
+      }
+    }
+    if constexpr (kArg) {
+      // One thread per row: the best key of the workgroup's columns goes to
+      // keys[m], with an atomic only when it beats the value already there
+      // (so few workgroups write). One device-scope round trip per row and
+      // workgroup instead of one per row and column tile: the lm_head at
+      // B = 16 went from 128 to 16 of them per workgroup.
+      __syncthreads();
+      const int mr = threadIdx.x, m = t * 16 + mr;
+      if (mr < 16 && m < B) {
+        uint64_t best = kbest[mr][0];
+#pragma unroll
+        for (int c = 1; c < kCols; ++c) best = kbest[mr][c] > best ? kbest[mr][c] : best;
+        uint64_t* slot = keys + m;
+        if (best > __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          __hip_atomic_fetch_max(slot, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
