@@ -19,8 +19,43 @@ def hipcc_command(out=OUT):
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              # Leading scalar kernel arguments arrive preloaded in SGPRs, so a
              # kernel's first loads need not wait for a kernarg read.
-             "-mllvm", "-amdgpu-kernarg-preload-count=16", "-o", out]
+             "-mllvm", "-amdgpu-kernarg-preload-count=16",
+             # Per-kernel register, scratch and occupancy report (checked below).
+             "-Rpass-analysis=kernel-resource-usage", "-o", out]
             + [os.path.join(_HERE, "csrc", s) for s in SOURCES])
+
+
+# Kernels of the handoff and attention paths: a lane's state must fit its
+# registers. A build in which any of them needs scratch (private) memory is
+# refused: a spill there once cost a serving step 2 ms unnoticed by every
+# correctness test. The decode-step GEMMs for more than 16 streams with wide
+# column groups do spill and are allowed (wgemm_kernel is not listed).
+NO_SCRATCH = ("decode_attn_kernel", "merge_kernel", "pack_kernel", "scatter_kernel",
+              "gather_kernel", "koni_scatter_kernel", "koni_gather_kernel")
+
+
+def resource_report(text):
+    """{mangled kernel name: {field: value}} from -Rpass-analysis=kernel-resource-usage."""
+    out, cur = {}, None
+    for ln in text.splitlines():
+        if "remark:" not in ln or "kernel-resource-usage" not in ln:
+            continue
+        body = ln.split("remark:", 1)[1].rsplit("[-Rpass-analysis", 1)[0].strip()
+        key, _, val = body.partition(":")
+        if key == "Function Name":
+            cur = out.setdefault(val.strip(), {})
+        elif cur is not None:
+            cur[key.strip()] = val.strip()
+    return out
+
+
+def scratch_kernels(report, names=NO_SCRATCH):
+    """(kernel, bytes per lane) of the listed kernels that use scratch memory."""
+    bad = []
+    for fn, fields in report.items():
+        if any(n in fn for n in names) and int(fields.get("ScratchSize [bytes/lane]", "0")) > 0:
+            bad.append((fn, int(fields["ScratchSize [bytes/lane]"])))
+    return bad
 
 
 def net_command(out=NET_OUT):
@@ -47,10 +82,18 @@ def build(verbose=False):
     tmp = OUT + ".tmp"
     r = subprocess.run(hipcc_command(tmp), stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                        text=True)
-    # The host pass warns that it does not know the packed-fp32 feature; nothing else is expected.
-    noise = [ln for ln in r.stdout.splitlines() if "packed-fp32-ops" not in ln]
+    # The host pass warns that it does not know the packed-fp32 feature, and
+    # the resource remarks are read below; nothing else is expected.
+    noise = [ln for ln in r.stdout.splitlines()
+             if "packed-fp32-ops" not in ln and "kernel-resource-usage" not in ln
+             and not ln.lstrip().startswith(("|", "^")) and not ln.strip()[:1].isdigit()]
     if r.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + "\n".join(noise))
+    bad = scratch_kernels(resource_report(r.stdout))
+    if bad:
+        os.remove(tmp)
+        raise RuntimeError("kernels that must keep their state in registers use scratch memory: "
+                           + ", ".join(f"{fn} ({n} bytes/lane)" for fn, n in bad))
     if verbose and noise:
         print("\n".join(noise))
     os.replace(tmp, OUT)

@@ -548,7 +548,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int sb0 = sa0 + stride;
   const bool has_b0 = sb0 < s_end;
   Span ra0, rb0;
-  auto first_loads = [&]() {
+  auto first_loads = [&]() __attribute__((always_inline)) {
     load_span<kNV, kVStream, knt>(a, h, sa0, g, j, active ? id0[0] : 0, active ? id0[1] : 0, ra0,
                                   active);
     load_span<kNV, kVStream, knt>(a, h, sb0, g, j, has_b0 ? id0[2] : 0, has_b0 ? id0[3] : 0, rb0,
@@ -629,7 +629,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // a time (ra, rb): while one is used the other's loads are in flight, and a
   // span's registers are refilled with the span two ahead as soon as it has
   // been used. The block ids of the next pair are read one pair ahead.
-  auto use = [&](auto first_c, Span& r, int s, int lo, int hi) {
+  auto use = [&](auto first_c, Span& r, int s, int lo, int hi) __attribute__((always_inline)) {
     if constexpr (kRope < 0) fold_span<kNV>(r, o);
     else attend_span<(kRope > 0), kNV>(a, r, qv, s, lo, hi, s_end, g, j,
                                        decltype(first_c)::value, m, lsum, o, nt);
@@ -637,7 +637,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Spans sa and sa + stride with the span sa + 2 stride still to come: use
   // both and refill both (the second refill dead when sa + 3 stride has no
   // tokens).
-  auto pair = [&](auto first_c, int sa, const int* cur, int* nxt) {
+  auto pair = [&](auto first_c, int sa, const int* cur, int* nxt) __attribute__((always_inline)) {
     const int sc = sa + 2 * stride, sd = sc + stride;
     const bool has_d = sd < s_end;
     ids(sc, nxt);
@@ -647,11 +647,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     load_span<kNV, kVStream, knt>(a, h, sd, g, j, has_d ? nxt[2] : 0, has_d ? nxt[3] : 0, rb0, has_d);
   };
   // The last one or two spans, already in registers: no loads.
-  auto last = [&](auto first_c, int sa, const int* cur) {
+  auto last = [&](auto first_c, int sa, const int* cur) __attribute__((always_inline)) {
     use(first_c, ra0, sa, cur[0], cur[1]);
     if (sa + stride < s_end) use(std::false_type{}, rb0, sa + stride, cur[2], cur[3]);
   };
-  auto spans = [&]() {
+  auto spans = [&]() __attribute__((always_inline)) {
     if (sa0 + 2 * stride < s_end) {
       int cur[4], nxt[4];
       pair(std::true_type{}, sa0, id0, nxt);
@@ -666,9 +666,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       last(std::true_type{}, sa0, id0);
     }
   };
+  // The fused RoPE path keeps a loop whose refills are conditional: its first
+  // pair's loads are issued before the rotation, so their waits are exact
+  // anyway, and with whole V (kNV = 8) the loop above needs more than the 256
+  // registers a lane has (it spilled; a serving step at contexts up to 1152,
+  // which use that shape, went from 3.07 to 5.1 ms).
+  auto pair_cond = [&](auto first_c, int sa, const int* cur, int* nxt) __attribute__((always_inline)) {
+    const int sb = sa + stride, sc = sa + 2 * stride, sd = sa + 3 * stride;
+    if (sc < s_end) ids(sc, nxt);
+    use(first_c, ra0, sa, cur[0], cur[1]);
+    if (sc < s_end) load_span<kNV, kVStream, knt>(a, h, sc, g, j, nxt[0], nxt[1], ra0);
+    if (sb < s_end) use(std::false_type{}, rb0, sb, cur[2], cur[3]);
+    if (sd < s_end) load_span<kNV, kVStream, knt>(a, h, sd, g, j, nxt[2], nxt[3], rb0);
+    return sc;
+  };
   if (active) {
-    if constexpr (kRope <= 0) first_loads();
-    spans();
+    if constexpr (kRope <= 0) {
+      first_loads();
+      spans();
+    } else {
+      int cur[4], nxt[4];
+      for (int sa = pair_cond(std::true_type{}, sa0, id0, cur); sa < s_end;) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) nxt[i] = cur[i];
+        sa = pair_cond(std::false_type{}, sa, nxt, cur);
+      }
+    }
   }
   const int64_t bq0 = (int64_t)b * a.Hq + qh0;
   if constexpr (kRope < 0) {
