@@ -859,11 +859,14 @@ void* device_scratch() {
 // wavefronts of 64 tokens each in flight. The context is split across
 // workgroups until about 256 of them (one per CU) exist, in splits of at least
 // min_split tokens, because a split costs the partial-result merge (an extra
-// launch): 1024 once B*Hkv alone reaches 128 workgroups, 512 from 32, 128
-// below. Measured per layer on MI355X, Hq=32, Hkv=8, ctx 512 (32-layer graph):
-// B=4 one split 7.7 us vs four 9.1 us, B=8 one 8.4 us vs two 10.6 us; cold
-// cache: B=16 one 10.5 us vs two 11.7 us, B=16 ctx 2048 two 28.9 us vs one
-// 32.3 us.
+// launch): 2048 once B*Hkv alone reaches 128 workgroups, 512 from 32, 128
+// below. Measured per layer on MI355X, Hq=32, Hkv=8 (32-layer graph), B=16:
+// ctx 1152 one split 14.85 us vs two 17.20, ctx 2048 one 24.02 vs two 25.47,
+// ctx 4096 two 45.1 vs one 47.2, ctx 8192 two 83.8 vs one 95.4; B=8 and B=4
+// at ctx 1152-4096: splits of 512 the fastest or within 4 % of it. (Before
+// the span loads were issued on every path, B=16 ctx 2048 was faster in two
+// splits, 28.9 vs 32.3 us, and the threshold was 1024: a decode step whose
+// tables hold 1152 tokens took 3.21 ms at ctx 512 instead of 3.01.)
 struct Plan {
   int nsplit, split_tokens;
   int qsplit;                    // log2 of the parts a unit's query heads are split in
@@ -887,7 +890,7 @@ constexpr int kTargetWorkgroups = 256;
 // a decoder keeps it fixed across steps), the sharing for the B launched.
 Plan plan_for(int B, int plan_B, int Hkv, int G, int max_ctx) {
   const int64_t pairs = (int64_t)plan_B * Hkv;
-  const int min_split = pairs >= 128 ? 1024 : pairs >= 32 ? 512 : 128;
+  const int min_split = pairs >= 128 ? 2048 : pairs >= 32 ? 512 : 128;
   int64_t nsplit = (kTargetWorkgroups + pairs - 1) / pairs;
   nsplit = std::min<int64_t>(nsplit, (max_ctx + min_split - 1) / min_split);
   nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, kMaxSplits));

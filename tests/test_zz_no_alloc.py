@@ -72,15 +72,26 @@ def test_noalloc_matches_workspace_entry_point(cuda):
 
 
 def test_noalloc_refuses_more_than_its_scratch(cuda):
-    """255 streams of one KV head with 16 query heads at context 2048 split in two:
-    4.2 MB of partials, more than the array holds. Refused before any launch."""
+    """255 streams of one KV head with 16 query heads at context 4096 split in two:
+    4.2 MB of partials, more than the array holds. Refused before any launch.
+    Every buffer is sized for the call (one cache block, every table entry 0), so
+    the call would stay in bounds even if a later launch plan did not refuse it."""
     from rngd_pd_amd import _lib
     lib = _lib.lib()
-    B, Hq, H, D, max_ctx = 255, 16, 1, 128, 2048
-    dummy = torch.zeros(64, dtype=torch.bfloat16, device=cuda)
-    rc = lib.pdk_decode_attn_noalloc(dummy.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), 1,
-                                     dummy.data_ptr(), max_ctx // 16, dummy.data_ptr(), max_ctx,
-                                     B, Hq, H, D, 0.1, dummy.data_ptr(),
+    B, Hq, H, D, max_ctx = 255, 16, 1, 128, 4096
+    max_blocks = max_ctx // 16
+    q = torch.zeros((B, Hq, D), dtype=torch.bfloat16, device=cuda)
+    ck = torch.zeros((1, H, 16, D), dtype=torch.bfloat16, device=cuda)
+    cv = torch.zeros((1, H, D, 16), dtype=torch.bfloat16, device=cuda)
+    tables = torch.zeros((B, max_blocks), dtype=torch.int32, device=cuda)
+    ctx = torch.full((B,), max_ctx, dtype=torch.int32, device=cuda)
+    out = torch.zeros((B, Hq, D), dtype=torch.bfloat16, device=cuda)
+    need = B * Hq * 2 * (D + 2) * 4                      # partials of two splits
+    assert need > 4 << 20                                # PDK_NOALLOC_SCRATCH_BYTES
+    rc = lib.pdk_decode_attn_noalloc(q.data_ptr(), ck.data_ptr(), cv.data_ptr(), 1,
+                                     tables.data_ptr(), max_blocks, ctx.data_ptr(), max_ctx,
+                                     B, Hq, H, D, 0.1, out.data_ptr(),
                                      torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
     assert rc == _lib.PDK_ENOMEM, (rc, lib.pdk_last_error())
     assert b"no-allocation" in lib.pdk_last_error()
