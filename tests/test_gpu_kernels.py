@@ -175,6 +175,12 @@ def _attn_case(rng, B, Hq, H, ctx, D=128):
     # unit) and 16 ways (32 per unit)
     (1, 64, 8, [200]),
     (2, 32, 2, [16, 1]),
+    # 128 (stream, KV head) units: one context split up to 2048 tokens (ragged
+    # lengths on the whole-context path), then two splits past it
+    (16, 32, 8, [2048, 1, 1999, 17, 512, 1024, 2047, 33, 700, 1500, 64, 2000, 129, 900,
+                 1800, 5]),
+    (16, 32, 8, [3000, 2049, 1, 2048, 100, 2500, 64, 999, 1234, 3000, 7, 2100, 1600, 800,
+                 2999, 40]),
 ])
 def test_decode_attention_vs_fp32(cuda, B, Hq, H, ctx):
     from rngd_pd_amd.kernels import decode_attention
