@@ -156,6 +156,24 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
     xp[t] = kAct ? x + (int64_t)(row >> 4) * 16 * K + (kg * 16 + (row & 15)) * 8
                  : x + (int64_t)row * K + kg * 8;
   }
+  // The residual under this thread's epilogue element (at most one per row
+  // tile when the workgroup's columns fit one pass of its threads), loaded
+  // before any weight from a clamped address, so every lane loads and the
+  // weights' waits stay exact: the epilogue then adds it without a round trip
+  // to memory after the products. y may be the residual itself (in place);
+  // only this thread writes that element, and only after this read.
+  constexpr bool kResPre =
+      (kEpi == kResidual || kEpi == kResidualSsq) && 256 * kCols <= kWaves * 64;
+  uint16_t rpre[kResPre ? kTiles : 1];
+  if constexpr (kResPre) {
+    const int e = min((int)threadIdx.x, 256 * kCols - 1);
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+      const int m = min(t * 16 + ((e >> 4) & 15), B - 1);
+      const int n = min(n0 + 16 * (e >> 8) + (e & 15), N - 1);
+      rpre[t] = r[kAct ? pdk::act_at(m, n, N) : (int64_t)m * N + n];
+    }
+  }
 
   f32x4 acc[kW][kTiles];
 #pragma unroll
@@ -323,7 +341,11 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
         continue;
       }
       float out = v[0];
-      if ((kEpi == kResidual || kEpi == kResidualSsq) && ok) out += pdk::bf16_to_f32(r[at]);
+      if constexpr (kResPre) {
+        if (ok) out += pdk::bf16_to_f32(rpre[t]);          // e == threadIdx.x here
+      } else if ((kEpi == kResidual || kEpi == kResidualSsq) && ok) {
+        out += pdk::bf16_to_f32(r[at]);
+      }
       if (kEpi == kSwiGLU) out = v[0] / (1.f + expf(-v[0])) * v[kPairs - 1];
       if (kEpi == kSwiGLURms) {
         const float s = rms[m < 64 ? m : 63];
