@@ -863,7 +863,9 @@ void* device_scratch() {
 // below. Measured per layer on MI355X, Hq=32, Hkv=8 (32-layer graph), B=16:
 // ctx 1152 one split 14.85 us vs two 17.20, ctx 2048 one 24.02 vs two 25.47,
 // ctx 4096 two 45.1 vs one 47.2, ctx 8192 two 83.8 vs one 95.4; B=8 and B=4
-// at ctx 1152-4096: splits of 512 the fastest or within 4 % of it. (Before
+// at ctx 1152-4096: splits of 512 the fastest or within 4 % of it; at ctx 512
+// one split: B=4 5.60 us against 7.22-7.87 in splits of 256, 128 or 64 tokens,
+// B=8 6.19 against 8.46-8.79. (Before
 // the span loads were issued on every path, B=16 ctx 2048 was faster in two
 // splits, 28.9 vs 32.3 us, and the threshold was 1024: a decode step whose
 // tables hold 1152 tokens took 3.21 ms at ctx 512 instead of 3.01.)
