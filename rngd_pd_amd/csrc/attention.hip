@@ -670,7 +670,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // pair's loads are issued before the rotation, so their waits are exact
   // anyway, and with whole V (kNV = 8) the loop above needs more than the 256
   // registers a lane has (it spilled; a serving step at contexts up to 1152,
-  // which use that shape, went from 3.07 to 5.1 ms).
+  // split in two then and so run with whole V, went from 3.07 to 5.1 ms).
   auto pair_cond = [&](auto first_c, int sa, const int* cur, int* nxt) __attribute__((always_inline)) {
     const int sb = sa + stride, sc = sa + 2 * stride, sd = sa + 3 * stride;
     if (sc < s_end) ids(sc, nxt);
