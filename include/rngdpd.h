@@ -396,11 +396,13 @@ int pdk_linear_argmax(const uint16_t* x, const uint16_t* w, int B, int K, int N,
 
 /* Tiled weights: the four GEMMs above also take w as a tiled copy, written
  * once (at weight load) by pdk_weight_tile, in which every 16-row x 128-column
- * block is contiguous in the order the kernels' load instructions read it, so
- * that the weight stream is read linearly. The copy holds
+ * block is contiguous in the order the kernels' load instructions read it,
+ * and the blocks are step-major (the first 128 columns of every 16-row tile,
+ * then the next 128), so that the workgroups running together read one
+ * region of memory. The copy holds
  * pdk_weight_tiled_elems(N, K) = ceil(N/16)*16*K bf16 (rows >= N zero):
  * element ((c*4 + kg)*16 + col)*8 + e of block (t, s), which starts at
- * (t*(K/128) + s)*2048, is w[16t + col][128s + 32c + 8kg + e]. A gate|up
+ * (s*ceil(N/16) + t)*2048, is w[16t + col][128s + 32c + 8kg + e]. A gate|up
  * weight [2M][K] is tiled as one matrix and needs M % 16 == 0. Results are
  * bit-identical to the [out][in] entry points. No reference counterpart: the
  * reference's weights stay in their torch layout (engines/decode_batch.py:

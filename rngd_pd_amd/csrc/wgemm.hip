@@ -27,10 +27,18 @@
 // in which the 4 KiB that a wavefront reads for one 16-column tile and one
 // 128-long k step are contiguous, in the order the lanes read them: each load
 // instruction then reads 1 KiB of consecutive bytes instead of 64 bytes of
-// each of 16 rows, and a workgroup streams its columns' weights linearly.
-//   tile t = rows 16t .. 16t+15 (rows >= N zero), K/128 step blocks of 2048
-//   elements each; element ((c * 4 + kg) * 16 + col) * 8 + e of step block s
-//   is W[16t + col][128 s + 32 c + 8 kg + e].
+// each of 16 rows.
+//   tile t = rows 16t .. 16t+15 (rows >= N zero); block (t, s) holds its k
+//   step s (2048 elements) and starts at (s * tiles + t) * 2048; element
+//   ((c * 4 + kg) * 16 + col) * 8 + e of it is W[16t + col][128 s + 32 c +
+//   8 kg + e].
+// The blocks are step-major: the workgroups of a launch advance through K
+// together, so at any time they read one region a few MiB wide instead of a
+// separate run per column tile spread over the whole matrix (HBM serves the
+// former faster). Tile-major, each column tile's K contiguous, the decode step
+// of Llama-3.1-8B took 2.985-2.988 ms at B = 16 and 2.855-2.857 at B = 4;
+// step-major 2.929-2.932 and 2.796-2.809 (three alternating runs of each on
+// one box, bit-identical results).
 //
 // Tiled activations. The _xt entry points take the decode step's bf16
 // activations (x, the residual and the output y) in the tiled layout of
@@ -63,6 +71,7 @@ __device__ __forceinline__ f32x4 mfma(const v8& a, const v8& b, f32x4 c) {
 
 constexpr int kStepK = 128;        // k per wave step: 4 MFMA of 32
 constexpr int kWaves = 8;
+constexpr int kBlock = 16 * kStepK;  // tiled W: one tile's k step, 4 KiB
 
 // kResidualSsq: kResidual that also writes, per 16-column tile and row, the
 // sum of squares of the bf16 outputs (ssq[row][tile]): the raw material of the
@@ -136,13 +145,16 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   const int n0 = blockIdx.x * 16 * kCols;
   const uint16_t* wp[kW];
   const int n_tiles = (N + 15) >> 4;
+  // Tiled W is step-major: k step s of every tile (gate and up tiles for
+  // SwiGLU), then step s + 1.
+  const int64_t step_stride = (int64_t)kPairs * n_tiles * kBlock;
 #pragma unroll
   for (int p = 0; p < kPairs; ++p)
 #pragma unroll
     for (int c = 0; c < kCols; ++c) {
       if (kTiled)   // tile of columns n0 + 16c (the last one past N), rows of pair p after it
         wp[p * kCols + c] =
-            w + ((int64_t)p * n_tiles + min((n0 >> 4) + c, n_tiles - 1)) * 16 * K + lane * 8;
+            w + ((int64_t)p * n_tiles + min((n0 >> 4) + c, n_tiles - 1)) * kBlock + lane * 8;
       else
         wp[p * kCols + c] = w + ((int64_t)p * N + min(n0 + 16 * c + col, N - 1)) * K + kg * 8;
     }
@@ -191,9 +203,8 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   const int s_hi = (int)((int64_t)(blockIdx.y + 1) * steps_all / splits);
   const int steps = s_hi - s_lo;
   // Steps of this wave: wave, wave + kWaves, ... (so the workgroup's waves
-  // read consecutive k blocks together; with tiled weights that is one
-  // contiguous 32 KiB run per column tile). Each wave's share, and so the
-  // order of the fp32 sums, is the same for both weight layouts.
+  // read consecutive k blocks together). Each wave's share, and so the order
+  // of the fp32 sums, is the same for both weight layouts.
   const int first = wave;
   const int n_mine = steps > wave ? (steps - wave + kWaves - 1) / kWaves : 0;
   constexpr int stride = kWaves;
@@ -205,7 +216,7 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
     for (int q = 0; q < kW; ++q)
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        wv[slot][q][c] = kTiled ? pdk::ld16_stream(wp[q] + (int64_t)k * 16 + 512 * c)
+        wv[slot][q][c] = kTiled ? pdk::ld16_stream(wp[q] + (k / kStepK) * step_stride + 512 * c)
                                 : pdk::ld16(wp[q] + k + 32 * c);
 #pragma unroll
     for (int t = 0; t < kTiles; ++t)
@@ -517,10 +528,10 @@ __global__ void weight_tile_kernel(const uint16_t* __restrict__ w, int N, int K,
   if (gi >= groups) return;
   const int lane = (int)(gi & 63);                   // (kg, col) = (lane >> 4, lane & 15)
   const int c = (int)((gi >> 6) & 3);
-  const int64_t blk = gi >> 8;                       // step block: tile * (K / 128) + step
-  const int steps = K / kStepK;
-  const int64_t t = blk / steps;
-  const int s = (int)(blk - t * steps);
+  const int64_t blk = gi >> 8;                       // block: step * tiles + tile
+  const int64_t n_t = (N + 15) / 16;
+  const int s = (int)(blk / n_t);
+  const int64_t t = blk - (int64_t)s * n_t;
   const int64_t row = t * 16 + (lane & 15);
   v8 v = pdk::zero8();
   if (row < N) v = pdk::ld16(w + row * K + s * kStepK + 32 * c + 8 * (lane >> 4));

@@ -161,8 +161,10 @@ def swiglu(gate_up, out=None, stream=None):
 
 class TiledWeight:
     """A weight [N, K] in the tiled layout of pdk_weight_tile: every 16-row x
-    128-column block contiguous, in the order the GEMM kernels read it, so the
-    weight stream is read linearly. ``data`` is the flat bf16 device tensor;
+    128-column block contiguous, in the order the GEMM kernels read it, and the
+    blocks step-major (the first 128 columns of every 16-row tile, then the
+    next 128), so the workgroups of a launch read one region of memory at a
+    time. ``data`` is the flat bf16 device tensor;
     ``shape`` is the (N, K) of the weight it was made from. The GEMM wrappers
     below take it wherever they take a [N, K] weight, with identical results."""
 

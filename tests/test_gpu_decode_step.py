@@ -603,13 +603,14 @@ def test_linear_argmax(cuda, B, K, N):
 
 def _tiled_layout(w):
     """The documented tiled layout of a [N, K] weight, by reshapes: block (t, s)
-    element ((c*4 + kg)*16 + col)*8 + e = w[16t + col][128s + 32c + 8kg + e]."""
+    starts at (s * ceil(N/16) + t) * 2048 (step-major), and its element
+    ((c*4 + kg)*16 + col)*8 + e = w[16t + col][128s + 32c + 8kg + e]."""
     N, K = w.shape
     nt = (N + 15) // 16
     pad = np.zeros((nt * 16, K), w.dtype)
     pad[:N] = w
     v = pad.reshape(nt, 16, K // 128, 4, 4, 8)            # t, col, s, c, kg, e
-    return np.ascontiguousarray(v.transpose(0, 2, 3, 4, 1, 5)).reshape(-1)
+    return np.ascontiguousarray(v.transpose(2, 0, 3, 4, 1, 5)).reshape(-1)
 
 
 @pytest.mark.parametrize("N,K", [(16, 128), (1000, 256), (7, 128), (6144, 4096), (128256, 128)])
