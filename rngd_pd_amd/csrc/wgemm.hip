@@ -671,11 +671,11 @@ int linear_splitk_final(const uint16_t* x, const uint16_t* w, int B, int K, int 
   // projection: 128 x 2 workgroups, 7 steps per wave) rather than four with
   // four splits (28 steps per workgroup: waves 0-3 take 4 and waves 4-7 take 3):
   // the decode step B=4 2.890 -> 2.848 ms, B=16 3.100 -> 3.097 in one process.
-  // One tile per workgroup without a split (the residual epilogue of
-  // pdk_linear_ssq, no partials) is faster at B=4 but slower at B=16, where
-  // x's loads are as many bytes as the weights: with tiled activations, step
-  // B=4 2.828 -> 2.784 ms, B=16 2.995 -> 3.000 (one process, 32-layer graph).
-  // The choice cannot follow B: a row's sums must not depend on the batch.
+  // One tile per workgroup without a split (pdk_linear_ssq, no partials) was
+  // faster at B=4 but slower at B=16, where x's loads are as many bytes as
+  // the weights, until the tiled weights became step-major; since then it is
+  // as fast at B=16 and faster at B=4, and the decode step uses it for the
+  // down projection.
   if (N >= 1024)
     return launch_cols<2, kPartialFinal, kTiled, kAct>(x, w, B, K, N, residual, residual, nullptr, st,
                                                  partials, splits, ssq, 0, 0.f, counters);

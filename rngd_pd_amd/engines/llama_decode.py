@@ -16,9 +16,7 @@ layer, one launch per line:
   k, v into the paged cache; ao = attention        pdk_decode_attn_rope (+ its merge when split)
   x = x + ao . Wo^T; ssq                            pdk_linear_ssq, residual fused
   a = silu(r g) * (r u), [g; u] = x . (Wgu diag g2)^T  pdk_linear_swiglu_rms
-  x = x + a . Wd^T; ssq                             pdk_linear_splitk_final: split over K, the last
-                                                    split of each column group adds the partials
-                                                    to x in split order and writes that group's ssq
+  x = x + a . Wd^T; ssq                             pdk_linear_ssq, residual fused
 
 before the first layer pdk_embed_ssq gathers the embedding rows and writes
 their ssq, and after the last the lm_head GEMM (weights folded with the final
@@ -167,14 +165,14 @@ class LlamaDecoder:
         self.logits = e(B, cfg.vocab)
         self.tokens = torch.empty(B, dtype=torch.int32, device=dev)
         self.keys = torch.zeros(B, dtype=torch.int64, device=dev)    # argmax scratch, kept zero
-        # The down projection runs split over K (its 14336-long rows) into fp32
-        # partial sums, which its last-arriving split adds to the residual:
-        # enough splits for about 256 workgroups of 32 columns (16 below
-        # hidden 1024). The count follows the model's shape alone, never B,
-        # so a row's sums do not depend on the batch.
-        groups = (H + 31) // 32 if H >= 1024 else (H + 15) // 16
-        self.down_splits = max(1, min(8, cfg.inter // 128, -(-256 // groups)))
-        self.part = torch.empty((self.down_splits, B, H), dtype=torch.float32, device=dev)
+        # The down projection (K = 14336 at 8B) runs as the O projection does:
+        # one workgroup per 16 columns over all of K, residual and sums of
+        # squares in its epilogue. Split over K in two with 32 columns per
+        # workgroup (pdk_linear_splitk_final: half the activation re-reads,
+        # and the last split of each column group adds the partials) the
+        # 8B step took as long at B = 16 (2.923-2.925 against 2.920-2.927 ms)
+        # and 34 us longer at B = 4 (2.767-2.770 against 2.733-2.738), in one
+        # process with step-major tiled weights.
         # The q|k|v projection (N = 6144 at 8B) splits K in two when every wave
         # of the GEMM still gets two 128-long steps of each half: 2 x 96 wide
         # workgroups instead of 384 narrow ones, which re-read x per 16
@@ -186,11 +184,9 @@ class LlamaDecoder:
         # the O projection for the post-attention norm (fused into gate|up),
         # and by the down projection (pdk_embed_ssq before layer 0) for the
         # pre-attention norm (fused into attention) and the final one (into
-        # the lm_head). The down projection's split counters start at zero
-        # and every call leaves them so.
+        # the lm_head).
         self.ssq = torch.zeros((B, H // 16), dtype=torch.float32, device=dev)
         self.ssq_a = torch.zeros((B, H // 16), dtype=torch.float32, device=dev)
-        self.counters = torch.zeros(max(1, H // 16), dtype=torch.int32, device=dev)
         self.inv = cfg.inv_freq().to(dev)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
         self._ws = None
@@ -216,7 +212,7 @@ class LlamaDecoder:
         suffix = "_xt" if self.act_tiled else "_tiled" if self.tiled else ""
         self._gemm = {n: n + suffix for n in
                       ("pdk_linear_splitk_rms", "pdk_linear_ssq", "pdk_linear_swiglu_rms",
-                       "pdk_linear_splitk_final", "pdk_linear_argmax_rms")}
+                       "pdk_linear_argmax_rms")}
         self._gemm["pdk_embed_ssq"] = "pdk_embed_ssq_xt" if self.act_tiled else "pdk_embed_ssq"
         self._gemm["pdk_decode_attn_rope"] = ("pdk_decode_attn_rope_xt" if self.act_tiled
                                               else "pdk_decode_attn_rope")
@@ -291,16 +287,14 @@ class LlamaDecoder:
         aop, actp, inv = self.ao.data_ptr(), self.act.data_ptr(), self.inv.data_ptr()
         call = _lib.call
         g = self._gemm
-        lin_skr, lin_skf = g["pdk_linear_splitk_rms"], g["pdk_linear_splitk_final"]
+        lin_skr = g["pdk_linear_splitk_rms"]
         lin_ssq, lin_swr, lin_amr = (g["pdk_linear_ssq"], g["pdk_linear_swiglu_rms"],
                                      g["pdk_linear_argmax_rms"])
-        ssqp, ssqa, cntp, n_ssq = (self.ssq.data_ptr(), self.ssq_a.data_ptr(),
-                                   self.counters.data_ptr(), H // 16)
+        ssqp, ssqa, n_ssq = self.ssq.data_ptr(), self.ssq_a.data_ptr(), H // 16
         emb, attn = g["pdk_embed_ssq"], g["pdk_decode_attn_rope"]
         with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
             call(emb, w.embed.data_ptr(), cfg.vocab, tokens.data_ptr(),
                  tokens.element_size(), B, H, xp, ssqa, st)
-            partp, sp = self.part.data_ptr(), self.down_splits
             pqp, qs = self.part_qkv.data_ptr(), self.qkv_splits
             for wqkv, wo, wgu, wd, ck, cv in self._layers:
                 call(lin_skr, xp, wqkv, B, H, QKV, qs, ssqa, n_ssq, eps, pqp, st)
@@ -308,7 +302,7 @@ class LlamaDecoder:
                      B, NH, NKV, HD, self.scale, ws_ptr, ws_bytes, aop, self.plan_batch, st)
                 call(lin_ssq, aop, wo, B, NH * HD, H, xp, xp, ssqp, st)
                 call(lin_swr, xp, wgu, B, H, M, ssqp, n_ssq, eps, actp, st)
-                call(lin_skf, actp, wd, B, M, H, sp, partp, xp, ssqa, cntp, st)
+                call(lin_ssq, actp, wd, B, M, H, xp, xp, ssqa, st)
             call(lin_amr, xp, self._lm_head.data_ptr(), B, H, cfg.vocab, ssqa, n_ssq, eps,
                  self.logits.data_ptr(), self.keys.data_ptr(), self.tokens.data_ptr(), st)
         return self.tokens[:B]
