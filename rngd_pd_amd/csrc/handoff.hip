@@ -115,7 +115,11 @@ __device__ __forceinline__ int64_t wave_unit() {
 
 // Frame layout per request: [L][2][F], F = Hkv*D*S; K frame [Hkv][D][S],
 // V frame [Hkv][S][D]; columns t >= P are zero (engines/prefill_full.py:378-379).
-template <bool kStream>
+// kNarrow: some request of the launch is narrow (its V rows past P are not
+// stored). Without it every V store is unconditional: dropping the per-lane
+// test took the 8-request Llama-3.1-8B batch of full-width frames from
+// 146.0-146.3 to 141.6-142.1 us (both libraries in one process).
+template <bool kStream, bool kNarrow>
 __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
   const int64_t unit = wave_unit();
   const int64_t n_moving = a.off[a.n_req];
@@ -158,7 +162,7 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
   // Narrow frames still get whole 64-token tiles of K (zeros past P): a K row
   // then ends on a 128-byte line, which keeps the stores whole lines when the
   // frame is in host memory. V rows past P are left unwritten.
-  const bool narrow = (R.flags & PDK_PACK_NARROW) != 0;
+  const bool narrow = kNarrow && (R.flags & PDK_PACK_NARROW) != 0;
   uint16_t* fk = R.frame + (int64_t)(2 * l) * F;
   uint16_t* fv = fk + F;
 #pragma unroll
@@ -437,15 +441,17 @@ extern "C" int pdk_pack_kv_batch(const pdk_pack_req* reqs, int n_reqs, int n_lay
   PDK_REQUIRE(gx < (1ll << 31), "launch too large");
   // Bytes the launch moves: valid tokens read, frame columns written.
   int64_t moved = 0;
+  bool any_narrow = false;
   for (int i = 0; i < n_reqs; ++i) {
     const bool narrow = (a.req[i].flags & PDK_PACK_NARROW) != 0;
+    any_narrow = any_narrow || narrow;
     moved += (int64_t)n_layers * 2 * n_kv_heads * head_dim * 2 *
              (a.req[i].P + (int64_t)(narrow ? a.req[i].P : S));
   }
-  if (moved > kStreamBytes)
-    hipLaunchKernelGGL(pack_kernel<true>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
-  else
-    hipLaunchKernelGGL(pack_kernel<false>, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
+  const bool stream_io = moved > kStreamBytes;
+  const auto kern = stream_io ? (any_narrow ? pack_kernel<true, true> : pack_kernel<true, false>)
+                              : (any_narrow ? pack_kernel<false, true> : pack_kernel<false, false>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)gx), dim3(256), 0, pdk::as_stream(stream), a);
   return pdk::check_launch("pack_kernel");
 }
 
