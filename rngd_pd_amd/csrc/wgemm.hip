@@ -106,11 +106,18 @@ __device__ __forceinline__ uint64_t argmax_key(uint32_t h, int n) {
 }
 
 // Loads in flight per wave: kDepth steps of W (and X), no more than about 160
-// VGPRs of load buffers, and at most 4: with one column tile per workgroup
-// (the O projection, K = 4096: 4 steps per wave) every step's loads are in
-// flight at once. Measured on the Llama-8B decode step at B=16 (32-layer
-// graph): depth 2 -> 3.124 ms, 3 -> 3.119, 4 -> 3.095; at B=4 no change.
-constexpr int depth_for(int tiles) {
+// VGPRs of load buffers, and at most 4. With step-major tiled weights fewer
+// steps in flight pay at one row tile (B <= 16), measured on the Llama-3.1-8B
+// decode step (32-layer graph, three alternating runs of each on one box):
+// one column tile (the O and down projections) at depth 2 instead of 4, B=16
+// 2.931-2.933 -> 2.907-2.911 ms, B=4 2.772-2.774 -> 2.759-2.762 (depth 1: B=16
+// 2.915-2.921); q|k|v (3 column tiles) at depth 1 instead of 2, B=16
+// 2.906-2.911 -> 2.895-2.908, B=4 unchanged. Before the weights were
+// step-major, depth 4 had been the fastest for one column tile.
+constexpr int depth_for(int row_tiles, int w_tiles) {
+  if (row_tiles == 1 && w_tiles == 1) return 2;
+  if (row_tiles == 1 && w_tiles == 3) return 1;
+  const int tiles = row_tiles + w_tiles;
   return 160 / (16 * tiles) < 1 ? 1 : 160 / (16 * tiles) > 4 ? 4 : 160 / (16 * tiles);
 }
 
@@ -135,7 +142,7 @@ __global__ __launch_bounds__(kWaves * 64) void wgemm_kernel(const uint16_t* __re
   constexpr bool kArg = kEpi == kArgmax || kEpi == kArgmaxRms;
   constexpr int kPairs = kGLU ? 2 : 1;
   constexpr int kW = kPairs * kCols;                 // W tiles per step
-  constexpr int kDepth = depth_for(kTiles + kW);
+  constexpr int kDepth = depth_for(kTiles, kW);
   __shared__ float red[kWaves][kW][256];
   __shared__ float rms[kRowScale ? 64 : 1];
   __shared__ int is_last;
