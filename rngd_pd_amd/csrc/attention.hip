@@ -573,8 +573,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto put = [&](int r, float x0, float x1) {
       if (r <= G) {
         uint16_t* dst = r < G ? q_rot[r] : kv_new[0];
-        dst[lane] = (uint16_t)pdk::f32_to_bf16_rne(x0 * cs - x1 * sn);
-        dst[lane + 64] = (uint16_t)pdk::f32_to_bf16_rne(x1 * cs + x0 * sn);
+        float y0, y1;
+        pdk::rope_pair(x0, x1, cs, sn, y0, y1);
+        dst[lane] = (uint16_t)pdk::f32_to_bf16_rne(y0);
+        dst[lane + 64] = (uint16_t)pdk::f32_to_bf16_rne(y1);
       } else {
         kv_new[1][(r - G - 1) * 64 + lane] = (uint16_t)pdk::f32_to_bf16_rne(x0);
       }

@@ -170,7 +170,9 @@ __global__ void rope_append_kernel(const void* src_, int64_t ld, int64_t split_s
     const float a = bf(val(c0 + i)), c = bf(val(c0 + i + half));
     float s, co;
     sincosf((float)max(pos, 0) * inv_freq[i], &s, &co);
-    const uint16_t o0 = to_bf(a * co - c * s), o1 = to_bf(c * co + a * s);
+    float y0, y1;
+    pdk::rope_pair(a, c, co, s, y0, y1);
+    const uint16_t o0 = to_bf(y0), o1 = to_bf(y1);
     if (head < NH) {
       uint16_t* q = q_out + ((int64_t)b * NH + head) * HD;
       q[i] = o0;

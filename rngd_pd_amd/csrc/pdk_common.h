@@ -178,6 +178,17 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 
+// RoPE on one pair of dims (x0, x1) = (dim i, dim i + D/2) with cos c and sin
+// s: (x0 c - x1 s, x1 c + x0 s), each as one fused multiply-add on a rounded
+// product. Written out so that every kernel that rotates (the fused attention
+// and the separate cache append) rounds the same way whatever the compiler
+// would contract on its own: their outputs are compared bit for bit.
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float& y0,
+                                          float& y1) {
+  y0 = __builtin_fmaf(x0, c, -(x1 * s));
+  y1 = __builtin_fmaf(x1, c, x0 * s);
+}
+
 }  // namespace pdk
 
 #define PDK_TRY_HIP(call)                              \
