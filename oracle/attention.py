@@ -40,7 +40,7 @@ def k_block_index(D):
     The block is 16-byte units of 8 consecutive dims of one token; the unit of
     (slot, d // 8) is ((t * (D // 32) + d // 32) * 4 + (d // 8) % 4) * 8 + j8
     with t = (slot >> 2) & 1 and j8 = (slot >> 3) * 4 + (slot & 3). This is a
-    layout of this build, not of the reference (whose decode K is dense
+    layout of this package's paged cache, not of the reference (whose decode K is dense
     [nl, B, NKV, HD, S], engines/decode_batch.py:305-330)."""
     if D % 32:
         raise ValueError(f"head_dim {D} is not a multiple of 32")

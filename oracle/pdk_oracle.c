@@ -68,7 +68,7 @@ int orc_pack_kv(const uint16_t* src_k, const uint16_t* src_v, int64_t layer_stri
  * token `slot` (0..15) and dim d. The block is 16-byte units of 8 dims of one
  * token in tiled order: the unit of (slot, d/8) is
  * ((t*(D/32) + d/32)*4 + (d/8)%4)*8 + j8, t = (slot>>2)&1,
- * j8 = (slot>>3)*4 + (slot&3). A layout of this build (the reference keeps
+ * j8 = (slot>>3)*4 + (slot&3). A layout of this package's paged cache (the reference keeps
  * dense per-stream K, engines/decode_batch.py:305-330). Needs D % 32 == 0. */
 static int64_t k_index(int slot, int d, int D) {
   const int t = (slot >> 2) & 1, j8 = ((slot >> 3) << 2) | (slot & 3);

@@ -201,7 +201,7 @@ class NixlTransport(Transport):
     """Cross-device NIXL path: not part of this package; fails loudly, never falls back."""
 
     def __init__(self, *a, **kw):
-        raise NotImplementedError("NIXL transport is not available in this build; "
+        raise NotImplementedError("NIXL transport is not available in this package; "
                                   "use the shm transport (same host)")
 
     def push(self, key, buf):

@@ -12,7 +12,7 @@ complete reply, so the bytes each direction carried between two calls are that
 exchange's. Exchanges the client cannot produce (a push whose CRC is wrong)
 go through the same proxy from a raw socket. The fixture holds, per exchange,
 its name, what the client sent and what the relay answered (hex), in order,
-plus the blobs' seeds and sizes; it is data, and the GPU box never needs the
+plus the blobs' seeds and sizes; it is data, and no run of the tests needs the
 reference: the tests replay it against the native relay and client and against
 the oracle's protocol restatement.
 """
