@@ -2,8 +2,9 @@
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and
 ``bench.py``'s ``cpu_baseline`` leg may import anything under ``oracle/``, and
-only as the checker (or, for the baseline, as the timed CPU restatement of the
-reference). The product package ``rngd_pd_amd`` never imports it.
+only as the oracle results are compared with (or, for the baseline, as the
+timed CPU restatement of the reference). The product package ``rngd_pd_amd``
+never imports it.
 
 Modules:
   native     ctypes wrapper over liboracle.so (pdk_oracle.c): pack, scatter,

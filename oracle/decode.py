@@ -1,7 +1,7 @@
 """numpy restatement of the reference's full decode step -- TEST INFRASTRUCTURE.
 
 Only the tests, the smoke check and the CPU-baseline leg of the benchmark use
-this module, and only as the checker: no product path imports it.
+this module, and only as the oracle results are compared with: no product path imports it.
 
 Follows cpu_layer (kernels/decode_batch.py:124-162) for one layer of B streams
 at their own positions, ModelConfig.inv_freq (engines/model.py:32-50) for the

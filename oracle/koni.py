@@ -1,6 +1,6 @@
 """numpy restatement of the reference's KONI KV receiver -- TEST INFRASTRUCTURE.
 
-Only tests use this module, as the checker. It follows KVReceiver.accept
+Only tests use this module, as the oracle results are compared with. It follows KVReceiver.accept
 (native_v4/kv.py:47-120): the same checks, in the same order, and the same
 placement (tensor t = 2*layer + kind; K units land in keys[layer][h][d][tok],
 V units in values[layer][h][tok][d], bf16 bits widened to float32), on dense

@@ -2,7 +2,7 @@
  * CPU oracle for the KV handoff and decode attention -- TEST INFRASTRUCTURE.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load this library, and only as the checker. It is a plain-loop restatement
+ * load this library, and only as the oracle results are compared with. It is a plain-loop restatement
  * of what the reference computes, written for clarity, not speed.
  *
  * Layouts match include/rngdpd.h:

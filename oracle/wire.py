@@ -3,7 +3,7 @@
 Follows connector/transport.py:29-43 (ser/deser), :80-101 (ShmTransport file
 protocol), connector/rngd_kv.py:122-166 (save_kv_layer / wait_for_layer_load)
 and serving/cluster.py:438-467 (_load_kv_now: f32 zero buffers, per-layer
-load, unlink by prefix). It is both the byte-level checker for the product's
+load, unlink by prefix). It is both the byte-level oracle for the product's
 frame codec and, timed, the CPU baseline of the handoff.
 """
 import os
