@@ -371,6 +371,43 @@ def test_pack_narrow_leaves_tail(cuda):
     assert (kf[..., group_end:] == three).all() and (vf[:, :, P:] == three).all()
 
 
+def test_pack_batch_mixing_narrow_and_full_frames(cuda):
+    """One launch with a narrow request between two full-width ones (flags per
+    request through the C ABI): the full frames equal the oracle's, the narrow one
+    holds its valid columns and nothing past them."""
+    from rngd_pd_amd import _lib
+    from rngd_pd_amd._lib import PackReq
+    from rngd_pd_amd.kernels import frame_shape
+    rng = np.random.default_rng(23)
+    L, H, D, S = 2, 8, 128, 256
+    lengths, flags = [200, 37, 256], [0, _lib.PDK_PACK_NARROW, 0]
+    srcs = [_prefill(rng, L, S, H, D) for _ in lengths]
+    dev = [(to_dev(k), to_dev(v)) for k, v in srcs]
+    frames = [torch.full(frame_shape(L, H, D, S), 3.0, dtype=torch.bfloat16, device=cuda)
+              for _ in lengths]
+    reqs = (PackReq * 3)(*[PackReq(k.data_ptr(), v.data_ptr(), f.data_ptr(), k.stride(0),
+                                   k.stride(1), P, fl)
+                           for (k, v), f, P, fl in zip(dev, frames, lengths, flags)])
+    print(f"pack mixed batch lengths={lengths} flags={flags}", flush=True)
+    _lib.call("pdk_pack_kv_batch", reqs, 3, L, S, H, D,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for (k, v), f, P, fl in zip(srcs, frames, lengths, flags):
+        want = orc.pack_kv(k, v, P, S)
+        got = to_host(f)
+        if not fl:
+            np.testing.assert_array_equal(got, want.reshape(got.shape))
+            continue
+        kf, vf = got.reshape(L, 2, -1)[:, 0].reshape(L, H, D, S), got.reshape(L, 2, -1)[:, 1].reshape(L, H, S, D)
+        wk = want.reshape(L, 2, -1)[:, 0].reshape(L, H, D, S)
+        wv = want.reshape(L, 2, -1)[:, 1].reshape(L, H, S, D)
+        group_end = min((P + 63) // 64 * 64, S)
+        np.testing.assert_array_equal(kf[..., :group_end], wk[..., :group_end])
+        np.testing.assert_array_equal(vf[:, :, :P], wv[:, :, :P])
+        assert (kf[..., group_end:] == np.uint16(0x4040)).all()
+        assert (vf[:, :, P:] == np.uint16(0x4040)).all()
+
+
 def test_decode_attention_workspace_reuse(cuda):
     """Split counters reset themselves: back-to-back calls of different shapes on one
     workspace all match the oracle."""
