@@ -502,10 +502,10 @@ def test_linear_swiglu(cuda, B, K, M):
     np.testing.assert_allclose(_f32(to_host(y)), want, rtol=HALF_ULP, atol=tol)
 
 
-@pytest.mark.parametrize("B,K,N", [(16, 4096, 4096), (4, 4096, 4096), (3, 256, 1024),
-                                   (64, 128, 256), (1, 128, 16), (33, 512, 2048)])
+@pytest.mark.parametrize("B,K,N", [(16, 4096, 4096), (4, 4096, 4096), (16, 14336, 4096),
+                                   (3, 256, 1024), (64, 128, 256), (1, 128, 16), (33, 512, 2048)])
 def test_linear_ssq(cuda, B, K, N):
-    """The O projection with the norm's raw material: y bit-identical to
+    """The O and down projections with the norm's raw material: y bit-identical to
     pdk_linear with the residual, ssq[t][b] the sum of y[b, 16t:16t+16]^2
     (as bf16 values), tiled and untiled weights alike."""
     from rngd_pd_amd import kernels as K_
