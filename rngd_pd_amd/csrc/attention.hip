@@ -668,11 +668,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       last(std::true_type{}, sa0, id0);
     }
   };
-  // The fused RoPE path keeps a loop whose refills are conditional: its first
-  // pair's loads are issued before the rotation, so their waits are exact
-  // anyway, and with whole V (kNV = 8) the loop above needs more than the 256
-  // registers a lane has (it spilled; a serving step at contexts up to 1152,
-  // split in two then and so run with whole V, went from 3.07 to 5.1 ms).
+  // The fused RoPE path with whole V (kNV = 8) keeps a loop whose refills are
+  // conditional: there the loop above needs more than the 256 registers a
+  // lane has (it spilled; a serving step at contexts up to 1152, split in two
+  // then and so run with whole V, went from 3.07 to 5.1 ms). With V split in
+  // halves it runs the loop above (190 registers): 16-stream steps at
+  // contexts U[128, 1152] 3.028-3.031 -> 3.020-3.025 ms.
   auto pair_cond = [&](auto first_c, int sa, const int* cur, int* nxt) __attribute__((always_inline)) {
     const int sb = sa + stride, sc = sa + 2 * stride, sd = sa + 3 * stride;
     if (sc < s_end) ids(sc, nxt);
@@ -686,6 +687,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if constexpr (kRope <= 0) {
       first_loads();
       spans();
+    } else if constexpr (kNV == 4) {
+      spans();                                   // first pair issued before the rotation
     } else {
       int cur[4], nxt[4];
       for (int sa = pair_cond(std::true_type{}, sa0, id0, cur); sa < s_end;) {
