@@ -27,11 +27,11 @@ decode_batch tokens/s alongside.
             into the paged cache, for one 512-token request and for the batch.
   decode    GQA decode attention, 32 layers x B streams at context 512, per-layer
             launches, eager and replayed from a HIP graph; B=16 at context 2048
-            (context split in two + merge) from a graph.
+            (one context split, no merge launch) from a graph.
   step      the full Llama-3.1-8B decode step (random-init weights) at B=4 and
             B=16, context 512, eager and from a HIP graph, beside the
             reference's published 21.54 / 35.54 ms per step.
-  serve     2 prefill producers + 1 decode consumer on this GPU (config 5):
+  serve     2 prefill producers + 1 decode consumer on this GPU:
             64 requests, Poisson(20/s), prompts U[128,1024], 128 greedy tokens.
   cpu       the oracle's restatement of the reference CPU shm path (ser -> /dev/shm
             -> deser -> f32 place) on a bounded sample of the same requests.
@@ -163,7 +163,7 @@ def make_tables(torch, dev, lengths, seed=0, slack=16):
 
 
 def bench_handoff(args, torch, K, lib, dev, out):
-    """Config 2 (the headline): the 8-request batch staged through pinned host
+    """The headline: the 8-request batch staged through pinned host
     memory, pipelined across requests and layers with no host synchronisation
     between them (HostStagedHandoff, "dma" mode: narrow pack into device
     frames; the DMA engines copy each request's valid columns down into its
@@ -298,7 +298,7 @@ def bench_handoff(args, torch, K, lib, dev, out):
         raise RuntimeError("pack launch failed: " + lib.pdk_last_error().decode())
     torch.cuda.synchronize()
 
-    # -- config 2: staged through pinned host memory (value) ------------------
+    # -- the batch staged through pinned host memory (value) -----------------
     reqs = [(p[:, 0], p[:, 1], P, t) for p, P, t in zip(prefill, lengths, tables)]
     staged = {}
     for mode in ("dma", "kernel"):
@@ -892,7 +892,7 @@ def bench_step(args, torch, dev, out, batches=(4, 16), ctx=512):
 
 
 def bench_serve(args, out):
-    """Config 5: two prefill producer processes and one decode consumer on this
+    """Two prefill producer processes and one decode consumer on this
     GPU (same-GPU IPC handoff, continuous batching at width 16), 64 requests
     with Poisson(20/s) arrivals, prompts U[128,1024], 128 greedy tokens each,
     random-init Llama-3.1-8B weights. Runs rngd_pd_amd.serving.pd_one_gpu as a
