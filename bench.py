@@ -703,9 +703,10 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
 
 def bench_decode_long(args, torch, K, dev, out, B=16, ctx=2048):
     """Decode attention at a longer context, B=16 x 2048 tokens (134 MB of K+V
-    per layer, 4.3 GB for 32 layers): the launch splits the context in two
-    and a merge launch combines the halves. 32 layers replayed from a HIP
-    graph, timed with events around the replays."""
+    per layer, 4.3 GB for 32 layers): with 128 (stream, KV head) units the
+    launch keeps the context in one split (no merge launch; a longer context
+    splits it and a merge launch combines the parts). 32 layers replayed from
+    a HIP graph, timed with events around the replays."""
     nb_per = ctx // BS
     nb = B * nb_per
     gen = torch.Generator(device=dev).manual_seed(17)
@@ -751,7 +752,7 @@ def bench_decode_long(args, torch, K, dev, out, B=16, ctx=2048):
         f"B{B}": {"layer_us_graph": round(us, 2),
                   "tokens_per_s_graph": round(B / (us * L) * 1e6, 1),
                   "roofline": roofline(kv_bytes, us * 1e-6)}}
-    log(f"decode B={B} ctx={ctx}: {us:.2f} us per layer (graph, attention + merge), "
+    log(f"decode B={B} ctx={ctx}: {us:.2f} us per layer (graph, attention and any merge), "
         f"{kv_bytes / us / 1e3:.0f} GB/s")
     del g, cache_k, cache_v
     torch.cuda.empty_cache()
