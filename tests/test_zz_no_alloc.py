@@ -62,8 +62,8 @@ def test_noalloc_matches_workspace_entry_point(cuda):
     from rngd_pd_amd import _lib
     lib = _lib.lib()
     rng = np.random.default_rng(31)
-    cases = [(4, 32, 8, [2048, 1500, 700, 33]),      # first call: 16 splits of 128 tokens
-             (2, 32, 8, [600, 129])]                   # second, smaller: fewer splits
+    cases = [(4, 32, 8, [2048, 1500, 700, 33]),      # first call: 4 splits of 512 tokens
+             (2, 32, 8, [600, 129])]                   # second, smaller: 5 splits of 128
     for B, Hq, H, ctx in cases:
         print(f"noalloc vs workspace: B={B} Hq={Hq} Hkv={H} ctx={ctx}", flush=True)
         q, ck, cv, tables, ctx_a = _case(rng, B, Hq, H, ctx)
