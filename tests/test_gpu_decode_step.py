@@ -757,6 +757,17 @@ def test_small_model_steps(cuda):
     _run_steps(cuda, cfg, [1, 16, 17, 200, 513], steps=3, seed=11)
 
 
+def test_small_model_steps_two_row_tiles(cuda):
+    """B = 20: every GEMM runs two 16-row tiles (the residual loaded early for
+    both, the prefetch depth of the two-tile shapes)."""
+    from rngd_pd_amd.engines.llama_decode import LlamaConfig
+    cfg = LlamaConfig(hidden=512, n_heads=8, n_kv_heads=2, head_dim=128, inter=1024,
+                      vocab=1000, n_layers=2)
+    ctx = [1, 16, 17, 200, 513, 64, 5, 300, 129, 2, 40, 77, 256, 511, 100, 33, 18, 250, 3, 90]
+    print("small model: 2 layers, B=20", flush=True)
+    _run_steps(cuda, cfg, ctx, steps=2, seed=13)
+
+
 def test_llama8b_shape_two_layers(cuda):
     """Llama-3.1-8B dimensions (hidden 4096, 32/8 heads, MLP 14336, vocab
     128256) with 2 of the 32 layers, B=16 at mixed context lengths."""
