@@ -145,6 +145,22 @@ class Timer:
         return statistics.median(a.elapsed_time(b) for a, b in self.pairs[name]) / 1e3
 
 
+def gpu_delay(torch, us):
+    """A function that queues a bounded spin of about `us` microseconds on torch's
+    current stream (torch.cuda._sleep, calibrated once with HIP events). Queued
+    before a batch of short launches, it lets the host enqueue all of them before
+    the first one starts, so events around the batch time the kernels back to
+    back rather than the host's launch rate."""
+    probe = 1 << 20
+    t = Timer(torch, 1)
+    t.begin("spin")
+    torch.cuda._sleep(probe)
+    t.end("spin")
+    torch.cuda.synchronize()
+    cycles = max(1, int(probe * us * 1e-6 / t.mean_s("spin")))
+    return lambda: torch.cuda._sleep(cycles)
+
+
 def workload(seed=0, n=8):
     rng = np.random.default_rng(seed)
     return [int(p) for p in rng.integers(64, S + 1, n)]
@@ -253,13 +269,16 @@ def bench_handoff(args, torch, K, lib, dev, out):
     # The dma-mode step packs each request narrow (valid columns only) into a
     # device frame and scatters each request from its uploaded frame: 8
     # launches of each per step, timed here on device frames as one group per
-    # kind (events around the 8 launches, mean per launch).
+    # kind (events around the 8 launches, mean per launch), queued behind a
+    # spin so that the host's launch rate does not enter the times.
     from rngd_pd_amd._lib import PDK_PACK_NARROW
     narrow = [PackReq(p.data_ptr(), p[:, 1].data_ptr(), f.data_ptr(), p.stride(0), p.stride(2),
                       P, PDK_PACK_NARROW) for p, f, P in zip(prefill, frames, lengths)]
     timer_n = Timer(torch, 4 * args.steps)
+    delay = gpu_delay(torch, 1000)
     for i in range(args.warmup + args.steps):
         if i >= args.warmup:
+            delay()
             timer_n.begin("pack")
         for r in range(n):
             if lib.pdk_pack_kv_batch(ctypes.byref(narrow[r]), 1, L, S, H, D, st):
@@ -631,12 +650,20 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
-        timer = Timer(torch, 4 * args.steps)
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            step(timer)
+            step()
         torch.cuda.synchronize()
         eager = (time.perf_counter() - t0) / args.steps
+        # The launches' own time: each step's 32 launches queued behind a 2 ms
+        # spin, so the host has enqueued them all before the first starts, and
+        # event pairs around the step time the kernels back to back.
+        delay = gpu_delay(torch, 2000)
+        timer = Timer(torch, args.steps)
+        for _ in range(args.steps):
+            delay()
+            step(timer)
+        torch.cuda.synchronize()
         # The same 32-layer step replayed from a HIP graph (no host launch cost).
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream(device=dev)
@@ -653,9 +680,13 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
         torch.cuda.synchronize()
         if not torch.equal(outp.view(torch.int16), graph_ref.view(torch.int16)):
             raise RuntimeError("graph replay differs from eager attention")
+        # Event pairs around each replay: the graph's own per-launch time.
+        gtimer = Timer(torch, args.steps)
         t0 = time.perf_counter()
         for _ in range(args.steps):
+            gtimer.begin("graph")
             g.replay()
+            gtimer.end("graph")
         torch.cuda.synchronize()
         graphed = (time.perf_counter() - t0) / args.steps
         # The same launches with attention's loads and none of its arithmetic
@@ -681,12 +712,14 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
         probe_us = (time.perf_counter() - t0) / args.steps / L * 1e6
         kv_bytes = B * ctx * H * D * 2 * 2 + 2 * B * HQ * D * 2   # K+V read, q read, out write
         kern = timer.mean_s("step") / L                           # one layer's launch(es)
+        kern_graph = gtimer.mean_s("graph") / L
         res[f"B{B}"] = {
             "tokens_per_s_graph": round(B / graphed, 1),
             "tokens_per_s_eager": round(B / eager, 1),
             "step_us_graph": round(graphed * 1e6, 1),
             "step_us_eager": round(eager * 1e6, 1),
             "layer_call_us": round(kern * 1e6, 2),
+            "layer_call_us_graph": round(kern_graph * 1e6, 2),
             "layer_us_graph": round(graphed / L * 1e6, 2),
             "read_probe_layer_us_graph": round(probe_us, 2),
             "roofline": roofline(kv_bytes, kern,
@@ -694,7 +727,8 @@ def bench_decode(args, torch, K, lib, dev, out, batches=(4, 8, 16), ctx=512):
             "step_hbm_frac_graph": round(L * kv_bytes / graphed / 1e9 / HBM_PEAK_GBS, 4),
         }
         log(f"decode B={B}: graph {graphed*1e6:.1f} us/step ({B/graphed:.0f} tok/s), "
-            f"eager {eager*1e6:.1f} us, layer call {kern*1e6:.2f} us; "
+            f"eager {eager*1e6:.1f} us, layer call {kern*1e6:.2f} us "
+            f"(graph {kern_graph*1e6:.2f}); "
             f"loads-only probe {probe_us:.2f} us/layer")
         del ws, g, gp
     out["extra"]["decode_batch"] = res
