@@ -150,7 +150,10 @@ def gpu_delay(torch, us):
     current stream (torch.cuda._sleep, calibrated once with HIP events). Queued
     before a batch of short launches, it lets the host enqueue all of them before
     the first one starts, so events around the batch time the kernels back to
-    back rather than the host's launch rate."""
+    back rather than the host's launch rate. Without torch.cuda._sleep the
+    function queues nothing (and the times may then include host gaps)."""
+    if not hasattr(torch.cuda, "_sleep"):
+        return lambda: None
     probe = 1 << 20
     t = Timer(torch, 1)
     t.begin("spin")
